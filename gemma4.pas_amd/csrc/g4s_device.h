@@ -1,0 +1,314 @@
+/*
+ * g4s_device.h -- device-side building blocks shared by the sampler kernels
+ * (gfx950, wave64).
+ */
+#ifndef G4S_DEVICE_H
+#define G4S_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemma4_sampler.h"
+#include "g4s_crmath.h"
+
+namespace g4s {
+
+constexpr int kMaxTopK = 1024;     /* largest TopK of the top-k path */
+constexpr int kCandRow = 16384;    /* workspace candidate slots per row */
+constexpr int kMaxSplits = 256;    /* vocabulary chunks per row */
+constexpr int kMergeLds = 2048;    /* merge candidates kept in LDS */
+constexpr int kRankMax = 512;      /* rank-by-count select up to this many keys */
+
+/* Order-preserving uint32 image of a binary32 value.  -0 maps to +0 (the
+ * reference compares Singles, where -0 = +0).  0 is reserved for "not a
+ * candidate": values <= fl32(-1e30) never enter the reference's heap
+ * (Model.pas:2636,2643). */
+__device__ __forceinline__ uint32_t f2key(float f)
+{
+    uint32_t b = __float_as_uint(f);
+    b = (b == 0x80000000u) ? 0u : b;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k)
+{
+    uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+    return __uint_as_float(b);
+}
+__device__ __forceinline__ uint32_t cand_key(float f) { return (f > -1e30f) ? f2key(f) : 0u; }
+
+/* Element access: dtype 0 = binary32, 1 = bf16 (bits << 16, Types.pas:417-424). */
+template <int DT>
+struct Elem;
+template <>
+struct Elem<0> {
+    static constexpr int VW = 4; /* elements per 16-byte load */
+    static constexpr int SIZE = 4;
+};
+template <>
+struct Elem<1> {
+    static constexpr int VW = 8;
+    static constexpr int SIZE = 2;
+};
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const char* row, int64_t e)
+{
+    if constexpr (DT == 0) {
+        return reinterpret_cast<const float*>(row)[e];
+    } else {
+        uint32_t b = reinterpret_cast<const uint16_t*>(row)[e];
+        return __uint_as_float(b << 16);
+    }
+}
+
+/* Load VW consecutive elements starting at e0 (a multiple of VW); elements at
+ * or beyond `limit` are returned as -inf and flagged invalid by the caller. */
+template <int DT>
+__device__ __forceinline__ void load_vec(const char* row, int64_t e0, int64_t limit,
+                                         float (&v)[Elem<DT>::VW])
+{
+    constexpr int VW = Elem<DT>::VW;
+    if (e0 + VW <= limit) {
+        uint4 q = *reinterpret_cast<const uint4*>(row + e0 * Elem<DT>::SIZE);
+        if constexpr (DT == 0) {
+            v[0] = __uint_as_float(q.x);
+            v[1] = __uint_as_float(q.y);
+            v[2] = __uint_as_float(q.z);
+            v[3] = __uint_as_float(q.w);
+        } else {
+            uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[2 * i] = __uint_as_float(w[i] << 16);
+                v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VW; ++i)
+            v[i] = (e0 + i < limit) ? load_elem<DT>(row, e0 + i) : -__builtin_inff();
+    }
+}
+
+/* ------------------------------------------------------------ wave helpers */
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+template <typename T>
+__device__ __forceinline__ T wave_bcast(T v, int src)
+{
+    return __shfl(v, src, 64);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint32_t w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint32_t w = __shfl_xor(v, o, 64);
+        v = w < v ? w : v;
+    }
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+/* k-th largest (1 <= k <= 64) of one uint32 per lane, all 64 lanes active:
+ * MSB-first binary search with ballot counts; uniform result. */
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k)
+{
+    uint32_t prefix = 0;
+#pragma unroll
+    for (int bit = 31; bit >= 0; --bit) {
+        uint32_t cand = prefix | (1u << bit);
+        uint64_t m = __ballot(v >= cand);
+        if (__popcll(m) >= k) prefix = cand;
+    }
+    return prefix;
+}
+
+/* Block-wide exclusive prefix sum in thread order; `total` receives the sum.
+ * s_wave holds BLOCK/64 ints.  Contains two barriers. */
+template <int BLOCK>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int& total)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_wave[wid] = x;
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < BLOCK / 64; ++w) {
+        int t = s_wave[w];
+        off += (w < wid) ? t : 0;
+        tot += t;
+    }
+    total = tot;
+    __syncthreads();
+    return off + x - v;
+}
+
+template <int BLOCK>
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* s_wave)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wave_max_u32(v);
+    if (lane == 0) s_wave[wid] = v;
+    __syncthreads();
+    uint32_t r = 0;
+#pragma unroll
+    for (int w = 0; w < BLOCK / 64; ++w) r = s_wave[w] > r ? s_wave[w] : r;
+    __syncthreads();
+    return r;
+}
+template <int BLOCK>
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, uint32_t* s_wave)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wave_min_u32(v);
+    if (lane == 0) s_wave[wid] = v;
+    __syncthreads();
+    uint32_t r = 0xFFFFFFFFu;
+#pragma unroll
+    for (int w = 0; w < BLOCK / 64; ++w) r = s_wave[w] < r ? s_wave[w] : r;
+    __syncthreads();
+    return r;
+}
+template <int BLOCK>
+__device__ __forceinline__ int block_sum_i32(int v, int* s_wave)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wave_sum_i32(v);
+    if (lane == 0) s_wave[wid] = v;
+    __syncthreads();
+    int r = 0;
+#pragma unroll
+    for (int w = 0; w < BLOCK / 64; ++w) r += s_wave[w];
+    __syncthreads();
+    return r;
+}
+
+/* ------------------------------------------------------------- selection */
+
+/* One MSD radix step: from the 256-bin histogram of the current digit, find
+ * the digit d with count(> d) < k <= count(>= d).  Writes d, count(> d) and
+ * count(== d) to s_misc[0..2].  Called by the whole block; the first wave
+ * does the work. */
+__device__ __forceinline__ void radix_digit_step(int k, const uint32_t* s_hist, int* s_misc)
+{
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const int lane = tid;
+        int c[4];
+        int lsum = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            c[q] = (int)s_hist[255 - (lane * 4 + q)];
+            lsum += c[q];
+        }
+        int incl = lsum;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        int run = incl - lsum;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            int d = 255 - (lane * 4 + q);
+            if (run < k && k <= run + c[q]) {
+                s_misc[0] = d;
+                s_misc[1] = run;
+                s_misc[2] = c[q];
+            }
+            run += c[q];
+        }
+    }
+}
+
+/* k-th largest (1 <= k <= number of selected entries) of key(i) over the
+ * entries i in [0, n) with sel(i), by 8-bit MSD radix select with an LDS
+ * histogram.  Returns the value; *gt = how many selected entries are larger,
+ * *eq = how many equal it.  s_hist: 256 uint32; s_misc: >= 3 ints. */
+template <int BLOCK, typename KeyF, typename SelF>
+__device__ uint32_t block_radix_kth(int n, int k, KeyF key, SelF sel, uint32_t* s_hist, int* s_misc,
+                                   int* gt, int* eq)
+{
+    const int tid = threadIdx.x;
+    uint32_t prefix = 0, mask = 0;
+    int above = 0, equal = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = tid; b < 256; b += BLOCK) s_hist[b] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += BLOCK) {
+            if (!sel(i)) continue;
+            uint32_t v = key(i);
+            if ((v & mask) == prefix) atomicAdd(&s_hist[(v >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        radix_digit_step(k, s_hist, s_misc);
+        __syncthreads();
+        above += s_misc[1];
+        equal = s_misc[2];
+        k -= s_misc[1];
+        prefix |= (uint32_t)s_misc[0] << shift;
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    *gt = above;
+    *eq = equal;
+    return prefix;
+}
+
+/* The same select over keys held in registers (ITEMS per thread, 0 = not
+ * selected).  Register arrays are only indexed with constants. */
+template <int BLOCK, int ITEMS>
+__device__ uint32_t regs_radix_kth(const uint32_t (&keys)[ITEMS], int k, uint32_t* s_hist,
+                                   int* s_misc, int* gt, int* eq)
+{
+    const int tid = threadIdx.x;
+    uint32_t prefix = 0, mask = 0;
+    int above = 0, equal = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = tid; b < 256; b += BLOCK) s_hist[b] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < ITEMS; ++q) {
+            uint32_t v = keys[q];
+            if (v != 0u && (v & mask) == prefix) atomicAdd(&s_hist[(v >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        radix_digit_step(k, s_hist, s_misc);
+        __syncthreads();
+        above += s_misc[1];
+        equal = s_misc[2];
+        k -= s_misc[1];
+        prefix |= (uint32_t)s_misc[0] << shift;
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    *gt = above;
+    *eq = equal;
+    return prefix;
+}
+
+}  // namespace g4s
+
+#endif

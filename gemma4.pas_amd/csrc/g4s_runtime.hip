@@ -1,0 +1,399 @@
+/*
+ * g4s_runtime.hip -- host runtime and C ABI of libgemma4_sampler.so.
+ *
+ * Owns the per-handle HBM workspace (allocated once in g4s_create, reused by
+ * every call), validates arguments the way the engine would have to, and
+ * dispatches each row to the top-k path or the full-vocabulary path exactly
+ * as DoSample's branch does (src/Gemma4.Model.pas:2756).  Errors follow the
+ * engine's convention of a failing result plus a message (StdApp.Base.pas
+ * TErrors), here a negative g4s_status and g4s_last_error().
+ */
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "g4s_full.h"
+#include "g4s_lmhead.h"
+#include "g4s_topk.h"
+
+#define G4S_API extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+thread_local std::string g_create_error;
+
+}  // namespace
+
+struct g4s_sampler {
+    int device = 0;
+    int32_t vocab = 0;
+    int32_t max_batch = 0;
+    float softcap = 0.0f;
+    hipStream_t stream = nullptr;
+    std::string err;
+
+    /* top-k path workspace */
+    uint32_t* cand_key = nullptr;
+    uint32_t* cand_idx = nullptr;
+    uint32_t* merge_key = nullptr;
+    uint32_t* merge_idx = nullptr;
+    g4s::ChunkRec* recs = nullptr;
+    uint32_t* tickets = nullptr;
+    /* full path workspace */
+    g4s::FullWorkspace full{};
+    /* per-call staging */
+    int32_t* d_ids = nullptr;
+    g4s_params* d_params = nullptr;
+    double* d_u = nullptr;
+    g4s_params* h_params = nullptr; /* pinned */
+    double* h_u = nullptr;          /* pinned */
+    int32_t* h_ids = nullptr;       /* pinned */
+    uint32_t* h_flags = nullptr;    /* pinned */
+    uint32_t* d_flags = nullptr;
+};
+
+namespace {
+
+int fail(g4s_sampler* s, int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (s)
+        s->err = buf;
+    else
+        g_create_error = buf;
+    return code;
+}
+
+int hip_fail(g4s_sampler* s, hipError_t e, const char* what)
+{
+    return fail(s, G4S_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+void release(g4s_sampler* s)
+{
+    auto f = [](void* p) {
+        if (p) (void)hipFree(p);
+    };
+    auto fh = [](void* p) {
+        if (p) (void)hipHostFree(p);
+    };
+    f(s->cand_key);
+    f(s->cand_idx);
+    f(s->merge_key);
+    f(s->merge_idx);
+    f(s->recs);
+    f(s->tickets);
+    g4s::full_free(s->full);
+    f(s->d_ids);
+    f(s->d_params);
+    f(s->d_u);
+    f(s->d_flags);
+    fh(s->h_params);
+    fh(s->h_u);
+    fh(s->h_ids);
+    fh(s->h_flags);
+}
+
+bool is_topk_row(const g4s_params& p, int32_t vocab) { return p.top_k >= 1 && p.top_k < vocab; }
+
+int check_logits(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
+                 int32_t batch)
+{
+    if (!d_logits) return fail(s, G4S_ERR_INVALID_ARGUMENT, "d_logits is NULL");
+    if (dtype != G4S_DTYPE_F32 && dtype != G4S_DTYPE_BF16)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "dtype %d is neither F32 nor BF16", dtype);
+    if (batch < 1 || batch > s->max_batch)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "batch %d outside [1, %d]", batch, s->max_batch);
+    if (batch > 1 && row_stride < s->vocab)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %d",
+                    (long long)row_stride, s->vocab);
+    const int64_t esize = dtype == G4S_DTYPE_F32 ? 4 : 2;
+    if (((uintptr_t)d_logits & 15u) != 0)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "d_logits must be 16-byte aligned");
+    if (batch > 1 && ((row_stride * esize) & 15) != 0)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT,
+                    "row_stride * sizeof(dtype) must be a multiple of 16 bytes");
+    return G4S_OK;
+}
+
+/* Enqueue both paths for `batch` rows whose parameters are at d_params/d_u
+ * (or inline p0/u0 when d_params is NULL). */
+int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride, int32_t batch,
+            const g4s_params* d_params, const double* d_u, const g4s_params* p0, double u0,
+            int32_t kbound, bool full_rows, int32_t* d_ids, const g4s_outputs* outputs)
+{
+    g4s_outputs out{};
+    if (outputs) out = *outputs;
+    if ((out.indices || out.probs) && out.capacity < 1)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "outputs.capacity must be >= 1");
+    if (kbound > 0) {
+        g4s::TopkConfig cfg = g4s::topk_plan(s->vocab, kbound);
+        if (!cfg.ok) return fail(s, G4S_ERR_UNSUPPORTED, "no top-k launch plan for K=%d", kbound);
+        g4s::TopkArgs a{};
+        a.logits = d_logits;
+        a.row_stride = row_stride;
+        a.vocab = s->vocab;
+        a.batch = batch;
+        a.params = d_params;
+        a.u = d_u;
+        if (p0) a.p0 = *p0;
+        a.u0 = u0;
+        a.splits = cfg.splits;
+        a.cap_c = cfg.cap_c;
+        a.kbound = kbound;
+        a.softcap = s->softcap;
+        a.cand_key = s->cand_key;
+        a.cand_idx = s->cand_idx;
+        a.merge_key = s->merge_key;
+        a.merge_idx = s->merge_idx;
+        a.recs = s->recs;
+        a.tickets = s->tickets;
+        a.ids = d_ids;
+        a.out = out;
+        hipError_t e = g4s::topk_launch(cfg, a, dtype, s->stream);
+        if (e != hipSuccess) return hip_fail(s, e, "top-k kernel launch");
+    }
+    if (full_rows) {
+        g4s::FullArgs f{};
+        f.logits = d_logits;
+        f.row_stride = row_stride;
+        f.vocab = s->vocab;
+        f.batch = batch;
+        f.params = d_params;
+        f.u = d_u;
+        if (p0) f.p0 = *p0;
+        f.u0 = u0;
+        f.softcap = s->softcap;
+        f.ws = s->full;
+        f.ids = d_ids;
+        f.out = out;
+        hipError_t e = g4s::full_launch(f, dtype, s->stream);
+        if (e != hipSuccess) return hip_fail(s, e, "full-vocabulary kernel launch");
+    }
+    return G4S_OK;
+}
+
+}  // namespace
+
+G4S_API const char* g4s_version(void) { return "gemma4_sampler 0.1.0 (gfx950)"; }
+
+G4S_API void g4s_params_set_defaults(g4s_params* p)
+{
+    /* TSamplingParams.SetDefaults, Model.pas:346-352 */
+    if (!p) return;
+    p->temperature = 1.0f;
+    p->top_k = 64;
+    p->top_p = 0.95f;
+    p->repetition_penalty = 1.0f;
+}
+
+G4S_API int32_t g4s_max_top_k(void) { return g4s::kMaxTopK; }
+
+G4S_API const char* g4s_last_error(const g4s_sampler* s)
+{
+    return s ? s->err.c_str() : g_create_error.c_str();
+}
+
+G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, float softcap,
+                       void* hip_stream)
+{
+    g_create_error.clear();
+    if (!out) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "out is NULL");
+    *out = nullptr;
+    if (vocab < 2 || vocab > (1 << 30))
+        return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "vocab %d outside [2, 2^30]", vocab);
+    if (max_batch < 1 || max_batch > 65535)
+        return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "max_batch %d outside [1, 65535]",
+                    max_batch);
+    if (!(softcap == softcap))
+        return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "softcap is NaN");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1)
+        return fail(nullptr, G4S_ERR_NO_DEVICE, "no HIP device visible");
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return fail(nullptr, G4S_ERR_NO_DEVICE, "hipGetDevice failed");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
+        return fail(nullptr, G4S_ERR_NO_DEVICE, "hipGetDeviceProperties failed");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, G4S_ERR_NO_DEVICE, "device %d is %s; this library targets gfx950",
+                    dev, prop.gcnArchName);
+
+    g4s_sampler* s = new g4s_sampler();
+    s->device = dev;
+    s->vocab = vocab;
+    s->max_batch = max_batch;
+    s->softcap = softcap;
+    s->stream = (hipStream_t)hip_stream;
+
+    const size_t mb = (size_t)max_batch;
+    bool ok = true;
+    auto dm = [&](void** p, size_t bytes) {
+        if (ok && hipMalloc(p, bytes) != hipSuccess) ok = false;
+    };
+    auto hm = [&](void** p, size_t bytes) {
+        if (ok && hipHostMalloc(p, bytes, hipHostMallocDefault) != hipSuccess) ok = false;
+    };
+    dm((void**)&s->cand_key, mb * g4s::kCandRow * sizeof(uint32_t));
+    dm((void**)&s->cand_idx, mb * g4s::kCandRow * sizeof(uint32_t));
+    dm((void**)&s->merge_key, mb * g4s::kCandRow * sizeof(uint32_t));
+    dm((void**)&s->merge_idx, mb * g4s::kCandRow * sizeof(uint32_t));
+    dm((void**)&s->recs, mb * g4s::kMaxSplits * sizeof(g4s::ChunkRec));
+    dm((void**)&s->tickets, mb * sizeof(uint32_t));
+    dm((void**)&s->d_ids, mb * sizeof(int32_t));
+    dm((void**)&s->d_params, mb * sizeof(g4s_params));
+    dm((void**)&s->d_u, mb * sizeof(double));
+    dm((void**)&s->d_flags, mb * sizeof(uint32_t));
+    hm((void**)&s->h_params, mb * sizeof(g4s_params));
+    hm((void**)&s->h_u, mb * sizeof(double));
+    hm((void**)&s->h_ids, mb * sizeof(int32_t));
+    hm((void**)&s->h_flags, mb * sizeof(uint32_t));
+    if (ok && g4s::full_alloc(s->full, vocab, max_batch) != hipSuccess) ok = false;
+    if (!ok) {
+        release(s);
+        delete s;
+        return fail(nullptr, G4S_ERR_OUT_OF_MEMORY,
+                    "workspace allocation failed (vocab %d, max_batch %d)", vocab, max_batch);
+    }
+    hipError_t e = hipMemsetAsync(s->tickets, 0, mb * sizeof(uint32_t), s->stream);
+    if (e == hipSuccess) e = g4s::full_init(s->full, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) {
+        release(s);
+        delete s;
+        return fail(nullptr, G4S_ERR_HIP, "workspace initialisation: %s", hipGetErrorString(e));
+    }
+    *out = s;
+    return G4S_OK;
+}
+
+G4S_API int g4s_destroy(g4s_sampler* s)
+{
+    if (!s) return G4S_OK;
+    (void)hipStreamSynchronize(s->stream);
+    release(s);
+    delete s;
+    return G4S_OK;
+}
+
+G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
+                          int32_t batch, const g4s_params* params, const double* u, int32_t* ids,
+                          const g4s_outputs* outputs)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    int rc = check_logits(s, d_logits, dtype, row_stride, batch);
+    if (rc) return rc;
+    if (!params || !u || !ids)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "params, u and ids must be non-NULL");
+    int32_t kbound = 0;
+    bool full_rows = false;
+    for (int32_t r = 0; r < batch; ++r) {
+        if (is_topk_row(params[r], s->vocab)) {
+            if (params[r].top_k > g4s::kMaxTopK)
+                return fail(s, G4S_ERR_UNSUPPORTED,
+                            "row %d: TopK %d exceeds the top-k path limit %d (TopK <= 0 or >= V "
+                            "selects the full-vocabulary path)",
+                            r, params[r].top_k, g4s::kMaxTopK);
+            kbound = params[r].top_k > kbound ? params[r].top_k : kbound;
+        } else {
+            full_rows = true;
+        }
+    }
+    /* u must be a probability-like number; the reference's Random is in [0,1) */
+    for (int32_t r = 0; r < batch; ++r)
+        if (!(u[r] >= 0.0 && u[r] < 1.0))
+            return fail(s, G4S_ERR_INVALID_ARGUMENT, "row %d: u = %g outside [0, 1)", r, u[r]);
+
+    g4s_outputs out{};
+    if (outputs) out = *outputs;
+    uint32_t* user_flags = out.flags;
+    out.flags = s->d_flags; /* always collect flags to report empty rows */
+
+    if (batch == 1) {
+        rc = enqueue(s, d_logits, dtype, row_stride, 1, nullptr, nullptr, &params[0], u[0], kbound,
+                     full_rows, s->d_ids, &out);
+    } else {
+        std::memcpy(s->h_params, params, sizeof(g4s_params) * batch);
+        std::memcpy(s->h_u, u, sizeof(double) * batch);
+        hipError_t e = hipMemcpyAsync(s->d_params, s->h_params, sizeof(g4s_params) * batch,
+                                      hipMemcpyHostToDevice, s->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(s->d_u, s->h_u, sizeof(double) * batch, hipMemcpyHostToDevice,
+                               s->stream);
+        if (e != hipSuccess) return hip_fail(s, e, "parameter upload");
+        rc = enqueue(s, d_logits, dtype, row_stride, batch, s->d_params, s->d_u, nullptr, 0.0,
+                     kbound, full_rows, s->d_ids, &out);
+    }
+    if (rc) return rc;
+    hipError_t e = hipMemcpyAsync(s->h_ids, s->d_ids, sizeof(int32_t) * batch,
+                                  hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(s->h_flags, s->d_flags, sizeof(uint32_t) * batch, hipMemcpyDeviceToHost,
+                           s->stream);
+    if (e == hipSuccess && user_flags)
+        e = hipMemcpyAsync(user_flags, s->d_flags, sizeof(uint32_t) * batch,
+                           hipMemcpyDeviceToDevice, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(s, e, "sampling");
+    std::memcpy(ids, s->h_ids, sizeof(int32_t) * batch);
+    for (int32_t r = 0; r < batch; ++r)
+        if (s->h_flags[r] & G4S_FLAG_EMPTY)
+            return fail(s, G4S_ERR_EMPTY_ROW, "row %d: no logit above -1e30 on the top-k path", r);
+    return G4S_OK;
+}
+
+G4S_API int g4s_sample(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
+                       int32_t batch, const g4s_params* params, const double* u, int32_t* ids)
+{
+    return g4s_sample_ex(s, d_logits, dtype, row_stride, batch, params, u, ids, nullptr);
+}
+
+G4S_API int g4s_sample_async(g4s_sampler* s, const void* d_logits, int32_t dtype,
+                             int64_t row_stride, int32_t batch, const g4s_params* d_params,
+                             const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,
+                             const g4s_outputs* outputs)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    int rc = check_logits(s, d_logits, dtype, row_stride, batch);
+    if (rc) return rc;
+    if (!d_params || !d_u || !d_ids)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "d_params, d_u and d_ids must be non-NULL");
+    if (k_bound < 0 || k_bound > g4s::kMaxTopK)
+        return fail(s, G4S_ERR_UNSUPPORTED, "k_bound %d outside [0, %d]", k_bound, g4s::kMaxTopK);
+    if (k_bound == 0 && !full_rows)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "k_bound == 0 and full_rows == 0: nothing to do");
+    return enqueue(s, d_logits, dtype, row_stride, batch, d_params, d_u, nullptr, 0.0, k_bound,
+                   full_rows != 0, d_ids, outputs);
+}
+
+G4S_API int g4s_lmhead_q4_0(g4s_sampler* s, const void* d_weights, int32_t rows, int32_t cols,
+                            const float* d_hidden, int32_t batch, float* d_logits,
+                            int64_t logits_stride)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    if (!d_weights || !d_hidden || !d_logits)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (rows < 1 || cols < 32 || (cols % 32) != 0)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "rows %d / cols %d (cols must be a multiple of 32)",
+                    rows, cols);
+    if (batch < 1 || logits_stride < rows)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "batch %d / logits_stride %lld", batch,
+                    (long long)logits_stride);
+    hipError_t e = g4s::lmhead_q4_0_launch((const uint8_t*)d_weights, rows, cols, d_hidden, batch,
+                                           d_logits, logits_stride, s->stream);
+    if (e == hipErrorNotSupported)
+        return fail(s, G4S_ERR_UNSUPPORTED, "LM-head shape not supported (batch %d)", batch);
+    if (e != hipSuccess) return hip_fail(s, e, "LM-head kernel launch");
+    return G4S_OK;
+}

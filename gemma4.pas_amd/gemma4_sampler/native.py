@@ -1,0 +1,240 @@
+"""ctypes binding of libgemma4_sampler.so (include/gemma4_sampler.h).
+
+The names mirror the reference's sampling surface: TSamplingParams
+(src/Gemma4.Model.pas:70-76, SetDefaults :346-352), the TInference setters
+SetTemperature / SetTopK / SetTopP (src/Gemma4.Inference.pas:2186-2199) and
+DoSample (src/Gemma4.Model.pas:2739-2827), so tests read like the engine's
+own call sites.  There is no fallback: if the library is missing, loading
+raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from . import hip
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libgemma4_sampler.so")
+
+G4S_OK = 0
+G4S_ERR_INVALID_ARGUMENT = -1
+G4S_ERR_UNSUPPORTED = -2
+G4S_ERR_NO_DEVICE = -3
+G4S_ERR_OUT_OF_MEMORY = -4
+G4S_ERR_HIP = -5
+G4S_ERR_EMPTY_ROW = -6
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+FLAG_TOPK_PATH = 0x1
+FLAG_FULL_PATH = 0x2
+FLAG_DREW = 0x4
+FLAG_REACHED = 0x8
+FLAG_TIE_LOWEST = 0x10
+FLAG_HEAP_REPLAY = 0x20
+FLAG_CHUNK_EXACT = 0x40
+FLAG_WIDE_MERGE = 0x80
+FLAG_EMPTY = 0x40000000
+FLAG_ERROR = 0x80000000
+
+EXPORTS = ("g4s_version", "g4s_params_set_defaults", "g4s_max_top_k", "g4s_create",
+           "g4s_destroy", "g4s_last_error", "g4s_sample", "g4s_sample_ex", "g4s_sample_async",
+           "g4s_lmhead_q4_0")
+
+
+class TSamplingParams(ctypes.Structure):
+    """g4s_params == TSamplingParams (Model.pas:70-76)."""
+    _fields_ = [("Temperature", ctypes.c_float), ("TopK", ctypes.c_int32),
+                ("TopP", ctypes.c_float), ("RepetitionPenalty", ctypes.c_float)]
+
+    def SetDefaults(self):
+        load().g4s_params_set_defaults(ctypes.byref(self))
+        return self
+
+    @classmethod
+    def make(cls, temperature, top_k, top_p):
+        return cls(float(temperature), int(top_k), float(top_p), 1.0)
+
+
+class Outputs(ctypes.Structure):
+    _fields_ = [("count", ctypes.c_void_p), ("indices", ctypes.c_void_p),
+                ("probs", ctypes.c_void_p), ("capacity", ctypes.c_int32),
+                ("argmax", ctypes.c_void_p), ("lsum", ctypes.c_void_p),
+                ("flags", ctypes.c_void_p)]
+
+
+class SamplerError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"g4s error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load():
+    """Load libgemma4_sampler.so from the package's lib/ (built in-tree)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = ctypes.CDLL(LIB_PATH)
+        L.g4s_version.restype = ctypes.c_char_p
+        L.g4s_last_error.restype = ctypes.c_char_p
+        L.g4s_last_error.argtypes = [ctypes.c_void_p]
+        L.g4s_max_top_k.restype = ctypes.c_int32
+        L.g4s_create.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32, ctypes.c_int32,
+                                 ctypes.c_float, ctypes.c_void_p]
+        L.g4s_destroy.argtypes = [ctypes.c_void_p]
+        L.g4s_sample.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                                 ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.g4s_sample_ex.argtypes = L.g4s_sample.argtypes + [ctypes.c_void_p]
+        L.g4s_sample_async.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+                                       ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                       ctypes.c_void_p, ctypes.c_void_p]
+        L.g4s_lmhead_q4_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+                                      ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                      ctypes.c_void_p, ctypes.c_int64]
+        _lib = L
+    return _lib
+
+
+def version():
+    return load().g4s_version().decode()
+
+
+def max_top_k():
+    return load().g4s_max_top_k()
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    if isinstance(x, hip.Buffer):
+        return x.ptr
+    if isinstance(x, int):
+        return ctypes.c_void_p(x)
+    return x
+
+
+def params_array(params):
+    arr = (TSamplingParams * len(params))()
+    for i, p in enumerate(params):
+        arr[i] = p
+    return arr
+
+
+class Sampler:
+    """One g4s_sampler handle: the device-side replacement of TModel.DoSample."""
+
+    def __init__(self, vocab, max_batch=1, softcap=30.0, stream=None):
+        L = load()
+        h = ctypes.c_void_p()
+        rc = L.g4s_create(ctypes.byref(h), int(vocab), int(max_batch), float(softcap),
+                          stream.handle if stream is not None else None)
+        if rc != G4S_OK:
+            raise SamplerError(rc, L.g4s_last_error(None).decode())
+        self.h = h
+        self.vocab = int(vocab)
+        self.max_batch = int(max_batch)
+        self.softcap = float(softcap)
+        self.params = TSamplingParams().SetDefaults()  # TInference.FSamplingParams
+
+    # TInference sampling surface (Inference.pas:2186-2199)
+    def SetTemperature(self, value):
+        self.params.Temperature = float(value)
+
+    def SetTopK(self, value):
+        self.params.TopK = int(value)
+
+    def SetTopP(self, value):
+        self.params.TopP = float(value)
+
+    @property
+    def SamplingParams(self):
+        return self.params
+
+    def last_error(self):
+        return load().g4s_last_error(self.h).decode()
+
+    def _check(self, rc):
+        if rc != G4S_OK:
+            raise SamplerError(rc, self.last_error())
+
+    def sample(self, d_logits, batch, params, u, dtype=DTYPE_F32, row_stride=None, outputs=None,
+               check=True):
+        """Synchronous g4s_sample(_ex); returns (status, ids ndarray)."""
+        L = load()
+        if isinstance(params, TSamplingParams):
+            params = [params] * batch
+        parr = params_array(params)
+        uarr = np.ascontiguousarray(np.asarray(u, dtype=np.float64).reshape(-1))
+        assert uarr.size == batch
+        ids = np.full(batch, -7, dtype=np.int32)
+        stride = self.vocab if row_stride is None else int(row_stride)
+        rc = L.g4s_sample_ex(self.h, _ptr(d_logits), int(dtype), stride, int(batch), parr,
+                             uarr.ctypes.data_as(ctypes.c_void_p),
+                             ids.ctypes.data_as(ctypes.c_void_p),
+                             ctypes.byref(outputs) if outputs is not None else None)
+        if check:
+            self._check(rc)
+        return rc, ids
+
+    def DoSample(self, d_logits, u, params=None, dtype=DTYPE_F32):
+        """Model.pas:2739: one row, this handle's SamplingParams unless given."""
+        _, ids = self.sample(d_logits, 1, [params or self.params], [u], dtype=dtype)
+        return int(ids[0])
+
+    def sample_async(self, d_logits, batch, d_params, d_u, k_bound, full_rows, d_ids,
+                     dtype=DTYPE_F32, row_stride=None, outputs=None):
+        L = load()
+        stride = self.vocab if row_stride is None else int(row_stride)
+        rc = L.g4s_sample_async(self.h, _ptr(d_logits), int(dtype), stride, int(batch),
+                                _ptr(d_params), _ptr(d_u), int(k_bound), int(full_rows),
+                                _ptr(d_ids), ctypes.byref(outputs) if outputs is not None else None)
+        self._check(rc)
+
+    def lmhead_q4_0(self, d_weights, rows, cols, d_hidden, batch, d_logits, logits_stride=None):
+        L = load()
+        rc = L.g4s_lmhead_q4_0(self.h, _ptr(d_weights), int(rows), int(cols), _ptr(d_hidden),
+                               int(batch), _ptr(d_logits),
+                               int(rows if logits_stride is None else logits_stride))
+        self._check(rc)
+
+    def close(self):
+        if self.h is not None and self.h.value:
+            load().g4s_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DeviceOutputs:
+    """Device buffers for g4s_outputs plus host readback."""
+
+    def __init__(self, batch, capacity):
+        self.batch, self.capacity = batch, capacity
+        self.count = hip.Buffer(4 * batch)
+        self.indices = hip.Buffer(4 * batch * capacity)
+        self.probs = hip.Buffer(4 * batch * capacity)
+        self.argmax = hip.Buffer(4 * batch)
+        self.lsum = hip.Buffer(4 * batch)
+        self.flags = hip.Buffer(4 * batch)
+        self.struct = Outputs(self.count.addr, self.indices.addr, self.probs.addr, capacity,
+                              self.argmax.addr, self.lsum.addr, self.flags.addr)
+
+    def read(self):
+        return dict(count=self.count.download(np.int32),
+                    indices=self.indices.download(np.int32).reshape(self.batch, self.capacity),
+                    probs=self.probs.download(np.float32).reshape(self.batch, self.capacity),
+                    argmax=self.argmax.download(np.int32),
+                    lsum=self.lsum.download(np.float32),
+                    flags=self.flags.download(np.uint32))

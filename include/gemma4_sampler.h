@@ -1,0 +1,167 @@
+/*
+ * gemma4_sampler.h -- C ABI of libgemma4_sampler.so, the MI355X (gfx950)
+ * token sampler for the Gemma4.pas engine.
+ *
+ * The library replaces the engine's CPU sampler, TModel.DoSample and its
+ * helpers (src/Gemma4.Model.pas:2615-2827, src/Gemma4.Tensors.pas:638-673,
+ * src/Gemma4.Layers.pas:300-316), on logits that stay in device memory.  It
+ * keeps the reference's sampling surface (TSamplingParams:
+ * Temperature / TopK / TopP) and its order of operations:
+ *   top-k path (0 < TopK < V): top-K on raw logits (min-heap tie semantics)
+ *     -> survivors ascending by vocab index -> softcap cap*tanh(x/cap)
+ *     -> * fl32(1/T) when T > 0 and T <> 1 -> softmax (sequential binary32
+ *     sum, division) -> greedy argmax -> if T > 0: first survivor, in index
+ *     order, whose running binary32 sum is >= fl32(u*TopP), else the argmax;
+ *   full path (TopK <= 0 or TopK >= V): softcap tanh(x*fl32(1/cap))*cap on
+ *     every logit -> temperature -> softmax over V (sequential binary32 sum,
+ *     reciprocal multiply) -> argmax -> the same index-order draw over V.
+ * Transcendental steps are correctly rounded to binary32.  System.Random is
+ * replaced by a caller-supplied uniform u in [0,1) per row, so a caller that
+ * passes the values its RNG would have produced reproduces the reference
+ * exactly.
+ *
+ * Conventions: functions return 0 (G4S_OK) or a negative g4s_status; the
+ * message of the last failure is kept per handle (g4s_last_error).  One
+ * handle = one HIP stream; a handle is not thread-safe; several handles may
+ * coexist.  Device pointers are HIP device memory of the handle's device.
+ */
+#ifndef GEMMA4_SAMPLER_H
+#define GEMMA4_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define G4S_ABI_VERSION 1
+
+typedef struct g4s_sampler g4s_sampler;
+
+typedef enum g4s_dtype {
+    G4S_DTYPE_F32 = 0,  /* binary32 logits (the engine's FLogits) */
+    G4S_DTYPE_BF16 = 1  /* bf16 logits, widened exactly as TBFloat16.ToSingle (Types.pas:417-424) */
+} g4s_dtype;
+
+typedef enum g4s_status {
+    G4S_OK = 0,
+    G4S_ERR_INVALID_ARGUMENT = -1, /* null pointer, bad size, misaligned logits, ... */
+    G4S_ERR_UNSUPPORTED = -2,      /* e.g. 1024 < TopK < V (see g4s_max_top_k) */
+    G4S_ERR_NO_DEVICE = -3,        /* no HIP device / wrong architecture */
+    G4S_ERR_OUT_OF_MEMORY = -4,    /* workspace allocation failed at create */
+    G4S_ERR_HIP = -5,              /* a HIP runtime call failed */
+    G4S_ERR_EMPTY_ROW = -6         /* a top-k row had no logit above -1e30 (id set to -1) */
+} g4s_status;
+
+/* TSamplingParams, src/Gemma4.Model.pas:70-76 (same fields, same meaning).
+ * repetition_penalty is carried for layout parity and, as in the reference,
+ * never read. */
+typedef struct g4s_params {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float repetition_penalty;
+} g4s_params;
+
+/* Per-row flags (g4s_outputs.flags) */
+#define G4S_FLAG_TOPK_PATH 0x1u     /* row took the top-k path */
+#define G4S_FLAG_FULL_PATH 0x2u     /* row took the full-vocabulary path */
+#define G4S_FLAG_DREW 0x4u          /* T > 0: a draw against u*TopP happened */
+#define G4S_FLAG_REACHED 0x8u       /* the running sum reached u*TopP */
+#define G4S_FLAG_TIE_LOWEST 0x10u   /* K-th value tied; resolved by the lowest-index rule */
+#define G4S_FLAG_HEAP_REPLAY 0x20u  /* K-th value tied; resolved by replaying the min-heap */
+#define G4S_FLAG_CHUNK_EXACT 0x40u  /* a vocabulary chunk needed the exact per-chunk select */
+#define G4S_FLAG_WIDE_MERGE 0x80u   /* the merge candidate set exceeded on-chip memory */
+#define G4S_FLAG_EMPTY 0x40000000u  /* no logit above -1e30 on the top-k path */
+#define G4S_FLAG_ERROR 0x80000000u  /* row rejected (e.g. TopK above the launch bound) */
+
+/* Optional per-row outputs; every pointer is device memory and may be NULL.
+ *   count   [batch]           candidates: K' survivors (top-k path) or V (full path)
+ *   indices [batch*capacity]  top-k path: survivor vocab indices, ascending
+ *   probs   [batch*capacity]  top-k path: normalised survivor probabilities
+ *                             (LVals after the division, Model.pas:2800-2801);
+ *                             full path: p_i over the vocabulary when capacity >= V
+ *   argmax  [batch]           token id of the greedy choice (first maximum of p)
+ *   lsum    [batch]           softmax denominator (LSum)
+ *   flags   [batch]           G4S_FLAG_* */
+typedef struct g4s_outputs {
+    int32_t* count;
+    int32_t* indices;
+    float* probs;
+    int32_t capacity;
+    int32_t* argmax;
+    float* lsum;
+    uint32_t* flags;
+} g4s_outputs;
+
+/* Library version string, e.g. "gemma4_sampler 0.1.0 (gfx950)". */
+const char* g4s_version(void);
+
+/* TSamplingParams.SetDefaults, src/Gemma4.Model.pas:346-352:
+ * T = 1.0, TopK = 64, TopP = 0.95, RepetitionPenalty = 1.0. */
+void g4s_params_set_defaults(g4s_params* params);
+
+/* Largest TopK the top-k path accepts (TopK <= 0 or >= V selects the full path). */
+int32_t g4s_max_top_k(void);
+
+/* Create a sampler for `vocab` logits per row and up to `max_batch` rows per
+ * call.  `softcap` is the model's final_logit_softcapping
+ * (Gemma4.Config.pas:74,209; 30.0 for Gemma 4; <= 0 disables it).
+ * `hip_stream` (hipStream_t, may be NULL = default stream) orders all work.
+ * Allocates the whole workspace; no later call allocates device memory.
+ * Replaces: the sampler state of TModel (FLogits/FConfig, Model.pas:131,161). */
+int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, float softcap,
+               void* hip_stream);
+
+/* Release the handle and its workspace.  NULL is accepted. */
+int g4s_destroy(g4s_sampler* sampler);
+
+/* Message of the most recent failure on this handle ("" if none).  With a
+ * NULL handle, the message of the most recent failed g4s_create. */
+const char* g4s_last_error(const g4s_sampler* sampler);
+
+/* Sample `batch` rows synchronously.  Replaces TModel.DoSample
+ * (src/Gemma4.Model.pas:2739-2827) and the per-token logits readback
+ * (Model.pas:1382-1385): the logits stay on the device, only ids return.
+ *   d_logits   device, `batch` rows of `vocab` logits, row i at
+ *              d_logits + i*row_stride elements; 16-byte aligned base and
+ *              row_stride*sizeof(dtype) a multiple of 16
+ *   params     host, `batch` entries (one TSamplingParams per row)
+ *   u          host, `batch` uniforms in [0,1) standing in for System.Random
+ *   ids        host, `batch` token ids written on return */
+int g4s_sample(g4s_sampler* sampler, const void* d_logits, int32_t dtype, int64_t row_stride,
+               int32_t batch, const g4s_params* params, const double* u, int32_t* ids);
+
+/* g4s_sample plus the optional device-side outputs described above. */
+int g4s_sample_ex(g4s_sampler* sampler, const void* d_logits, int32_t dtype, int64_t row_stride,
+                  int32_t batch, const g4s_params* params, const double* u, int32_t* ids,
+                  const g4s_outputs* outputs);
+
+/* Stream-ordered variant for callers that keep parameters on the device
+ * (graph capture, serving loops).  d_params, d_u and d_ids are device
+ * arrays of `batch` entries.  `k_bound` >= every TopK of a top-k-path row
+ * (1..g4s_max_top_k(); 0 when no row takes the top-k path) sizes the launch;
+ * `full_rows` != 0 when some row may take the full-vocabulary path.  Rows
+ * that violate k_bound get id -1 and G4S_FLAG_ERROR.  Returns after
+ * enqueueing; results are valid once the stream reaches this point. */
+int g4s_sample_async(g4s_sampler* sampler, const void* d_logits, int32_t dtype,
+                     int64_t row_stride, int32_t batch, const g4s_params* d_params,
+                     const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,
+                     const g4s_outputs* outputs);
+
+/* LM head for the sampler's config-5 workload: logits = W * h for `batch`
+ * hidden vectors, with W in the engine's Q4_0 layout (TQ4Block rows,
+ * src/Gemma4.Types.pas:139-142: fp16 scale + 16 interleaved nibble bytes per
+ * 32 weights).  Bit-exact with CpuMatVecQ4 (src/Gemma4.Tensors.pas:546-598):
+ * each logit is the left-to-right single-rounding sum over the row.
+ *   d_weights  device, rows*(cols/32)*18 bytes; d_hidden device [batch*cols] fp32;
+ *   d_logits   device [batch*logits_stride] fp32 output.  cols % 32 == 0.
+ * Stream-ordered on the handle's stream. */
+int g4s_lmhead_q4_0(g4s_sampler* sampler, const void* d_weights, int32_t rows, int32_t cols,
+                    const float* d_hidden, int32_t batch, float* d_logits,
+                    int64_t logits_stride);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,247 @@
+"""GPU parity of the top-k path (0 < TopK < V) against the CPU oracle, through
+the C ABI.  Token ids, survivor index sets, probabilities, LSum and the greedy
+id must all equal the oracle's bit for bit (the stated tolerance for
+probabilities is 1e-6 relative; exact equality is asserted).  Draws whose
+threshold lies within 1e-6 of a running-sum boundary are counted and printed.
+"""
+import numpy as np
+import pytest
+
+from gemma4_sampler import hip, native, workload as wl
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+V = wl.V_GEMMA4
+CAP = wl.SOFTCAP_GEMMA4
+SEED = 20261201
+
+
+def _params(t, k, p):
+    return [native.TSamplingParams.make(float(a), int(b), float(c)) for a, b, c in zip(t, k, p)]
+
+
+def check_rows(orc, rows, t, k, p, u, got_ids, outs, softcap=CAP, label=""):
+    """Compare every row with the oracle; returns the number of boundary draws."""
+    boundary = 0
+    for r in range(len(rows)):
+        tok, det, idx, probs = orc.do_sample(rows[r], t[r], k[r], p[r], u[r], softcap=softcap)
+        ctx = f"{label} row {r} (T={t[r]}, K={k[r]}, P={p[r]}, u={u[r]!r})"
+        assert got_ids[r] == tok, f"{ctx}: gpu id {got_ids[r]} != oracle {tok}"
+        if outs is not None:
+            n = det["count"]
+            assert outs["count"][r] == n, ctx
+            assert np.array_equal(outs["indices"][r][:n], idx), ctx
+            gp = outs["probs"][r][:n]
+            rel = np.max(np.abs(gp.astype(np.float64) - probs) / np.maximum(probs, 1e-45)) if n else 0
+            assert rel <= 1e-6, f"{ctx}: prob rel diff {rel}"
+            assert np.array_equal(gp.view(np.uint32), probs.view(np.uint32)), f"{ctx}: probs not bit-exact"
+            assert outs["lsum"][r] == det["lsum"], ctx
+            assert outs["argmax"][r] == idx[det["argmax_pos"]], ctx
+        if det["drew"] and det["reached"]:
+            th = det["threshold"]
+            d = min(th - det["cum_prev"] if det["chosen_pos"] > 0 else np.inf, det["cum_at"] - th)
+            boundary += d < 1e-6
+    return boundary
+
+
+@pytest.fixture(scope="module")
+def big():
+    s = native.Sampler(V, max_batch=64, softcap=CAP)
+    yield s
+    s.close()
+
+
+def test_generators_match_host():
+    n = 3
+    d = hip.Buffer(n * V * 4)
+    wl.dev_peaky_rows(d, SEED, 98, n, V, greedy_every=100)
+    hip.synchronize()
+    host = wl.host_peaky_rows(SEED, 98, n, V, greedy_every=100)
+    dev = d.download(np.float32).reshape(n, V)
+    assert np.array_equal(dev.view(np.uint32), host.view(np.uint32))
+    b = hip.Buffer(2 * V * 2)
+    wl.dev_flat_bf16_rows(b, SEED, 0, 2, V)
+    hip.synchronize()
+    assert np.array_equal(b.download(np.uint16).reshape(2, V), wl.host_flat_bf16_rows(SEED, 0, 2, V))
+    w = hip.Buffer(64 * 80 * 18)
+    wl.dev_q4_weights(w, SEED, 64, 2560)
+    h = hip.Buffer(4 * 2560 * 4)
+    wl.dev_hidden(h, SEED, 4, 2560)
+    hip.synchronize()
+    assert np.array_equal(w.download(np.uint8), wl.host_q4_weights(SEED, 64, 2560))
+    assert np.array_equal(h.download(np.float32).reshape(4, 2560).view(np.uint32),
+                          wl.host_hidden(SEED, 4, 2560).view(np.uint32))
+
+
+def test_peaky_row_single(big, orc):
+    """One peaky row, T=0.7 K=64 P=0.95 (the CPU-reference configuration)."""
+    row = wl.host_peaky_rows(SEED, 0, 1, V)
+    u = wl.host_row_u(SEED, 0, 1)
+    d = hip.Buffer.from_array(row)
+    outs = native.DeviceOutputs(1, 64)
+    _, ids = big.sample(d, 1, [native.TSamplingParams.make(0.7, 64, 0.95)], u,
+                        outputs=outs.struct)
+    o = outs.read()
+    check_rows(orc, row, [0.7], [64], [0.95], u, ids, o, label="peaky")
+    assert o["flags"][0] & native.FLAG_TOPK_PATH and o["count"][0] == 64
+
+
+def test_decode_rows_back_to_back(big, orc):
+    """300 peaky rows one at a time (B=1), every 100th greedy with planted ties."""
+    n = 300
+    rows = wl.host_peaky_rows(SEED, 0, n, V, greedy_every=wl.GREEDY_EVERY)
+    u = wl.host_row_u(SEED, 0, n)
+    t, k, p = wl.peaky_params(range(n))
+    d = hip.Buffer.from_array(rows)
+    ids = np.empty(n, np.int32)
+    for r in range(n):
+        _, one = big.sample(d.offset(r * V * 4), 1, _params(t[r:r + 1], k[r:r + 1], p[r:r + 1]),
+                            u[r:r + 1])
+        ids[r] = one[0]
+    nb = check_rows(orc, rows, t, k, p, u, ids, None, label="decode")
+    for r in range(wl.GREEDY_EVERY - 1, n, wl.GREEDY_EVERY):
+        m = rows[r].max()
+        assert ids[r] == int(np.flatnonzero(rows[r] == m)[0]), "lowest index among planted maxima"
+    print(f"decode rows: {n}, boundary draws (|u*P - cum| < 1e-6): {nb}")
+
+
+def test_mixed_batch(big, orc):
+    """B=64 peaky rows with per-row T ~ U(0.3,1.5), K in {1,20,64,256}, P in {.8,.9,.95,1}."""
+    B = 64
+    rows = wl.host_peaky_rows(SEED + 1, 0, B, V)
+    t, k, p = wl.host_mixed_params(SEED + 1, 0, B)
+    u = wl.host_row_u(SEED + 1, 0, B)
+    d = hip.Buffer.from_array(rows)
+    outs = native.DeviceOutputs(B, 256)
+    _, ids = big.sample(d, B, _params(t, k, p), u, outputs=outs.struct)
+    nb = check_rows(orc, rows, t, k, p, u, ids, outs.read(), label="mixed")
+    print(f"mixed batch: boundary draws {nb}")
+
+
+def test_async_matches_sync(big, orc):
+    B = 16
+    rows = wl.host_peaky_rows(SEED + 2, 0, B, V)
+    t, k, p = wl.host_mixed_params(SEED + 2, 0, B)
+    u = wl.host_row_u(SEED + 2, 0, B)
+    d = hip.Buffer.from_array(rows)
+    parr = native.params_array(_params(t, k, p))
+    dp = hip.Buffer(16 * B)
+    hip.check(hip.lib().hipMemcpy(dp.ptr, parr, 16 * B, hip.H2D))
+    du = hip.Buffer.from_array(u)
+    di = hip.Buffer(4 * B)
+    big.sample_async(d, B, dp, du, int(k.max()), 0, di)
+    hip.synchronize()
+    _, ids = big.sample(d, B, _params(t, k, p), u)
+    assert np.array_equal(di.download(np.int32), ids)
+    check_rows(orc, rows, t, k, p, u, ids, None, label="async")
+
+
+@pytest.mark.parametrize("vocab", [2, 3, 7, 100, 1000, 5000, 40000])
+def test_small_vocab_random(orc, vocab):
+    """Integer-valued rows (dense ties), masked logits, every K regime incl. V-1."""
+    rng = np.random.default_rng(vocab)
+    B = 24
+    s = native.Sampler(vocab, max_batch=B, softcap=CAP)
+    rows = np.empty((B, vocab), F32)
+    for r in range(B):
+        kind = r % 4
+        if kind == 0:
+            rows[r] = rng.normal(0, 3, vocab)
+        elif kind == 1:
+            rows[r] = rng.integers(0, 6, vocab)
+        elif kind == 2:
+            rows[r] = rng.integers(0, 3, vocab)
+            rows[r][rng.random(vocab) < 0.3] = -np.inf
+        else:
+            rows[r] = np.sort(rng.integers(0, 50, vocab)).astype(F32)
+    k = np.array([rng.choice([1, 2, min(5, vocab - 1), min(64, vocab - 1), vocab - 1,
+                              min(1024, vocab - 1)]) for _ in range(B)], np.int32)
+    k = np.clip(k, 1, vocab - 1)
+    t = rng.choice([0.0, 0.7, 1.0, 1.3], B).astype(F32)
+    p = rng.choice([0.0, 0.5, 0.95, 1.0], B).astype(F32)
+    u = np.floor(rng.random(B) * 2**32) / 2**32
+    d = hip.Buffer.from_array(rows)
+    cap = int(k.max())
+    outs = native.DeviceOutputs(B, cap)
+    rc, ids = s.sample(d, B, _params(t, k, p), u, outputs=outs.struct, check=False)
+    o = outs.read()
+    empty = [r for r in range(B) if not np.any(rows[r] > F32(-1e30))]
+    if empty:
+        assert rc == native.G4S_ERR_EMPTY_ROW
+        for r in empty:
+            assert ids[r] == -1 and (o["flags"][r] & native.FLAG_EMPTY)
+    else:
+        assert rc == 0, s.last_error()
+    keep = [r for r in range(B) if r not in empty]
+    sub = {key: (val[keep] if hasattr(val, "__len__") else val) for key, val in o.items()}
+    check_rows(orc, rows[keep], t[keep], k[keep], p[keep], u[keep], ids[keep], sub,
+               label=f"V={vocab}")
+    s.close()
+
+
+def test_heap_tie_counterexample(orc):
+    s = native.Sampler(4, max_batch=1, softcap=CAP)
+    row = np.array([1, 1, 4, 2], F32)
+    d = hip.Buffer.from_array(row)
+    outs = native.DeviceOutputs(1, 3)
+    _, ids = s.sample(d, 1, [native.TSamplingParams.make(0.7, 3, 0.95)], [0.25],
+                      outputs=outs.struct)
+    o = outs.read()
+    assert list(o["indices"][0]) == [1, 2, 3]
+    assert o["flags"][0] & native.FLAG_HEAP_REPLAY
+    check_rows(orc, row[None], [0.7], [3], [0.95], [0.25], ids, o)
+    s.close()
+
+
+def test_full_size_tie_regimes(big, orc):
+    """Full-size rows whose K-th value is massively tied: all-equal rows
+    (exact per-chunk select, lowest-index rule), 0/1 rows with late 2s (heap
+    replay), and bf16-valued rows."""
+    rng = np.random.default_rng(77)
+    rows = np.zeros((4, V), F32)
+    rows[1] = rng.integers(0, 2, V)
+    rows[1][rng.choice(V, 10, replace=False)] = 2.0
+    rows[2] = (rng.normal(0, 0.5, V).astype(F32).view(np.uint32) & 0xFFFF0000).view(F32)
+    rows[3] = rng.integers(0, 2, V)
+    rows[3][V - 5:] = 3.0
+    t = np.array([0.7, 1.0, 1.0, 0.5], F32)
+    k = np.array([64, 64, 256, 20], np.int32)
+    p = np.array([0.95, 0.9, 0.99, 0.8], F32)
+    u = np.array([0.5, 0.25, 0.75, 0.125])
+    d = hip.Buffer.from_array(rows)
+    outs = native.DeviceOutputs(4, 256)
+    _, ids = big.sample(d, 4, _params(t, k, p), u, outputs=outs.struct)
+    o = outs.read()
+    check_rows(orc, rows, t, k, p, u, ids, o, label="ties")
+    assert o["flags"][0] & native.FLAG_TIE_LOWEST
+    assert o["flags"][3] & native.FLAG_HEAP_REPLAY
+
+
+def test_bf16_logits_topk(orc):
+    B = 8
+    s = native.Sampler(V, max_batch=B, softcap=CAP)
+    b = wl.host_flat_bf16_rows(SEED + 3, 0, B, V)
+    rows = (b.astype(np.uint32) << 16).view(F32)
+    k = np.array([1, 20, 64, 256, 1, 20, 64, 256], np.int32)
+    t = np.full(B, 1.0, F32)
+    p = np.full(B, 0.99, F32)
+    u = wl.host_row_u(SEED + 3, 0, B)
+    d = hip.Buffer.from_array(b)
+    outs = native.DeviceOutputs(B, 256)
+    _, ids = s.sample(d, B, _params(t, k, p), u, dtype=native.DTYPE_BF16, outputs=outs.struct)
+    check_rows(orc, rows, t, k, p, u, ids, outs.read(), label="bf16")
+    s.close()
+
+
+def test_argument_errors_on_device(big):
+    d = hip.Buffer(V * 4)
+    rc, _ = big.sample(d, 1, [native.TSamplingParams.make(1.0, 2000, 0.9)], [0.5], check=False)
+    assert rc == native.G4S_ERR_UNSUPPORTED and "TopK" in big.last_error()
+    rc, _ = big.sample(d, 1, [native.TSamplingParams.make(1.0, 5, 0.9)], [1.0], check=False)
+    assert rc == native.G4S_ERR_INVALID_ARGUMENT
+    rc, _ = big.sample(d.offset(4), 1, [native.TSamplingParams.make(1.0, 5, 0.9)], [0.5],
+                       check=False)
+    assert rc == native.G4S_ERR_INVALID_ARGUMENT and "aligned" in big.last_error()
+    rc, _ = big.sample(d, 65, [native.TSamplingParams.make(1.0, 5, 0.9)] * 65, [0.5] * 65,
+                       check=False)
+    assert rc == native.G4S_ERR_INVALID_ARGUMENT

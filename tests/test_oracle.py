@@ -1,0 +1,263 @@
+"""Pins the CPU oracle (oracle/g4s_oracle.cpp) against closed forms,
+invariants, brute force and hand-traced heap cases, so that a plausible
+restatement mistake (a dropped term, a flipped comparison, a wrong index)
+fails here.  The reference ships no sampler tests or golden vectors."""
+import itertools
+
+import numpy as np
+import pytest
+
+F32 = np.float32
+
+
+def test_semantics_switch(orc):
+    assert orc.load().orc_semantics().decode() == "Extended=x87-80bit"
+    assert orc.load(double=True).orc_semantics().decode() == "Extended=binary64"
+
+
+# --------------------------------------------------------------- a6 top-k
+def test_heap_tie_counterexample(orc):
+    # Hand trace of Model.pas:2632-2664 on [1,1,4,2], K=3: index 0 is evicted.
+    assert list(orc.select_topk_indices([1, 1, 4, 2], 3)) == [1, 2, 3]
+
+
+def test_heap_hand_traces(orc):
+    # [5,5,5] K=2: third 5 is rejected (v <= root) -> first two survive
+    assert list(orc.select_topk_indices([5, 5, 5], 2)) == [0, 1]
+    # [1,2,2,3] K=2: 1 in, 2 in (root 1), 2@2 replaces root 1, 3 replaces root (2@1 or 2@2)
+    # heap after 2@2: [(2,2),(2,1)]? trace: init[-e,-e]; 1@0 -> child=1: -e<1 -> heap[0]=-e,pos=1 ->
+    # [(-e),(1,0)]; 2@1 root -e: child 1 (1,0) >= 2? no -> heap[0]=(1,0), pos=1 -> [(1,0),(2,1)];
+    # 2@2: root 1 < 2: child 1 (2,1) >= 2 -> break -> heap[0]=(2,2) -> [(2,2),(2,1)];
+    # 3@3: root 2 < 3: child (2,1) >= 3? no -> heap[0]=(2,1), pos 1 -> [(2,1),(3,3)]
+    assert list(orc.select_topk_indices([1, 2, 2, 3], 2)) == [1, 3]
+
+
+def _brute_multiset(x, k):
+    v = np.array(x, F32)
+    valid = v[v > F32(-1e30)]
+    return sorted(valid.tolist(), reverse=True)[:k]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_topk_multiset_and_order(orc, seed):
+    rng = np.random.default_rng(seed)
+    for _ in range(60):
+        V = int(rng.integers(1, 300))
+        alphabet = rng.integers(2, 40)
+        x = rng.integers(0, alphabet, V).astype(F32) - alphabet / 2
+        if rng.random() < 0.3:
+            x[rng.random(V) < 0.2] = -np.inf
+        K = int(rng.integers(1, V + 2))
+        idx = orc.select_topk_indices(x, K)
+        assert list(idx) == sorted(idx), "ascending by index"
+        assert len(set(idx.tolist())) == len(idx)
+        assert sorted(x[idx].tolist(), reverse=True) == _brute_multiset(x, K)
+
+
+def test_k1_is_first_argmax(orc):
+    rng = np.random.default_rng(7)
+    for _ in range(200):
+        x = rng.integers(0, 5, int(rng.integers(1, 50))).astype(F32)
+        assert list(orc.select_topk_indices(x, 1)) == [int(np.argmax(x))]
+
+
+def test_exhaustive_tiny(orc):
+    # all rows over {0,1,2} of length <= 6, all K: multiset + ascending + K=1 rule
+    for V in range(1, 7):
+        for row in itertools.product([0.0, 1.0, 2.0], repeat=V):
+            x = np.array(row, F32)
+            for K in range(1, V + 1):
+                idx = orc.select_topk_indices(x, K)
+                assert sorted(x[idx].tolist(), reverse=True) == _brute_multiset(x, K)
+                assert list(idx) == sorted(idx)
+            assert list(orc.select_topk_indices(x, 1)) == [int(np.argmax(x))]
+
+
+def test_minus_1e30_never_selected(orc):
+    x = np.array([-1e30, -1e30, -3e38, 0.5], F32)
+    assert list(orc.select_topk_indices(x, 3)) == [3]
+    assert list(orc.select_topk_indices(np.array([-1e30], F32), 1)) == []
+
+
+# --------------------------------------------------------------- a9 softcap
+def test_softcap_closed_forms(orc):
+    assert orc.softcap_topk(0.0) == 0.0
+    assert orc.logit_softcap([0.0])[0] == 0.0
+    for x in (0.3, 2.0, 17.0, 29.0, 100.0):
+        assert orc.softcap_topk(-x) == -orc.softcap_topk(x)
+    assert orc.softcap_topk(1e6) == F32(30.0)
+    assert orc.logit_softcap([1e6])[0] == F32(30.0)
+    xs = np.linspace(-80, 80, 4001, dtype=F32)
+    ys = np.array([orc.softcap_topk(x) for x in xs])
+    assert np.all(np.diff(ys) >= 0), "monotone"
+
+
+def test_softcap_forms_are_correctly_rounded(orc):
+    mp = pytest.importorskip("mpmath")
+    mp.mp.dps = 50
+    rng = np.random.default_rng(3)
+    inv = F32(1.0) / F32(30.0)
+    for x in rng.normal(0, 12, 300).astype(F32):
+        a = mp.mpf(float(x))
+        exact_topk = 30 * mp.tanh(a / 30)
+        exact_full = mp.tanh(a * mp.mpf(float(inv))) * 30
+        assert orc.softcap_topk(x) == _rn32(exact_topk)
+        assert orc.logit_softcap([x])[0] == _rn32(exact_full)
+
+
+def _rn32(v):
+    import mpmath as mp
+    f = F32(float(v))
+    cands = [f, np.nextafter(f, F32(np.inf)), np.nextafter(f, F32(-np.inf))]
+    return min(cands, key=lambda c: abs(mp.mpf(float(c)) - v))
+
+
+# --------------------------------------------------------------- a8 softmax
+def test_softmax_sequential_sum(orc):
+    rng = np.random.default_rng(11)
+    x = rng.normal(0, 2, 5000).astype(F32)
+    p, lsum = orc.softmax_f32(x)
+    m = x.max()
+    e = np.array([orc.exp_diff(v, m) for v in x], F32)
+    assert lsum == np.cumsum(e, dtype=F32)[-1], "left-to-right binary32 sum"
+    inv = F32(1.0) / lsum
+    assert np.array_equal(p, e * inv), "reciprocal multiply, not division"
+    assert abs(float(lsum) - float(np.sum(e.astype(np.float64)))) < 1e-3 * float(lsum)
+
+
+def test_seqsum_literal(orc):
+    rng = np.random.default_rng(12)
+    a = rng.random(100000).astype(F32)
+    s, first = orc.seqsum(a, F32(1000.5))
+    c = np.cumsum(a, dtype=F32)
+    assert s == c[-1]
+    assert first == int(np.argmax(c >= F32(1000.5)))
+
+
+# --------------------------------------------------- a5/a7 DoSample tail
+def test_equal_logits_uniform(orc):
+    x = np.zeros(1000, F32)
+    tok, det, idx, probs = orc.do_sample(x, 0.7, 8, 0.95, 0.0)
+    assert list(idx) == list(range(8))  # K-th value tied everywhere: heap keeps indices 0..7
+    assert np.all(probs == F32(1.0) / F32(8.0))
+
+
+def test_u_zero_picks_first_survivor(orc):
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 3, 4096).astype(F32)
+    for k in (5, 64, 0):
+        tok, det, idx, probs = orc.do_sample(x, 0.7, k, 0.95, 0.0)
+        assert tok == int(idx[0]) and det["chosen_pos"] == 0
+
+
+def test_threshold_above_total_falls_back_to_argmax(orc):
+    x = np.array([0.0, 3.0, 1.0, 3.0], F32)
+    # P huge => u*P beyond the final running sum
+    tok, det, idx, probs = orc.do_sample(x, 1.0, 3, 1e30, 0.5)
+    assert det["reached"] == 0 and tok == int(idx[det["argmax_pos"]])
+    assert tok == 1  # first maximum of p
+
+
+def test_temperature_nonpositive_is_greedy(orc):
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 3, 2048).astype(F32)
+    for T in (0.0, -1.0):
+        for k in (10, 0):
+            tok, det, idx, probs = orc.do_sample(x, T, k, 0.95, 0.9)
+            assert det["drew"] == 0
+            assert tok == int(np.argmax(x))
+
+
+def test_temperature_one_is_unscaled(orc):
+    rng = np.random.default_rng(8)
+    x = rng.normal(0, 3, 1024).astype(F32)
+    _, _, idx1, p1 = orc.do_sample(x, 1.0, 16, 0.9, 0.3, softcap=0.0)
+    e = np.array([orc.exp_diff(v, x[idx1].max()) for v in x[idx1]], F32)
+    lsum = np.cumsum(e, dtype=F32)[-1]
+    assert np.array_equal(p1, e / lsum)
+
+
+def test_topp_nonpositive_picks_first(orc):
+    rng = np.random.default_rng(9)
+    x = rng.normal(0, 3, 1024).astype(F32)
+    tok, det, idx, _ = orc.do_sample(x, 0.8, 32, 0.0, 0.77)
+    assert det["chosen_pos"] == 0
+
+
+def test_position_monotone_in_u(orc):
+    rng = np.random.default_rng(10)
+    x = rng.normal(0, 1, 2048).astype(F32)
+    for k in (64, 0):
+        last = -1
+        for u in np.linspace(0, 0.999, 40):
+            _, det, _, _ = orc.do_sample(x, 1.3, k, 0.9, u)
+            assert det["chosen_pos"] >= last
+            last = det["chosen_pos"]
+
+
+def test_full_path_matches_pieces(orc):
+    rng = np.random.default_rng(13)
+    x = rng.normal(0, 1, 3000).astype(F32)
+    T, P, u = 0.8, 0.9, 0.37
+    s = orc.logit_softcap(x)
+    inv = F32(1.0) / F32(T)
+    s = s * inv
+    p, lsum = orc.softmax_f32(s)
+    t = F32(np.float64(u) * np.float64(F32(P)))
+    c = np.cumsum(p, dtype=F32)
+    want = int(np.argmax(c >= t))
+    tok, det, idx, probs = orc.do_sample(x, T, 0, P, u)
+    assert tok == want and np.array_equal(probs, p) and det["lsum"] == lsum
+
+
+# ----------------------------------------------------- conversions / Q4_0
+def test_bf16_widening_exhaustive(orc):
+    # every non-NaN bf16 pattern (ctypes' float return quiets signalling NaNs)
+    bits = np.arange(65536, dtype=np.uint32)
+    not_nan = ((bits >> 7) & 0xFF) != 0xFF
+    not_nan |= (bits & 0x7F) == 0
+    want = (bits << 16).view(F32)
+    got = np.array([orc.bf16_to_f32(b) for b in bits[not_nan]], F32)
+    assert np.array_equal(got.view(np.uint32), want[not_nan].view(np.uint32))
+
+
+def test_f16_normals_match_ieee_and_denormal_quirk(orc):
+    for b in list(range(0x0400, 0x7C00, 97)) + [0x3C00, 0xBC00, 0x7BFF]:
+        assert orc.f16_to_f32(b) == np.array([b], np.uint16).view(np.float16).astype(F32)[0]
+    # Types.pas:459-463 raises the exponent while normalising a denormal:
+    # 0x0001 decodes to 2^-4, not 2^-24 (restated as written)
+    assert orc.f16_to_f32(0x0001) == F32(0.0625)
+    assert orc.f16_from_f32(F32(1.0)) == 0x3C00
+    assert orc.f16_from_f32(F32(1e-6)) == 0  # flush to zero
+
+
+def test_q4_roundtrip(orc):
+    rng = np.random.default_rng(14)
+    x = rng.normal(0, 1, 32 * 50).astype(F32)
+    q = orc.f32_to_q4(x)
+    for b in range(50):
+        blk = q[b * 18:(b + 1) * 18]
+        d = orc.dequant_q4_block(blk)
+        scale = orc.f16_to_f32(int(blk[0]) | (int(blk[1]) << 8))
+        assert np.all(np.abs(d - x[b * 32:(b + 1) * 32]) <= scale * 1.5 + 1e-6)
+
+
+def test_matvec_q4_one_hot_and_ones(orc):
+    rng = np.random.default_rng(15)
+    rows, cols = 16, 128
+    w = rng.integers(0, 256, rows * (cols // 32) * 18).astype(np.uint8)
+    for r in range(rows):
+        for b in range(cols // 32):  # plausible fp16 scales
+            off = (r * (cols // 32) + b) * 18
+            s = orc.f16_from_f32(F32(rng.uniform(0.001, 0.02)))
+            w[off], w[off + 1] = s & 0xFF, s >> 8
+    deq = np.concatenate([orc.dequant_q4_block(w[i * 18:(i + 1) * 18])
+                          for i in range(rows * cols // 32)]).reshape(rows, cols)
+    for c in (0, 1, 31, 32, 77, 127):
+        h = np.zeros(cols, F32)
+        h[c] = 1.0
+        assert np.array_equal(orc.matvec_q4(w, h, rows, cols), deq[:, c])
+    ones = np.ones(cols, F32)
+    got = orc.matvec_q4(w, ones, rows, cols)
+    want = np.array([np.cumsum(deq[r], dtype=F32)[-1] for r in range(rows)], F32)
+    assert np.array_equal(got, want)
