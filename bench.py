@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X token sampler (libgemma4_sampler.so) on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+
+The headline workload is the decode-style single-row stream: B=1, V=262144
+fp32 peaky logits, T=0.7, TopK=64, TopP=0.95, every 100th row greedy
+(TopK=1) with the row maximum planted 2-4 more times.  A "step" is one
+sampler call on one freshly generated row; K steps are timed, after W
+untimed warm-up rows.  `value` is the per-row p50 latency of the
+synchronous call (entry to token id on the host), in microseconds.
+
+Also reported on the same line: p99, the batched mixed-settings workload
+(B=64 fp32, per-row T/K/P) as rows/s and GB/s, the flat bf16 full-vocabulary
+workload (B=256, TopK disabled, P=0.99) as rows/s, GB/s and the fraction of
+the HBM roofline, the roofline of the dominant kernel measured with HIP
+events on the sampler's stream, and the CPU oracle's per-row latency on the
+host (one core, a bounded sample of the same rows).  Every sampled id of the
+timed rows is checked against the CPU oracle.
+"""
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "gemma4.pas_amd")
+for _p in (PKG, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "sampler p50 latency (B=1) + rows/s & HBM GB/s (B=256), V=262144"
+HBM_PEAK_GBPS = 8000.0
+SEED = 4242
+V = 262144
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def harness():
+    from gemma4_sampler import native
+    path = os.path.join(PKG, "lib", "libg4s_harness.so")
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is missing: run __graft_entry__.build() first")
+    native.load()
+    H = ctypes.CDLL(path)
+    vp, i32, i64, u64, f32 = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64,
+                              ctypes.c_float)
+    H.g4h_decode_latency.argtypes = [vp, vp, vp, u64, i32, i32, i32, i32, f32, i32, f32, i32,
+                                     vp, vp, vp]
+    H.g4h_batch_throughput.argtypes = [vp, vp, vp, i32, i64, i32, vp, vp, i32, i32, vp, i32,
+                                       i32, vp, vp, vp]
+    return H
+
+
+def _vp(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def pct(a, q):
+    return float(np.percentile(np.asarray(a, np.float64), q))
+
+
+def decode_latency(H, stream, rows0, nrows, mode):
+    """Run the B=1 decode stream; returns (host_us, gpu_us, ids)."""
+    from gemma4_sampler import hip, native, workload as wl
+    s = native.Sampler(V, max_batch=1, softcap=wl.SOFTCAP_GEMMA4, stream=stream)
+    d = hip.Buffer(V * 4)
+    host_us = np.zeros(nrows, np.float64)
+    gpu_us = np.zeros(nrows, np.float32)
+    ids = np.full(nrows, -9, np.int32)
+    rc = H.g4h_decode_latency(s.h, stream.handle, d.ptr, SEED, rows0, nrows, V, wl.GREEDY_EVERY,
+                              0.7, 64, 0.95, mode, _vp(host_us), _vp(gpu_us), _vp(ids))
+    if rc != 0:
+        raise RuntimeError(f"g4h_decode_latency mode {mode} failed: {rc} {s.last_error()}")
+    s.close()
+    d.free()
+    return host_us, gpu_us, ids
+
+
+def check_decode_ids(rows0, ids, threads, time_rows):
+    """Every id of the decode stream against the CPU oracle (host-generated
+    rows, one call per row on one core).  The first `time_rows` calls are
+    timed: that is the CPU baseline.  Returns (mismatches, latencies_us)."""
+    from gemma4_sampler import workload as wl
+    from oracle import oracle as orc
+    n = len(ids)
+    bad = 0
+    lat = []
+    chunk = 256
+    for c0 in range(0, n, chunk):
+        m = min(chunk, n - c0)
+        rows = wl.host_peaky_rows(SEED, rows0 + c0, m, V, greedy_every=wl.GREEDY_EVERY,
+                                  threads=threads)
+        t, k, p = wl.peaky_params(range(rows0 + c0, rows0 + c0 + m))
+        u = wl.host_row_u(SEED, rows0 + c0, m)
+        for r in range(m):
+            t0 = time.perf_counter()
+            want = orc.sample_batch(rows[r:r + 1], 0, V, V, (t[r:r + 1], k[r:r + 1], p[r:r + 1]),
+                                    u[r:r + 1], softcap=wl.SOFTCAP_GEMMA4, threads=1)
+            if len(lat) < time_rows:
+                lat.append((time.perf_counter() - t0) * 1e6)
+            bad += int(want[0] != ids[c0 + r])
+    return bad, np.asarray(lat)
+
+
+def batch_throughput(H, stream, d_logits, dtype, batch, params, u, k_bound, full_rows, warmup,
+                     steps):
+    from gemma4_sampler import hip, native, workload as wl
+    s = native.Sampler(V, max_batch=batch, softcap=wl.SOFTCAP_GEMMA4, stream=stream)
+    parr = native.params_array(params)
+    dp = hip.Buffer(ctypes.sizeof(parr))
+    hip.check(hip.lib().hipMemcpy(dp.ptr, parr, ctypes.sizeof(parr), hip.H2D))
+    du = hip.Buffer.from_array(np.asarray(u, np.float64))
+    di = hip.Buffer(4 * batch)
+    step_us = np.zeros(steps, np.float32)
+    tot = ctypes.c_float()
+    wall = ctypes.c_double()
+    rc = H.g4h_batch_throughput(s.h, stream.handle, d_logits.ptr, dtype, V, batch, dp.ptr, du.ptr,
+                                k_bound, full_rows, di.ptr, warmup, steps, _vp(step_us),
+                                ctypes.byref(tot), ctypes.byref(wall))
+    if rc != 0:
+        raise RuntimeError(f"g4h_batch_throughput failed: {rc} {s.last_error()}")
+    ids = di.download(np.int32)
+    s.close()
+    return step_us, tot.value, wall.value, ids
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-rows", type=int, default=10000)
+    ap.add_argument("--batch-steps", type=int, default=200)
+    ap.add_argument("--quick", action="store_true", help="small run for profiling")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the sampler is a single-GPU path (rows are "
+              f"independent; a multi-GPU deployment runs one sampler per GPU). "
+              f"--gpus {args.gpus} is not supported.", file=sys.stderr)
+        return 2
+    if args.quick:
+        args.steps, args.warmup, args.cpu_rows, args.batch_steps = 500, 50, 50, 50
+
+    from gemma4_sampler import hip, native, workload as wl
+    H = harness()
+    if hip.device_count() < 1:
+        raise RuntimeError("no HIP device: the sampler has no CPU path")
+    stream = hip.Stream()
+    threads = min(16, os.cpu_count() or 1)
+
+    # ---- B=1 decode stream (headline) -------------------------------------
+    log(f"decode stream: warmup {args.warmup} rows, timed {args.steps} rows (sync API)")
+    decode_latency(H, stream, 0, args.warmup, 0)
+    host_us, gpu_us, ids = decode_latency(H, stream, args.warmup, args.steps, 0)
+    log(f"decode stream: p50 {pct(host_us, 50):.2f} us, p99 {pct(host_us, 99):.2f} us")
+    log("decode stream: checking every id against the CPU oracle (one core per row)")
+    bad, cpu_lat = check_decode_ids(args.warmup, ids, threads,
+                                    0 if args.no_cpu else args.cpu_rows)
+    log(f"decode stream: {bad} mismatching ids of {len(ids)}")
+    n_async = min(args.steps, 2000)
+    a_host, a_gpu, a_ids = decode_latency(H, stream, args.warmup, n_async, 1)
+    bad_async = int(np.sum(a_ids != ids[:n_async]))
+    log(f"decode stream (async + readback): p50 {pct(a_host, 50):.2f} us, mismatches {bad_async}")
+
+    # ---- dominant kernel of the decode stream: top-k path at B=1 ------------
+    d1 = hip.Buffer(V * 4)
+    wl.dev_peaky_rows(d1, SEED, 0, 1, V, stream=stream)
+    stream.synchronize()
+    k_us, _, _, _ = batch_throughput(H, stream, d1, native.DTYPE_F32, 1,
+                                     [native.TSamplingParams.make(0.7, 64, 0.95)], [0.5], 64, 0,
+                                     100, max(args.batch_steps, 500))
+    k_med = float(np.median(k_us))
+    k_mean = float(np.mean(k_us))
+    log(f"top-k kernel B=1: median {k_med:.2f} us, mean {k_mean:.2f} us per launch")
+
+    # ---- B=64 mixed settings, fp32 ------------------------------------------
+    B3 = 64
+    d3 = hip.Buffer(B3 * V * 4)
+    wl.dev_peaky_rows(d3, SEED + 3, 0, B3, V, stream=stream)
+    stream.synchronize()
+    t3, k3, p3 = wl.host_mixed_params(SEED + 3, 0, B3)
+    u3 = wl.host_row_u(SEED + 3, 0, B3)
+    par3 = [native.TSamplingParams.make(a, b, c) for a, b, c in zip(t3, k3, p3)]
+    s3_us, _, _, ids3 = batch_throughput(H, stream, d3, native.DTYPE_F32, B3, par3, u3,
+                                         int(k3.max()), 0, 20, args.batch_steps)
+    rows3 = wl.host_peaky_rows(SEED + 3, 0, B3, V, threads=threads)
+    from oracle import oracle as orc
+    want3 = orc.sample_batch(rows3, 0, V, V, (t3, k3, p3), u3, softcap=wl.SOFTCAP_GEMMA4,
+                             threads=threads)
+    bad3 = int(np.sum(want3 != ids3))
+    med3 = float(np.median(s3_us))
+    b64 = {"batch": B3, "dtype": "f32", "us_per_batch_p50": med3,
+           "rows_per_s": B3 / (med3 * 1e-6), "hbm_gbps": B3 * V * 4 / (med3 * 1e-6) / 1e9,
+           "frac_hbm": B3 * V * 4 / (med3 * 1e-6) / 1e9 / HBM_PEAK_GBPS, "id_mismatches": bad3}
+    log(f"B=64 mixed: {med3:.2f} us/batch, {b64['hbm_gbps']:.0f} GB/s, mismatches {bad3}")
+    d3.free()
+
+    # ---- B=256 bf16 full-vocabulary path -------------------------------------
+    B4 = 256
+    b256 = {"batch": B4, "dtype": "bf16", "status": "not measured"}
+    try:
+        d4 = hip.Buffer(B4 * V * 2)
+        wl.dev_flat_bf16_rows(d4, SEED + 4, 0, B4, V, stream=stream)
+        stream.synchronize()
+        t4, k4, p4 = wl.flat_params(B4)
+        u4 = wl.host_row_u(SEED + 4, 0, B4)
+        par4 = [native.TSamplingParams.make(a, b, c) for a, b, c in zip(t4, k4, p4)]
+        s4_us, _, _, ids4 = batch_throughput(H, stream, d4, native.DTYPE_BF16, B4, par4, u4, 0, 1,
+                                             10, args.batch_steps)
+        med4 = float(np.median(s4_us))
+        gbps4 = B4 * V * 2 / (med4 * 1e-6) / 1e9
+        b256 = {"batch": B4, "dtype": "bf16", "us_per_batch_p50": med4,
+                "rows_per_s": B4 / (med4 * 1e-6), "hbm_gbps": gbps4,
+                "frac_hbm": gbps4 / HBM_PEAK_GBPS}
+        log(f"B=256 bf16 full path: {med4:.2f} us/batch, {gbps4:.0f} GB/s")
+        d4.free()
+    except (native.SamplerError, RuntimeError) as e:
+        b256["status"] = f"not available: {e}"
+        log(f"B=256 bf16 full path: {e}")
+
+    # ---- CPU baseline (timed above, on the same rows) ---------------------
+    cpu = None
+    if not args.no_cpu and len(cpu_lat):
+        cpu = {"value": pct(cpu_lat, 50), "unit": "us", "cores": 1, "kind": "port",
+               "sample": f"p50 per-row latency of the C++ oracle's DoSample (one call per row, "
+                         f"one host core) over the first {len(cpu_lat)} rows of the same decode "
+                         f"stream; p99 {pct(cpu_lat, 99):.1f} us; "
+                         f"{platform.processor() or platform.machine()}, "
+                         f"{os.cpu_count()} host cpus visible"}
+        log(f"CPU oracle: p50 {cpu['value']:.1f} us over {len(cpu_lat)} rows")
+
+    algo_bytes = V * 4
+    achieved = algo_bytes / (k_mean * 1e-6) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": pct(host_us, 50),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": float(np.mean(host_us)) / 1000.0,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded peaky N(0,3^2) logits + 16 spikes; greedy rows with planted "
+                "max ties)",
+        "config": {"workload": "decode stream B=1 V=262144 fp32, T=0.7 K=64 P=0.95, every "
+                               "100th row greedy; synchronous g4s_sample per row",
+                   "batch": 1, "vocab": V, "rows": args.steps},
+        "p99_us": pct(host_us, 99),
+        "gpu_event_p50_us": pct(gpu_us, 50),
+        "async_readback_p50_us": pct(a_host, 50),
+        "id_mismatches": bad + bad_async,
+        "roofline": {"bound": "hbm", "kernel": "topk_kernel (B=1)", "achieved": achieved,
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": None, "kernel_us_mean": k_mean, "kernel_us_median": k_med,
+                     "algorithmic_bytes": algo_bytes},
+        "b64_mixed": b64,
+        "b256_flat_full": b256,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0 if (bad + bad_async + bad3) == 0 else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

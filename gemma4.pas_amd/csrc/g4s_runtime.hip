@@ -315,12 +315,19 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
 
     g4s_outputs out{};
     if (outputs) out = *outputs;
+    /* ids (and flags, unless the caller wants them on the device) are written
+     * by the kernel straight into this handle's pinned host buffers: the
+     * synchronous call needs no copy after the kernel, only the stream sync. */
     uint32_t* user_flags = out.flags;
-    out.flags = s->d_flags; /* always collect flags to report empty rows */
+    for (int32_t r = 0; r < batch; ++r) {
+        s->h_ids[r] = -1;
+        s->h_flags[r] = 0u;
+    }
+    if (!user_flags) out.flags = s->h_flags;
 
     if (batch == 1) {
         rc = enqueue(s, d_logits, dtype, row_stride, 1, nullptr, nullptr, &params[0], u[0], kbound,
-                     full_rows, s->d_ids, &out);
+                     full_rows, s->h_ids, &out);
     } else {
         std::memcpy(s->h_params, params, sizeof(g4s_params) * batch);
         std::memcpy(s->h_u, u, sizeof(double) * batch);
@@ -331,17 +338,13 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
                                s->stream);
         if (e != hipSuccess) return hip_fail(s, e, "parameter upload");
         rc = enqueue(s, d_logits, dtype, row_stride, batch, s->d_params, s->d_u, nullptr, 0.0,
-                     kbound, full_rows, s->d_ids, &out);
+                     kbound, full_rows, s->h_ids, &out);
     }
     if (rc) return rc;
-    hipError_t e = hipMemcpyAsync(s->h_ids, s->d_ids, sizeof(int32_t) * batch,
-                                  hipMemcpyDeviceToHost, s->stream);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(s->h_flags, s->d_flags, sizeof(uint32_t) * batch, hipMemcpyDeviceToHost,
+    hipError_t e = hipSuccess;
+    if (user_flags)
+        e = hipMemcpyAsync(s->h_flags, user_flags, sizeof(uint32_t) * batch, hipMemcpyDeviceToHost,
                            s->stream);
-    if (e == hipSuccess && user_flags)
-        e = hipMemcpyAsync(user_flags, s->d_flags, sizeof(uint32_t) * batch,
-                           hipMemcpyDeviceToDevice, s->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) return hip_fail(s, e, "sampling");
     std::memcpy(ids, s->h_ids, sizeof(int32_t) * batch);

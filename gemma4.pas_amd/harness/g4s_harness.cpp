@@ -1,0 +1,174 @@
+/*
+ * g4s_harness.cpp -- native timing loops over the libgemma4_sampler.so C ABI.
+ *
+ * Benchmark plumbing, not part of the sampler: it drives the same entry
+ * points a host engine binds (g4s_sample, g4s_sample_async) and times them
+ * without an interpreter between the clock and the call.  Rows are produced
+ * on the device by the workload generator (libg4s_workload.so) outside the
+ * timed region, into the buffer the sampler then reads, so every sample sees
+ * freshly written logits the way the engine's LM head leaves them.
+ */
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "gemma4_sampler.h"
+#include "../workload/g4w_api.h"
+
+#define G4H_API extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+inline double now_us()
+{
+    return std::chrono::duration<double, std::micro>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+}  // namespace
+
+/*
+ * Decode-style latency: `nrows` single-row samples back to back.  Row r of
+ * the peaky workload (every `greedy_every`-th row greedy, TopK = 1, with the
+ * maximum planted 2-4 more times) is generated into d_row, then sampled with
+ * T, K, P and u of that row.
+ *   mode 0: g4s_sample (synchronous; host params in, host id out)
+ *   mode 1: g4s_sample_async (params and u already on the device) + a
+ *           4-byte id readback and a stream sync
+ * host_us[r]: wall clock of the sampler call, entry to id on the host.
+ * gpu_us[r] : hipEvent time of the same work on the sampler's stream.
+ * ids[r]    : the sampled token id.
+ */
+G4H_API int g4h_decode_latency(g4s_sampler* s, void* stream, void* d_row, uint64_t seed,
+                               int32_t row0, int32_t nrows, int32_t vocab, int32_t greedy_every,
+                               float temperature, int32_t top_k, float top_p, int32_t mode,
+                               double* host_us, float* gpu_us, int32_t* ids)
+{
+    hipStream_t st = (hipStream_t)stream;
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -100;
+    g4s_params* dpar = nullptr;
+    double* du = nullptr;
+    int32_t* did = nullptr;
+    int32_t* hid = nullptr;
+    g4s_params* hpar = nullptr;
+    double* hu = nullptr;
+    int rc = 0;
+    if (hipMalloc((void**)&dpar, sizeof(g4s_params)) != hipSuccess ||
+        hipMalloc((void**)&du, sizeof(double)) != hipSuccess ||
+        hipMalloc((void**)&did, sizeof(int32_t)) != hipSuccess ||
+        hipHostMalloc((void**)&hid, sizeof(int32_t), hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void**)&hpar, sizeof(g4s_params), hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void**)&hu, sizeof(double), hipHostMallocDefault) != hipSuccess)
+        rc = -101;
+    for (int32_t i = 0; rc == 0 && i < nrows; ++i) {
+        const int32_t r = row0 + i;
+        g4s_params p;
+        p.temperature = temperature;
+        p.top_k = (greedy_every > 0 && (r % greedy_every) == greedy_every - 1) ? 1 : top_k;
+        p.top_p = top_p;
+        p.repetition_penalty = 1.0f;
+        double u = 0.0;
+        g4w_host_row_u(seed, r, 1, &u);
+        if (g4w_dev_peaky_rows(seed, r, 1, vocab, vocab, (float*)d_row, greedy_every, st) != 0) {
+            rc = -102;
+            break;
+        }
+        if (mode == 1) {
+            *hpar = p;
+            *hu = u;
+            if (hipMemcpyAsync(dpar, hpar, sizeof(p), hipMemcpyHostToDevice, st) != hipSuccess ||
+                hipMemcpyAsync(du, hu, sizeof(u), hipMemcpyHostToDevice, st) != hipSuccess) {
+                rc = -103;
+                break;
+            }
+        }
+        if (hipStreamSynchronize(st) != hipSuccess) {
+            rc = -104;
+            break;
+        }
+        int32_t id = -1;
+        double t0 = now_us();
+        (void)hipEventRecord(e0, st);
+        if (mode == 0) {
+            rc = g4s_sample(s, d_row, G4S_DTYPE_F32, vocab, 1, &p, &u, &id);
+            (void)hipEventRecord(e1, st);
+        } else {
+            rc = g4s_sample_async(s, d_row, G4S_DTYPE_F32, vocab, 1, dpar, du, top_k, 0, did,
+                                  nullptr);
+            if (rc == 0 && hipMemcpyAsync(hid, did, 4, hipMemcpyDeviceToHost, st) != hipSuccess)
+                rc = -105;
+            (void)hipEventRecord(e1, st);
+            if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -106;
+            id = *hid;
+        }
+        double t1 = now_us();
+        if (rc != 0) break;
+        (void)hipEventSynchronize(e1);
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        host_us[i] = t1 - t0;
+        gpu_us[i] = ms * 1000.0f;
+        ids[i] = id;
+    }
+    (void)hipStreamSynchronize(st);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (dpar) (void)hipFree(dpar);
+    if (du) (void)hipFree(du);
+    if (did) (void)hipFree(did);
+    if (hid) (void)hipHostFree(hid);
+    if (hpar) (void)hipHostFree(hpar);
+    if (hu) (void)hipHostFree(hu);
+    return rc;
+}
+
+/*
+ * Batched throughput: `steps` stream-ordered samples of the same resident
+ * batch (g4s_sample_async, parameters on the device), each bracketed by a
+ * pair of events on the sampler's stream.  step_us[i] = event time of step
+ * i.  `warmup` untimed steps run first.  The whole timed loop is also
+ * bracketed by one event pair (total_us) and the host clock (wall_us).
+ */
+G4H_API int g4h_batch_throughput(g4s_sampler* s, void* stream, const void* d_logits, int32_t dtype,
+                                 int64_t row_stride, int32_t batch, const g4s_params* d_params,
+                                 const double* d_u, int32_t k_bound, int32_t full_rows,
+                                 int32_t* d_ids, int32_t warmup, int32_t steps, float* step_us,
+                                 float* total_us, double* wall_us)
+{
+    hipStream_t st = (hipStream_t)stream;
+    std::vector<hipEvent_t> ev((size_t)steps + 1);
+    for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) return -100;
+    int rc = 0;
+    for (int32_t i = 0; rc == 0 && i < warmup; ++i)
+        rc = g4s_sample_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound,
+                              full_rows, d_ids, nullptr);
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    double t0 = now_us();
+    if (rc == 0) (void)hipEventRecord(ev[0], st);
+    for (int32_t i = 0; rc == 0 && i < steps; ++i) {
+        rc = g4s_sample_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound,
+                              full_rows, d_ids, nullptr);
+        (void)hipEventRecord(ev[(size_t)i + 1], st);
+    }
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    double t1 = now_us();
+    if (rc == 0) {
+        for (int32_t i = 0; i < steps; ++i) {
+            float ms = 0.0f;
+            (void)hipEventElapsedTime(&ms, ev[(size_t)i], ev[(size_t)i + 1]);
+            step_us[i] = ms * 1000.0f;
+        }
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, ev[0], ev[(size_t)steps]);
+        *total_us = ms * 1000.0f;
+        *wall_us = t1 - t0;
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    return rc;
+}

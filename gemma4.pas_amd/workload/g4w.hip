@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "g4w.h"
+#include "g4w_api.h"
 
 #define G4W_API extern "C" __attribute__((visibility("default")))
 

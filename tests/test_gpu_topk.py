@@ -156,14 +156,20 @@ def test_small_vocab_random(orc, vocab):
             rows[r] = np.sort(rng.integers(0, 50, vocab)).astype(F32)
     k = np.array([rng.choice([1, 2, min(5, vocab - 1), min(64, vocab - 1), vocab - 1,
                               min(1024, vocab - 1)]) for _ in range(B)], np.int32)
-    k = np.clip(k, 1, vocab - 1)
+    k = np.clip(k, 1, min(vocab - 1, native.max_top_k()))
     t = rng.choice([0.0, 0.7, 1.0, 1.3], B).astype(F32)
     p = rng.choice([0.0, 0.5, 0.95, 1.0], B).astype(F32)
     u = np.floor(rng.random(B) * 2**32) / 2**32
-    d = hip.Buffer.from_array(rows)
+    # rows padded to a 16-byte stride; the padding holds values that would win
+    # every selection if the kernel read past `vocab`
+    stride = (vocab + 3) // 4 * 4
+    padded = np.full((B, stride), 1e30, F32)
+    padded[:, :vocab] = rows
+    d = hip.Buffer.from_array(padded)
     cap = int(k.max())
     outs = native.DeviceOutputs(B, cap)
-    rc, ids = s.sample(d, B, _params(t, k, p), u, outputs=outs.struct, check=False)
+    rc, ids = s.sample(d, B, _params(t, k, p), u, row_stride=stride, outputs=outs.struct,
+                       check=False)
     o = outs.read()
     empty = [r for r in range(B) if not np.any(rows[r] > F32(-1e30))]
     if empty:
