@@ -55,6 +55,7 @@ def harness():
                               ctypes.c_float)
     H.g4h_decode_latency.argtypes = [vp, vp, vp, u64, i32, i32, i32, i32, f32, i32, f32, i32,
                                      vp, vp, vp]
+    H.g4h_null_roundtrip.argtypes = [vp, i32, i32, vp]
     H.g4h_batch_throughput.argtypes = [vp, vp, vp, i32, i64, i32, vp, vp, i32, i32, vp, i32,
                                        i32, vp, vp, vp]
     return H
@@ -157,6 +158,16 @@ def main():
         raise RuntimeError("no HIP device: the sampler has no CPU path")
     stream = hip.Stream()
     threads = min(16, os.cpu_count() or 1)
+
+    # ---- host floor of a synchronous single-kernel call --------------------
+    floor = {}
+    for mode, name in ((0, "launch_sync_p50_us"), (1, "launch_spin_p50_us")):
+        us = np.zeros(2000)
+        rc = H.g4h_null_roundtrip(stream.handle, len(us), mode, _vp(us))
+        if rc != 0:
+            raise RuntimeError(f"g4h_null_roundtrip mode {mode} failed: {rc}")
+        floor[name] = pct(us[200:], 50)
+    log(f"null-kernel round trip: {floor}")
 
     # ---- B=1 decode stream (headline) -------------------------------------
     log(f"decode stream: warmup {args.warmup} rows, timed {args.steps} rows (sync API)")
@@ -262,6 +273,7 @@ def main():
         "gpu_event_p50_us": pct(gpu_us, 50),
         "async_readback_p50_us": pct(a_host, 50),
         "id_mismatches": bad + bad_async,
+        "null_kernel_roundtrip": floor,
         "roofline": {"bound": "hbm", "kernel": "topk_kernel (B=1)", "achieved": achieved,
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": None, "kernel_us_mean": k_mean, "kernel_us_median": k_med,

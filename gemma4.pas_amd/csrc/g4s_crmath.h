@@ -28,8 +28,10 @@
 
 #if defined(__HIPCC__)
 #define G4S_HD __host__ __device__ __forceinline__
+#define G4S_HD_COLD static __host__ __device__ __attribute__((noinline, cold))
 #else
 #define G4S_HD static inline
+#define G4S_HD_COLD static __attribute__((noinline, cold))
 #endif
 
 namespace g4s {
@@ -260,6 +262,15 @@ G4S_HD dd expm1_dd(dd x)
     return dd_mul(s, x);
 }
 
+/* The double-double evaluations below run only when the binary64 result
+ * lies too close to a binary32 rounding midpoint (a few times in 2^20): they
+ * are kept out of line so the fast paths stay small. */
+G4S_HD_COLD float exp_cr32_slow(double xh, double xl)
+{
+    dd e = exp_dd(xh, xl);
+    return round_dd_f32(e.hi, e.lo);
+}
+
 /* RN32(e^(xh + xl)), |xl| <= ulp(xh). */
 G4S_HD float exp_cr32(double xh, double xl)
 {
@@ -269,8 +280,7 @@ G4S_HD float exp_cr32(double xh, double xl)
     double y = exp_fast_d(xh);
     y = fma_d(y, xl, y);
     if (rounding_safe(y, 8, 0x1p-50)) return (float)y; /* eps = 2^-50 */
-    dd e = exp_dd(xh, xl);
-    return round_dd_f32(e.hi, e.lo);
+    return exp_cr32_slow(xh, xl);
 }
 
 /* RN32(e^(a - b)) for binary32 a, b with the difference taken exactly
@@ -337,6 +347,14 @@ G4S_HD dd tanh_dd(dd w)
     return neg ? dd_neg(t) : t;
 }
 
+/* RN32(c * tanh(wh + wl)) in double-double (out of line, rare). */
+G4S_HD_COLD float tanh_scaled_cr32_slow(double wh, double wl, double c)
+{
+    dd tt = tanh_dd(dd{wh, wl});
+    dd yy = dd_mul_d(tt, c);
+    return round_dd_f32(yy.hi, yy.lo);
+}
+
 /* RN32(cap * tanh(x / cap)) with the quotient exact: the top-k softcap
  * `LCap * Tanh(LVals[LI] / LCap)` (Model.pas:2776).  cap > 0. */
 G4S_HD float softcap_topk_cr32(float x, float cap)
@@ -349,9 +367,7 @@ G4S_HD float softcap_topk_cr32(float x, float cap)
     double t = tanh_fast_d(wh);
     double y = cd * fma_d(wl, fma_d(-t, t, 1.0), t);
     if (rounding_safe(y, 16, 0x1p-49)) return (float)y; /* eps = 2^-49 */
-    dd tt = tanh_dd(dd{wh, wl});
-    dd yy = dd_mul_d(tt, cd);
-    return round_dd_f32(yy.hi, yy.lo);
+    return tanh_scaled_cr32_slow(wh, wl, cd);
 }
 
 /* RN32(tanh(x * inv_cap) * cap), inv_cap = fl32(1/cap): the full-vocabulary
@@ -365,9 +381,7 @@ G4S_HD float softcap_full_cr32(float x, float inv_cap, float cap)
     double t = tanh_fast_d(w);
     double y = t * (double)cap;
     if (rounding_safe(y, 16, 0x1p-49)) return (float)y;
-    dd tt = tanh_dd(dd{w, 0.0});
-    dd yy = dd_mul_d(tt, (double)cap);
-    return round_dd_f32(yy.hi, yy.lo);
+    return tanh_scaled_cr32_slow(w, 0.0, (double)cap);
 }
 
 /* RN32(u * p) for binary64 u and binary32 p (`Random * TopP`, Model.pas:2813). */

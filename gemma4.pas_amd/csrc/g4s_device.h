@@ -90,53 +90,131 @@ __device__ __forceinline__ void load_vec(const char* row, int64_t e0, int64_t li
     }
 }
 
+/* Load VW consecutive in-bounds elements starting at e0 (a multiple of VW):
+ * one unconditional 16-byte load. */
+template <int DT>
+__device__ __forceinline__ void load_vec_full(const char* row, int64_t e0, float (&v)[Elem<DT>::VW])
+{
+    const uint4 q = *reinterpret_cast<const uint4*>(row + e0 * Elem<DT>::SIZE);
+    if constexpr (DT == 0) {
+        v[0] = __uint_as_float(q.x);
+        v[1] = __uint_as_float(q.y);
+        v[2] = __uint_as_float(q.z);
+        v[3] = __uint_as_float(q.w);
+    } else {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+    }
+}
+
+/* Publish a row's completion for a host that spins on `done` instead of
+ * synchronizing the stream: every store the calling wave made before this
+ * point is visible to the host before done[row] reads `seq`.  Called by all
+ * lanes of the wave that wrote the row's outputs (lane 0 stores the word). */
+__device__ __forceinline__ void publish_done(uint32_t* done, int row, uint32_t seq)
+{
+    if (!done) return;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+    if ((threadIdx.x & 63) == 0)
+        __hip_atomic_store(done + row, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 /* ------------------------------------------------------------ wave helpers */
+
+/* Cross-lane steps on DPP (no LDS crossbar).  A wave64 inclusive scan is
+ * row_shr 1,2,4,8 inside each 16-lane row, then row_bcast 15 and 31 across
+ * rows; a lane without a source keeps the identity `id`. */
+#define G4S_DPP_STEP(x, OP, id, T, ctrl, rmask) \
+    x = OP(x, (T)__builtin_amdgcn_update_dpp((int)(id), (int)(x), ctrl, rmask, 0xf, false))
+#define G4S_DPP_SCAN(x, OP, id, T)                 \
+    do {                                           \
+        G4S_DPP_STEP(x, OP, id, T, 0x111, 0xf);    \
+        G4S_DPP_STEP(x, OP, id, T, 0x112, 0xf);    \
+        G4S_DPP_STEP(x, OP, id, T, 0x114, 0xf);    \
+        G4S_DPP_STEP(x, OP, id, T, 0x118, 0xf);    \
+        G4S_DPP_STEP(x, OP, id, T, 0x142, 0xa);    \
+        G4S_DPP_STEP(x, OP, id, T, 0x143, 0xc);    \
+    } while (0)
+
+__device__ __forceinline__ int g4s_add_i(int a, int b) { return a + b; }
+__device__ __forceinline__ uint32_t g4s_max_u(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t g4s_min_u(uint32_t a, uint32_t b) { return a < b ? a : b; }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-template <typename T>
-__device__ __forceinline__ T wave_bcast(T v, int src)
+/* Inclusive prefix sum over the 64 lanes of a wave (all lanes active). */
+__device__ __forceinline__ int wave_inclusive_scan(int v)
 {
-    return __shfl(v, src, 64);
+    G4S_DPP_SCAN(v, g4s_add_i, 0, int);
+    return v;
 }
 
+/* Wave-uniform reductions (all lanes active): the last lane of the scan. */
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint32_t w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
+    G4S_DPP_SCAN(v, g4s_max_u, 0u, uint32_t);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint32_t w = __shfl_xor(v, o, 64);
-        v = w < v ? w : v;
-    }
-    return v;
+    G4S_DPP_SCAN(v, g4s_min_u, 0xFFFFFFFFu, uint32_t);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 __device__ __forceinline__ int wave_sum_i32(int v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    G4S_DPP_SCAN(v, g4s_add_i, 0, int);
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
-/* k-th largest (1 <= k <= 64) of one uint32 per lane, all 64 lanes active:
- * MSB-first binary search with ballot counts; uniform result. */
-__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k)
+/* The k1-th and k2-th largest (1 <= k <= 64; 0 for k outside that range) of
+ * one uint32 per lane (all 64 lanes active), in one MSB-first ballot
+ * search.  Each result P is the largest value with #{lanes: v >= P} >= k
+ * (0 when no positive value qualifies); uniform. */
+__device__ __forceinline__ void wave_kth_largest2(uint32_t v, int k1, int k2, uint32_t& r1,
+                                                  uint32_t& r2)
 {
-    uint32_t prefix = 0;
-#pragma unroll
+    uint32_t p1 = 0, p2 = 0;
+    const bool on1 = k1 >= 1 && k1 <= 64, on2 = k2 >= 1 && k2 <= 64;
+#pragma unroll 4
     for (int bit = 31; bit >= 0; --bit) {
-        uint32_t cand = prefix | (1u << bit);
-        uint64_t m = __ballot(v >= cand);
-        if (__popcll(m) >= k) prefix = cand;
+        const uint32_t c1 = p1 | (1u << bit), c2 = p2 | (1u << bit);
+        const int n1 = __popcll(__ballot(v >= c1));
+        const int n2 = __popcll(__ballot(v >= c2));
+        if (n1 >= k1) p1 = c1;
+        if (n2 >= k2) p2 = c2;
     }
-    return prefix;
+    r1 = on1 ? p1 : 0u;
+    r2 = on2 ? p2 : 0u;
+}
+
+/* k-th largest key (1 <= k <= 64*NG) over NG keys per lane of one wave,
+ * zero keys ignored (all 64 lanes active), by an MSB-first ballot search;
+ * *gt / *eq = how many keys are above / equal to it.  Uniform results. */
+template <int NG>
+__device__ __forceinline__ uint32_t wave_select_kth(const uint32_t (&v)[NG], int k, int* gt,
+                                                    int* eq)
+{
+    uint32_t p = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = p | (1u << bit);
+        int n = 0;
+#pragma unroll
+        for (int q = 0; q < NG; ++q) n += __popcll(__ballot(v[q] >= c));
+        if (n >= k) p = c;
+    }
+    int g = 0, e = 0;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        g += __popcll(__ballot(v[q] > p));
+        e += __popcll(__ballot(v[q] == p && v[q] != 0u));
+    }
+    *gt = g;
+    *eq = e;
+    return p;
 }
 
 /* Block-wide exclusive prefix sum in thread order; `total` receives the sum.
@@ -145,18 +223,13 @@ template <int BLOCK>
 __device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int& total)
 {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
+    const int x = wave_inclusive_scan(v);
     if (lane == 63) s_wave[wid] = x;
     __syncthreads();
     int off = 0, tot = 0;
 #pragma unroll
     for (int w = 0; w < BLOCK / 64; ++w) {
-        int t = s_wave[w];
+        const int t = s_wave[w];
         off += (w < wid) ? t : 0;
         tot += t;
     }
@@ -223,12 +296,7 @@ __device__ __forceinline__ void radix_digit_step(int k, const uint32_t* s_hist, 
             c[q] = (int)s_hist[255 - (lane * 4 + q)];
             lsum += c[q];
         }
-        int incl = lsum;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
+        const int incl = wave_inclusive_scan(lsum);
         int run = incl - lsum;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {

@@ -10,6 +10,7 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -36,23 +37,21 @@ struct g4s_sampler {
     std::string err;
 
     /* top-k path workspace */
-    uint32_t* cand_key = nullptr;
-    uint32_t* cand_idx = nullptr;
-    uint32_t* merge_key = nullptr;
-    uint32_t* merge_idx = nullptr;
+    uint64_t* cand = nullptr;
+    uint64_t* merge = nullptr;
     g4s::ChunkRec* recs = nullptr;
     uint32_t* tickets = nullptr;
     /* full path workspace */
     g4s::FullWorkspace full{};
     /* per-call staging */
-    int32_t* d_ids = nullptr;
     g4s_params* d_params = nullptr;
     double* d_u = nullptr;
     g4s_params* h_params = nullptr; /* pinned */
     double* h_u = nullptr;          /* pinned */
     int32_t* h_ids = nullptr;       /* pinned */
     uint32_t* h_flags = nullptr;    /* pinned */
-    uint32_t* d_flags = nullptr;
+    uint32_t* h_done = nullptr;     /* pinned, coherent: per-row completion words */
+    uint32_t seq = 0;               /* last completion value handed to a launch */
 };
 
 namespace {
@@ -84,21 +83,18 @@ void release(g4s_sampler* s)
     auto fh = [](void* p) {
         if (p) (void)hipHostFree(p);
     };
-    f(s->cand_key);
-    f(s->cand_idx);
-    f(s->merge_key);
-    f(s->merge_idx);
+    f(s->cand);
+    f(s->merge);
     f(s->recs);
     f(s->tickets);
     g4s::full_free(s->full);
-    f(s->d_ids);
     f(s->d_params);
     f(s->d_u);
-    f(s->d_flags);
     fh(s->h_params);
     fh(s->h_u);
     fh(s->h_ids);
     fh(s->h_flags);
+    fh(s->h_done);
 }
 
 bool is_topk_row(const g4s_params& p, int32_t vocab) { return p.top_k >= 1 && p.top_k < vocab; }
@@ -127,7 +123,8 @@ int check_logits(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t ro
  * (or inline p0/u0 when d_params is NULL). */
 int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride, int32_t batch,
             const g4s_params* d_params, const double* d_u, const g4s_params* p0, double u0,
-            int32_t kbound, bool full_rows, int32_t* d_ids, const g4s_outputs* outputs)
+            int32_t kbound, bool full_rows, int32_t* d_ids, const g4s_outputs* outputs,
+            uint32_t* done = nullptr, uint32_t seq = 0)
 {
     g4s_outputs out{};
     if (outputs) out = *outputs;
@@ -146,16 +143,16 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         if (p0) a.p0 = *p0;
         a.u0 = u0;
         a.splits = cfg.splits;
-        a.cap_c = cfg.cap_c;
+        a.cap_log2 = cfg.cap_log2;
         a.kbound = kbound;
         a.softcap = s->softcap;
-        a.cand_key = s->cand_key;
-        a.cand_idx = s->cand_idx;
-        a.merge_key = s->merge_key;
-        a.merge_idx = s->merge_idx;
+        a.cand = s->cand;
+        a.merge = s->merge;
         a.recs = s->recs;
         a.tickets = s->tickets;
         a.ids = d_ids;
+        a.done = done;
+        a.seq = seq;
         a.out = out;
         hipError_t e = g4s::topk_launch(cfg, a, dtype, s->stream);
         if (e != hipSuccess) return hip_fail(s, e, "top-k kernel launch");
@@ -242,20 +239,19 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
     auto hm = [&](void** p, size_t bytes) {
         if (ok && hipHostMalloc(p, bytes, hipHostMallocDefault) != hipSuccess) ok = false;
     };
-    dm((void**)&s->cand_key, mb * g4s::kCandRow * sizeof(uint32_t));
-    dm((void**)&s->cand_idx, mb * g4s::kCandRow * sizeof(uint32_t));
-    dm((void**)&s->merge_key, mb * g4s::kCandRow * sizeof(uint32_t));
-    dm((void**)&s->merge_idx, mb * g4s::kCandRow * sizeof(uint32_t));
+    dm((void**)&s->cand, mb * g4s::kCandRow * sizeof(uint64_t));
+    dm((void**)&s->merge, mb * g4s::kCandRow * sizeof(uint64_t));
     dm((void**)&s->recs, mb * g4s::kMaxSplits * sizeof(g4s::ChunkRec));
     dm((void**)&s->tickets, mb * sizeof(uint32_t));
-    dm((void**)&s->d_ids, mb * sizeof(int32_t));
     dm((void**)&s->d_params, mb * sizeof(g4s_params));
     dm((void**)&s->d_u, mb * sizeof(double));
-    dm((void**)&s->d_flags, mb * sizeof(uint32_t));
     hm((void**)&s->h_params, mb * sizeof(g4s_params));
     hm((void**)&s->h_u, mb * sizeof(double));
     hm((void**)&s->h_ids, mb * sizeof(int32_t));
     hm((void**)&s->h_flags, mb * sizeof(uint32_t));
+    if (ok && hipHostMalloc((void**)&s->h_done, mb * sizeof(uint32_t), hipHostMallocCoherent) !=
+                  hipSuccess)
+        ok = false;
     if (ok && g4s::full_alloc(s->full, vocab, max_batch) != hipSuccess) ok = false;
     if (!ok) {
         release(s);
@@ -316,18 +312,24 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
     g4s_outputs out{};
     if (outputs) out = *outputs;
     /* ids (and flags, unless the caller wants them on the device) are written
-     * by the kernel straight into this handle's pinned host buffers: the
-     * synchronous call needs no copy after the kernel, only the stream sync. */
+     * by the kernel straight into this handle's pinned host buffers, and each
+     * row then publishes a completion word: the synchronous call spins on
+     * those words instead of synchronizing the stream, and needs no copy
+     * after the kernel. */
     uint32_t* user_flags = out.flags;
+    if (++s->seq == 0) s->seq = 1;
+    const uint32_t seq = s->seq;
     for (int32_t r = 0; r < batch; ++r) {
         s->h_ids[r] = -1;
         s->h_flags[r] = 0u;
     }
     if (!user_flags) out.flags = s->h_flags;
+    /* rows of the full-vocabulary path do not publish completion words */
+    uint32_t* done = (!user_flags && !full_rows) ? s->h_done : nullptr;
 
     if (batch == 1) {
         rc = enqueue(s, d_logits, dtype, row_stride, 1, nullptr, nullptr, &params[0], u[0], kbound,
-                     full_rows, s->h_ids, &out);
+                     full_rows, s->h_ids, &out, done, seq);
     } else {
         std::memcpy(s->h_params, params, sizeof(g4s_params) * batch);
         std::memcpy(s->h_u, u, sizeof(double) * batch);
@@ -338,15 +340,33 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
                                s->stream);
         if (e != hipSuccess) return hip_fail(s, e, "parameter upload");
         rc = enqueue(s, d_logits, dtype, row_stride, batch, s->d_params, s->d_u, nullptr, 0.0,
-                     kbound, full_rows, s->h_ids, &out);
+                     kbound, full_rows, s->h_ids, &out, done, seq);
     }
     if (rc) return rc;
     hipError_t e = hipSuccess;
-    if (user_flags)
-        e = hipMemcpyAsync(s->h_flags, user_flags, sizeof(uint32_t) * batch, hipMemcpyDeviceToHost,
-                           s->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
-    if (e != hipSuccess) return hip_fail(s, e, "sampling");
+    bool published = false;
+    if (done) {
+        /* bounded spin (about a second), then the stream decides */
+        const auto t0 = std::chrono::steady_clock::now();
+        for (uint64_t spin = 0;; ++spin) {
+            int32_t r = 0;
+            while (r < batch && __atomic_load_n(&s->h_done[r], __ATOMIC_ACQUIRE) == seq) ++r;
+            if (r == batch) {
+                published = true;
+                break;
+            }
+            if ((spin & 1023u) == 1023u &&
+                std::chrono::steady_clock::now() - t0 > std::chrono::seconds(1))
+                break;
+        }
+    }
+    if (!published) {
+        if (user_flags)
+            e = hipMemcpyAsync(s->h_flags, user_flags, sizeof(uint32_t) * batch,
+                               hipMemcpyDeviceToHost, s->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) return hip_fail(s, e, "sampling");
+    }
     std::memcpy(ids, s->h_ids, sizeof(int32_t) * batch);
     for (int32_t r = 0; r < batch; ++r)
         if (s->h_flags[r] & G4S_FLAG_EMPTY)

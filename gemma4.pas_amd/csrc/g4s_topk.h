@@ -16,6 +16,14 @@ struct ChunkRec {
     uint32_t mode_e; /* bit 31: exact select; bits 0-30: copies of the K-th key in the chunk */
 };
 
+/* A candidate: order-preserving key in the high word, vocab index in the low word. */
+__host__ __device__ inline uint64_t cand_pack(uint32_t key, uint32_t idx)
+{
+    return ((uint64_t)key << 32) | idx;
+}
+__host__ __device__ inline uint32_t cand_key_of(uint64_t c) { return (uint32_t)(c >> 32); }
+__host__ __device__ inline uint32_t cand_idx_of(uint64_t c) { return (uint32_t)c; }
+
 struct TopkArgs {
     const void* logits;
     int64_t row_stride; /* elements */
@@ -26,21 +34,21 @@ struct TopkArgs {
     g4s_params p0;
     double u0;
     int32_t splits;
-    int32_t cap_c;  /* candidate slots per chunk (2 * kbound) */
-    int32_t kbound; /* every top-k row has TopK <= kbound */
+    int32_t cap_log2; /* candidate slots per chunk = 1 << cap_log2 (>= 2 * kbound) */
+    int32_t kbound;   /* every top-k row has TopK <= kbound */
     float softcap;
-    uint32_t* cand_key; /* [batch][kCandRow] */
-    uint32_t* cand_idx;
-    uint32_t* merge_key; /* [batch][kCandRow] merge scratch when candidates exceed LDS */
-    uint32_t* merge_idx;
-    ChunkRec* recs;     /* [batch][kMaxSplits] */
-    uint32_t* tickets;  /* [batch], zero between launches */
-    int32_t* ids;       /* device [batch] */
+    uint64_t* cand;   /* [batch][kCandRow] chunk candidates */
+    uint64_t* merge;  /* [batch][kCandRow] merge candidates beyond what LDS holds */
+    ChunkRec* recs;   /* [batch][kMaxSplits] */
+    uint32_t* tickets; /* [batch], zero between launches */
+    int32_t* ids;      /* [batch] (device or host-pinned) */
+    uint32_t* done;    /* [batch] host-pinned completion words, or NULL */
+    uint32_t seq;      /* value written to done[row] once the row's outputs are visible */
     g4s_outputs out;
 };
 
 struct TopkConfig {
-    int block, items, chunk, splits, cap_c;
+    int block, items, chunk, splits, cap_log2;
     bool ok;
 };
 

@@ -2,29 +2,36 @@
  * g4s_topk.hip -- the top-k sampling path on gfx950 (rows with 0 < TopK < V).
  *
  * Replaces DoSelectTopKIndices + the top-k branch of DoSample
- * (src/Gemma4.Model.pas:2615-2689, 2765-2826).  One kernel launch per batch:
+ * (src/Gemma4.Model.pas:2615-2689, 2765-2826).  One kernel launch per batch,
+ * grid = splits x rows, one workgroup per vocabulary chunk:
  *
- *  phase 1 (grid = splits x rows, one workgroup per vocabulary chunk)
+ *  phase 1 (every workgroup)
  *    - 16-byte loads of the chunk into registers as order-preserving keys;
  *    - a provable lower bound theta of the chunk's K-th largest key: each
- *      wave takes the ceil(K/waves)-th largest of its per-thread maxima
- *      (ballot binary search) and the block keeps the minimum;
- *    - every key >= theta is a candidate (a superset of the chunk's top-K);
- *      if more than 2K qualify (heavy ties), an exact per-chunk radix select
- *      emits the keys above the chunk's K-th value plus its first K copies
- *      in index order;
- *    - rc = the ceil(K/splits)-th largest key of the chunk: min over chunks
- *      of rc is a second lower bound of the row's K-th largest;
- *    - candidates and the chunk record go to the HBM workspace, then an
- *      atomic ticket elects the last workgroup of the row.
+ *      wave takes the ceil(K/waves)-th largest of its 64 thread maxima
+ *      (ballot binary search; distinct threads, so the wave holds at least
+ *      that many keys >= its value) and the block keeps the minimum;
+ *    - every key >= theta is a candidate (a superset of the chunk's top-K),
+ *      written straight to the chunk's HBM slots by wave-level compaction;
+ *      if more than the chunk's slot count qualify (heavy ties), an exact
+ *      per-chunk radix select emits the keys above the chunk's K-th value
+ *      plus its first K copies in index order;
+ *    - rc, a value the chunk holds at least ceil(K/splits) keys >= (the
+ *      largest over waves of that order statistic of the thread maxima):
+ *      min over chunks of rc is a second lower bound of the row's K-th
+ *      largest;
+ *    - an atomic ticket elects the last workgroup of the row.
  *  merge + tail (last workgroup of each row)
- *    - keeps candidates >= max(bounds) (typically ~K..2K of them), selects
- *      the exact K-th value tau, resolves ties at tau like the reference's
- *      min-heap (lowest index when the heap layout cannot matter, a full
- *      heap replay otherwise), sorts the survivors by vocab index;
- *    - wave 0 runs the reference's tail in index order: softcap, 1/T,
- *      max, exp, sequential binary32 LSum, division, argmax, sequential
- *      running sum against fl32(u*TopP).
+ *    - loads every chunk record and candidate slot of the row with
+ *      independent loads (one memory round trip), keeps candidates
+ *      >= max(max bound, min rc), selects the exact K-th value tau,
+ *      resolves ties at tau like the reference's min-heap (lowest index when
+ *      the heap layout cannot matter, a full heap replay otherwise), and
+ *      sorts the survivors by vocab index;
+ *    - wave 0 runs the reference's tail in index order: softcap, 1/T, max,
+ *      exp, sequential binary32 LSum, division, argmax, sequential running
+ *      sum against fl32(u*TopP).  The sequential sums are exact left-to-right
+ *      binary32 chains (one readlane per term).
  */
 #include "g4s_topk.h"
 
@@ -34,53 +41,54 @@ using namespace g4s::cr;
 
 namespace {
 
+constexpr int kBatchLoads = 16; /* candidate slots one merge thread loads per round */
+
 struct TopkShared {
-    /* phase 1 */
     uint32_t wtheta[16];
     int scan[16];
-    uint32_t red[16];
-    int misc[8];
-    uint32_t hist[256];
-    /* merge */
-    ChunkRec rec[kMaxSplits];
-    uint32_t mkey[kMergeLds]; /* phase-1 emission buffer, then merge candidates */
-    uint32_t midx[kMergeLds];
-    uint32_t skey[kMaxTopK]; /* survivors (unsorted), heap values during a replay */
-    int32_t sidx[kMaxTopK];
-    uint32_t tkey[kMaxTopK]; /* survivors sorted by index */
-    int32_t tidx[kMaxTopK];
-    float val[kMaxTopK];     /* tail: v, then e, then p */
-    float prob[kMaxTopK];
+    uint32_t red[48];
+    int misc[8]; /* [0..3] counters and flags (see the kernel), [4..6] select results */
     int flag_last;
+    uint32_t hist[256];
+    ChunkRec rec[kMaxSplits];
+    uint64_t mc[kMergeLds];     /* phase-1 emission, then merge candidates, then replay tiles */
+    uint64_t surv[kMaxTopK];    /* survivors (unsorted); min-heap storage during a replay */
+    uint64_t sorted[kMaxTopK];  /* survivors ascending by vocab index */
+    float val[kMaxTopK];        /* tail: v, then e */
+    float prob[kMaxTopK];
 };
+
+__device__ __forceinline__ float lane_f(float x, int l)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
 
 /* ------------------------------------------------------------ heap replay */
 
 /* Exact replay of the reference's min-heap pass (Model.pas:2632-2664) over a
  * whole row, for rows whose K-th value is tied in a way the heap layout
  * decides.  Elements are screened in tiles against the current root; the
- * screened ones (in index order) are inserted by one lane.  Returns the heap
- * size in use (entries with index >= 0 are the survivors). */
+ * screened ones (in index order) are inserted by one lane.  On return
+ * hv[0..K) / hi[0..K) hold the heap. */
 template <int BLOCK, int DT>
-__device__ int heap_replay(const char* row, int vocab, int K, TopkShared& sh)
+__device__ void heap_replay(const char* row, int vocab, int K, TopkShared& sh, float* hv,
+                            int32_t* hi)
 {
-    float* hv = reinterpret_cast<float*>(sh.skey);
-    int32_t* hi = sh.sidx;
-    float* qv = reinterpret_cast<float*>(sh.mkey);
-    int32_t* qi = reinterpret_cast<int32_t*>(sh.midx);
+    float* qv = reinterpret_cast<float*>(sh.mc);
+    int32_t* qi = reinterpret_cast<int32_t*>(sh.mc) + kMergeLds;
     const int tid = threadIdx.x;
     for (int i = tid; i < K; i += BLOCK) {
-        hv[i] = -1e30f;
+        hv[i] = -1e30f; /* :2634-2638 */
         hi[i] = -1;
     }
     __syncthreads();
     for (int base = 0; base < vocab; base += BLOCK) {
-        int e = base + tid;
-        float x = (e < vocab) ? load_elem<DT>(row, e) : 0.0f;
-        float root = hv[0];
-        int take = (e < vocab) && !(x <= root);
+        const int e = base + tid;
+        const float x = (e < vocab) ? load_elem<DT>(row, e) : 0.0f;
+        const float root = hv[0];
+        const int take = (e < vocab) && !(x <= root);
         int total;
-        int pos = block_exclusive_scan<BLOCK>(take, sh.scan, total);
+        const int pos = block_exclusive_scan<BLOCK>(take, sh.scan, total);
         if (take) {
             qv[pos] = x;
             qi[pos] = e;
@@ -88,7 +96,7 @@ __device__ int heap_replay(const char* row, int vocab, int K, TopkShared& sh)
         __syncthreads();
         if (tid == 0) {
             for (int q = 0; q < total; ++q) {
-                float v = qv[q];
+                const float v = qv[q];
                 if (v <= hv[0]) continue; /* :2643-2644 */
                 int p = 0;
                 for (;;) { /* :2647-2661 */
@@ -106,19 +114,30 @@ __device__ int heap_replay(const char* row, int vocab, int K, TopkShared& sh)
         }
         __syncthreads();
     }
-    return K;
 }
 
-/* Rank-by-count k-th largest over an LDS/global array (n <= kRankMax). */
+/* Rank-by-count k-th largest of key(i), i in [0, n) (n <= kRankMax).  The
+ * inner scan reads eight keys per step so the LDS loads overlap. */
 template <int BLOCK, typename KeyF>
 __device__ uint32_t rank_kth(int n, int k, KeyF key, int* s_misc, int* gt, int* eq)
 {
     const int tid = threadIdx.x;
     for (int i = tid; i < n; i += BLOCK) {
-        uint32_t ki = key(i);
+        const uint32_t ki = key(i);
         int g = 0, q = 0;
-        for (int j = 0; j < n; ++j) {
-            uint32_t kj = key(j);
+        int j = 0;
+        for (; j + 8 <= n; j += 8) {
+            uint32_t kk[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) kk[t] = key(j + t);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                g += kk[t] > ki;
+                q += kk[t] == ki;
+            }
+        }
+        for (; j < n; ++j) {
+            const uint32_t kj = key(j);
             g += kj > ki;
             q += kj == ki;
         }
@@ -129,11 +148,19 @@ __device__ uint32_t rank_kth(int n, int k, KeyF key, int* s_misc, int* gt, int* 
         }
     }
     __syncthreads();
-    uint32_t r = (uint32_t)s_misc[4];
+    const uint32_t r = (uint32_t)s_misc[4];
     *gt = s_misc[5];
     *eq = s_misc[6];
     __syncthreads();
     return r;
+}
+
+template <int BLOCK, typename KeyF>
+__device__ uint32_t select_kth(int n, int k, KeyF key, TopkShared& sh, int* gt, int* eq)
+{
+    if (n <= kRankMax) return rank_kth<BLOCK>(n, k, key, sh.misc, gt, eq);
+    return block_radix_kth<BLOCK>(n, k, key, [](int) { return true; }, sh.hist, sh.misc + 4, gt,
+                                  eq);
 }
 
 }  // namespace
@@ -145,6 +172,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     constexpr int NV = ITEMS / VW;
     constexpr int NW = BLOCK / 64;
     constexpr int CHUNK = BLOCK * ITEMS;
+    static_assert(BLOCK >= kMaxSplits, "one merge thread per chunk record");
     __shared__ TopkShared sh;
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -158,9 +186,12 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     const int K = rp.top_k;
     if (!(K >= 1 && K < V)) return; /* full-vocabulary row (Model.pas:2756) */
     if (K > a.kbound) {
-        if (chunk == 0 && tid == 0) {
-            a.ids[row] = -1;
-            if (a.out.flags) a.out.flags[row] = G4S_FLAG_ERROR | G4S_FLAG_TOPK_PATH;
+        if (chunk == 0 && wid == 0) {
+            if (lane == 0) {
+                a.ids[row] = -1;
+                if (a.out.flags) a.out.flags[row] = G4S_FLAG_ERROR | G4S_FLAG_TOPK_PATH;
+            }
+            publish_done(a.done, row, a.seq);
         }
         return;
     }
@@ -168,61 +199,101 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     const char* rowp = reinterpret_cast<const char*>(a.logits) +
                        (int64_t)row * a.row_stride * Elem<DT>::SIZE;
     const int64_t cbase = (int64_t)chunk * CHUNK;
-    const int cap_c = a.cap_c;
-    uint32_t* gkey = a.cand_key + (int64_t)row * kCandRow + (int64_t)chunk * cap_c;
-    uint32_t* gidx = a.cand_idx + (int64_t)row * kCandRow + (int64_t)chunk * cap_c;
+    const int cap = 1 << a.cap_log2;
+    uint64_t* gcand = a.cand + (int64_t)row * kCandRow + ((int64_t)chunk << a.cap_log2);
+    if (tid == 0) {
+        sh.misc[0] = 0; /* emission counter */
+        sh.misc[1] = 0; /* merge counter */
+        sh.misc[2] = 0; /* survivor counter */
+        sh.misc[3] = 0; /* K-th key tie flag */
+    }
 
     /* ------------------------------------------------------- phase 1 */
     uint32_t keys[ITEMS];
+    if (cbase + CHUNK <= V) {
+        /* whole chunk in bounds: independent unconditional 16-byte loads */
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        float v[VW];
-        int64_t e0 = cbase + ((int64_t)j * BLOCK + tid) * VW;
-        load_vec<DT>(rowp, e0, V, v);
+        for (int j = 0; j < NV; ++j) {
+            float v[VW];
+            load_vec_full<DT>(rowp, cbase + ((int64_t)j * BLOCK + tid) * VW, v);
 #pragma unroll
-        for (int q = 0; q < VW; ++q) keys[j * VW + q] = (e0 + q < V) ? cand_key(v[q]) : 0u;
+            for (int q = 0; q < VW; ++q) keys[j * VW + q] = cand_key(v[q]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            float v[VW];
+            const int64_t e0 = cbase + ((int64_t)j * BLOCK + tid) * VW;
+            load_vec<DT>(rowp, e0, V, v);
+#pragma unroll
+            for (int q = 0; q < VW; ++q) keys[j * VW + q] = (e0 + q < V) ? cand_key(v[q]) : 0u;
+        }
     }
     uint32_t tmax = 0;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) tmax = keys[i] > tmax ? keys[i] : tmax;
+    /* per wave: the ceil(K/waves)-th and the ceil(K/splits)-th largest of the
+     * 64 thread maxima (distinct elements, so the wave holds at least that
+     * many keys >= each value) */
     const int kw = (K + NW - 1) / NW;
-    uint32_t wth = (kw <= 64) ? wave_kth_largest(tmax, kw) : 0u;
-    if (lane == 0) sh.wtheta[wid] = wth;
+    const int m = (K + S - 1) / S;
+    uint32_t wth, wrc;
+    wave_kth_largest2(tmax, kw, m, wth, wrc);
+    if (lane == 0) {
+        sh.wtheta[wid] = wth;
+        sh.red[wid] = wrc;
+    }
     __syncthreads();
-    uint32_t theta = 0xFFFFFFFFu;
+    /* theta: every wave has >= kw keys >= theta, so the chunk has >= K;
+     * rc: some wave has >= m keys >= rc */
+    uint32_t theta = 0xFFFFFFFFu, rc = 0u;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) theta = sh.wtheta[w] < theta ? sh.wtheta[w] : theta;
+    for (int w = 0; w < NW; ++w) {
+        theta = sh.wtheta[w] < theta ? sh.wtheta[w] : theta;
+        rc = sh.red[w] > rc ? sh.red[w] : rc;
+    }
     theta = theta < 1u ? 1u : theta;
 
+    /* emit every key >= theta straight to the chunk's HBM slots: wave-level
+     * compaction, one LDS atomic per wave for the wave's base */
     int mine = 0;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) mine += keys[i] >= theta;
-    int total;
-    int off = block_exclusive_scan<BLOCK>(mine, sh.scan, total);
-
-    uint32_t rec_bound, rec_mode_e;
-    int emitted;
-    if (total <= cap_c) {
-        /* common case: every key >= theta is a candidate */
+    {
+        const int incl = wave_inclusive_scan(mine);
+        int base = 0;
+        if (lane == 63) base = atomicAdd(&sh.misc[0], incl);
+        base = __builtin_amdgcn_readlane(base, 63);
+        int pos = base + incl - mine;
 #pragma unroll
         for (int j = 0; j < NV; ++j)
 #pragma unroll
             for (int q = 0; q < VW; ++q) {
-                uint32_t k = keys[j * VW + q];
+                const uint32_t k = keys[j * VW + q];
                 if (k >= theta) {
-                    sh.mkey[off] = k;
-                    sh.midx[off] = (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q);
-                    ++off;
+                    if (pos < cap)
+                        gcand[pos] =
+                            cand_pack(k, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q));
+                    ++pos;
                 }
             }
-        emitted = total;
-        rec_bound = theta;
-        rec_mode_e = 0;
-    } else {
-        /* heavy ties or a weak theta: exact K-th largest of the chunk */
+    }
+    __syncthreads();
+    const int total = sh.misc[0];
+
+    uint32_t rec_bound = theta, rec_mode_e = 0;
+    int emitted = total;
+    if (total > cap) {
+        /* heavy ties or a weak theta: exact K-th largest of the chunk (the
+         * chunk holds more than cap >= 2K keys >= theta >= 1, so at least K).
+         * The slots are rewritten below: every wave's first-attempt stores
+         * complete before any rewrite is issued. */
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
         int gt_c, eq_c;
-        uint32_t tau_c = regs_radix_kth<BLOCK, ITEMS>(keys, K, sh.hist, sh.misc, &gt_c, &eq_c);
-        /* keys strictly above tau_c, any order */
+        const uint32_t tau_c =
+            regs_radix_kth<BLOCK, ITEMS>(keys, K, sh.hist, sh.misc + 4, &gt_c, &eq_c);
+        /* keys strictly above tau_c, any order (fewer than K of them) */
         int gmine = 0;
 #pragma unroll
         for (int i = 0; i < ITEMS; ++i) gmine += keys[i] > tau_c;
@@ -232,17 +303,16 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         for (int j = 0; j < NV; ++j)
 #pragma unroll
             for (int q = 0; q < VW; ++q) {
-                uint32_t k = keys[j * VW + q];
+                const uint32_t k = keys[j * VW + q];
                 if (k > tau_c) {
-                    sh.mkey[goff] = k;
-                    sh.midx[goff] = (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q);
+                    gcand[goff] = cand_pack(k, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q));
                     ++goff;
                 }
             }
         /* the first min(eq, K) copies of tau_c in index order: load slot j,
          * then thread, then position within the vector */
         const int want = eq_c < K ? eq_c : K;
-        int base = gtot;
+        const int base = gtot;
         int taken = 0;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
@@ -254,11 +324,9 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 #pragma unroll
             for (int q = 0; q < VW; ++q) {
                 if (keys[j * VW + q] == tau_c) {
-                    if (taken + r < want) {
-                        sh.mkey[base + taken + r] = tau_c;
-                        sh.midx[base + taken + r] =
-                            (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q);
-                    }
+                    if (taken + r < want)
+                        gcand[base + taken + r] = cand_pack(
+                            tau_c, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q));
                     ++r;
                 }
             }
@@ -267,24 +335,6 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         emitted = gtot + want;
         rec_bound = tau_c;
         rec_mode_e = 0x80000000u | (uint32_t)eq_c;
-    }
-    __syncthreads();
-
-    /* rc = m-th largest key of the chunk, m = ceil(K / splits) */
-    const int m = (K + S - 1) / S;
-    uint32_t rc = 0;
-    if (emitted >= m) {
-        int g, q;
-        if (emitted <= kRankMax)
-            rc = rank_kth<BLOCK>(emitted, m, [&](int i) { return sh.mkey[i]; }, sh.misc, &g, &q);
-        else
-            rc = block_radix_kth<BLOCK>(
-                emitted, m, [&](int i) { return sh.mkey[i]; }, [&](int) { return true; }, sh.hist,
-                sh.misc, &g, &q);
-    }
-    for (int i = tid; i < emitted; i += BLOCK) {
-        gkey[i] = sh.mkey[i];
-        gidx[i] = sh.midx[i];
     }
     if (tid == 0) {
         ChunkRec r;
@@ -296,252 +346,340 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     }
 
     /* ----------------------------------------------- last workgroup elects */
-    __threadfence();
+    /* release this chunk's slots and record; only the elected workgroup
+     * acquires (an acquire at agent scope invalidates the XCD's L2) */
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (tid == 0) {
-        uint32_t prev = atomicAdd(&a.tickets[row], 1u);
+        const uint32_t prev = atomicAdd(&a.tickets[row], 1u);
         sh.flag_last = (prev == (uint32_t)(S - 1));
     }
     __syncthreads();
     if (!sh.flag_last) return;
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) a.tickets[row] = 0u;
 
     /* ------------------------------------------------------------ merge */
     uint32_t flags = G4S_FLAG_TOPK_PATH;
-    uint32_t lb = 1u, lr = 0xFFFFFFFFu;
-    bool any_exact = false;
-    for (int c = tid; c < S; c += BLOCK) {
-        ChunkRec r = a.recs[(int64_t)row * kMaxSplits + c];
-        sh.rec[c] = r;
+    const uint64_t* rcand = a.cand + (int64_t)row * kCandRow;
+    uint64_t* gmerge = a.merge + (int64_t)row * kCandRow;
+    const int span = S << a.cap_log2;
+
+    /* one round trip: the chunk records and the first batch of slots (the
+     * index is clamped instead of branched on, so every load is issued) */
+    if (tid < S) sh.rec[tid] = a.recs[(int64_t)row * kMaxSplits + tid];
+    uint64_t v[kBatchLoads];
+#pragma unroll
+    for (int i = 0; i < kBatchLoads; ++i) {
+        const int f = tid + i * BLOCK;
+        v[i] = rcand[f < span ? f : span - 1];
     }
     __syncthreads();
+    uint32_t lb, lr;
+    bool any_exact;
     {
-        uint32_t mb = 1u, mr = 0xFFFFFFFFu;
-        int ex = 0;
-        for (int c = tid; c < S; c += BLOCK) {
-            mb = sh.rec[c].bound > mb ? sh.rec[c].bound : mb;
-            mr = sh.rec[c].rc < mr ? sh.rec[c].rc : mr;
-            ex |= (sh.rec[c].mode_e >> 31) != 0;
+        uint32_t mb = 1u, mr = 0xFFFFFFFFu, ex = 0u;
+        if (tid < S) {
+            const ChunkRec r = sh.rec[tid];
+            mb = r.bound > 1u ? r.bound : 1u;
+            mr = r.rc;
+            ex = r.mode_e >> 31;
         }
-        lb = block_max_u32<BLOCK>(mb, sh.red);
-        lr = block_min_u32<BLOCK>(mr, sh.red);
-        any_exact = block_sum_i32<BLOCK>(ex, sh.scan) != 0;
+        mb = wave_max_u32(mb);
+        mr = wave_min_u32(mr);
+        ex = wave_max_u32(ex);
+        if (lane == 0) {
+            sh.red[wid] = mb;
+            sh.red[16 + wid] = mr;
+            sh.red[32 + wid] = ex;
+        }
+        __syncthreads();
+        lb = 1u;
+        lr = 0xFFFFFFFFu;
+        ex = 0u;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            lb = sh.red[w] > lb ? sh.red[w] : lb;
+            lr = sh.red[16 + w] < lr ? sh.red[16 + w] : lr;
+            ex |= sh.red[32 + w];
+        }
+        any_exact = ex != 0u;
     }
     if (any_exact) flags |= G4S_FLAG_CHUNK_EXACT;
     const uint32_t L = lb > lr ? lb : lr;
 
-    /* candidates >= L: count, then gather (LDS when they fit, else HBM) */
-    const uint32_t* rkey = a.cand_key + (int64_t)row * kCandRow;
-    const uint32_t* ridx = a.cand_idx + (int64_t)row * kCandRow;
-    const int span = S * cap_c;
-    int cnt = 0;
-    for (int f = tid; f < span; f += BLOCK) {
-        int c = f / cap_c, p = f - c * cap_c;
-        if (p < (int)sh.rec[c].count && rkey[f] >= L) ++cnt;
-    }
-    int M;
-    int moff = block_exclusive_scan<BLOCK>(cnt, sh.scan, M);
-    const bool wide = M > kMergeLds;
-    uint32_t* mk = wide ? a.merge_key + (int64_t)row * kCandRow : sh.mkey;
-    uint32_t* mi = wide ? a.merge_idx + (int64_t)row * kCandRow : sh.midx;
-    if (wide) flags |= G4S_FLAG_WIDE_MERGE;
-    for (int f = tid; f < span; f += BLOCK) {
-        int c = f / cap_c, p = f - c * cap_c;
-        if (p < (int)sh.rec[c].count) {
-            uint32_t k = rkey[f];
-            if (k >= L) {
-                mk[moff] = k;
-                mi[moff] = ridx[f];
-                ++moff;
+    /* keep the candidates >= L (wave-level compaction); LDS holds the first
+     * kMergeLds of them, the rest go to the row's HBM merge area */
+    auto keep = [&](int f, uint64_t c) {
+        return f < span && (f & (cap - 1)) < (int)sh.rec[f >> a.cap_log2].count &&
+               cand_key_of(c) >= L;
+    };
+    for (int b0 = 0; b0 < span; b0 += kBatchLoads * BLOCK) {
+        if (b0 > 0) {
+#pragma unroll
+            for (int i = 0; i < kBatchLoads; ++i) {
+                const int f = b0 + tid + i * BLOCK;
+                v[i] = rcand[f < span ? f : span - 1];
+            }
+        }
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < kBatchLoads; ++i) cnt += keep(b0 + tid + i * BLOCK, v[i]);
+        const int incl = wave_inclusive_scan(cnt);
+        int base = 0;
+        if (lane == 63) base = atomicAdd(&sh.misc[1], incl);
+        base = __builtin_amdgcn_readlane(base, 63);
+        int pos = base + incl - cnt;
+#pragma unroll
+        for (int i = 0; i < kBatchLoads; ++i) {
+            if (keep(b0 + tid + i * BLOCK, v[i])) {
+                if (pos < kMergeLds)
+                    sh.mc[pos] = v[i];
+                else
+                    gmerge[pos] = v[i];
+                ++pos;
             }
         }
     }
     __syncthreads();
+    const int M = sh.misc[1];
+    if (M > kMergeLds) flags |= G4S_FLAG_WIDE_MERGE;
+    auto ent = [&](int i) -> uint64_t { return i < kMergeLds ? sh.mc[i] : gmerge[i]; };
+    auto ekey = [&](int i) { return cand_key_of(ent(i)); };
+    auto eidx = [&](int i) { return cand_idx_of(ent(i)); };
 
-    /* exact K-th largest among the M candidates */
+    /* exact top K of the M candidates */
     int nsurv = 0;
-    if (M <= K) {
-        /* M < K: fewer than K logits above -1e30 in the whole row; M == K:
-         * the candidates are exactly the top K.  Either way all survive. */
-        for (int i = tid; i < M; i += BLOCK) {
-            sh.skey[i] = mk[i];
-            sh.sidx[i] = (int32_t)mi[i];
-        }
-        nsurv = M;
-    } else {
-        int G, E;
-        uint32_t tau;
-        if (M <= kRankMax)
-            tau = rank_kth<BLOCK>(M, K, [&](int i) { return mk[i]; }, sh.misc, &G, &E);
-        else
-            tau = block_radix_kth<BLOCK>(
-                M, K, [&](int i) { return mk[i]; }, [&](int) { return true; }, sh.hist, sh.misc,
-                &G, &E);
-        const int need = K - G;
-        /* a chunk whose exact select truncated copies of tau */
-        int trunc = 0;
-        for (int c = tid; c < S; c += BLOCK) {
-            uint32_t me = sh.rec[c].mode_e;
-            if ((me >> 31) && sh.rec[c].bound == tau && (int)(me & 0x7FFFFFFFu) > K) trunc = 1;
-        }
-        trunc = block_sum_i32<BLOCK>(trunc, sh.scan);
-        int mode = 0; /* 0: all >= tau survive, 1: lowest-index ties, 2: heap replay */
-        int32_t idx_thr = 0x7FFFFFFF;
-        if (E != need || trunc) {
-            /* t* = index of the K-th element >= tau in index order */
-            int g2, e2;
-            uint32_t tstar_inv = block_radix_kth<BLOCK>(
-                M, K, [&](int i) { return ~mi[i]; }, [&](int i) { return mk[i] >= tau; }, sh.hist,
-                sh.misc, &g2, &e2);
-            int32_t tstar = (int32_t)~tstar_inv;
-            uint32_t mg = 0;
-            for (int i = tid; i < M; i += BLOCK)
-                if (mk[i] > tau) mg = (mi[i] + 1u) > mg ? (mi[i] + 1u) : mg;
-            mg = block_max_u32<BLOCK>(mg, sh.red);
-            const int32_t max_gt = (int32_t)mg - 1; /* -1 when nothing is above tau */
-            if (max_gt < tstar) {
-                mode = 1;
-                uint32_t thr_inv = block_radix_kth<BLOCK>(
-                    M, need, [&](int i) { return ~mi[i]; }, [&](int i) { return mk[i] == tau; },
-                    sh.hist, sh.misc, &g2, &e2);
-                idx_thr = (int32_t)~thr_inv;
-                flags |= G4S_FLAG_TIE_LOWEST;
-            } else {
-                mode = 2;
-                flags |= G4S_FLAG_HEAP_REPLAY;
-            }
-        }
-        if (mode < 2) {
-            int take_n = 0;
-            for (int i = tid; i < M; i += BLOCK) {
-                uint32_t k = mk[i];
-                take_n += (k > tau) || (k == tau && (mode == 0 || (int32_t)mi[i] <= idx_thr));
-            }
-            int sv;
-            int soff = block_exclusive_scan<BLOCK>(take_n, sh.scan, sv);
-            for (int i = tid; i < M; i += BLOCK) {
-                uint32_t k = mk[i];
-                if ((k > tau) || (k == tau && (mode == 0 || (int32_t)mi[i] <= idx_thr))) {
-                    sh.skey[soff] = k;
-                    sh.sidx[soff] = (int32_t)mi[i];
-                    ++soff;
+    bool general = any_exact || M > kMergeLds;
+    if (!general) {
+        /* one wave finds the K-th largest key tau of the M candidates (ballot
+         * search over registers); when the candidates hold exactly K keys
+         * >= tau there is no choice to make and they are the survivors.
+         * Otherwise (copies of tau must be split) the general path decides. */
+        if (M <= K) {
+            for (int i = tid; i < M; i += BLOCK) sh.surv[i] = sh.mc[i];
+            nsurv = M;
+        } else if (M <= 512) {
+            if (wid == 0) {
+                uint32_t kk[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int i = lane + 64 * q;
+                    kk[q] = i < M ? cand_key_of(sh.mc[i]) : 0u;
+                }
+                int G, E;
+                const uint32_t tau = wave_select_kth<8>(kk, K, &G, &E);
+                if (lane == 0) {
+                    sh.misc[4] = (int)tau;
+                    sh.misc[5] = (E == K - G) ? 0 : 1;
                 }
             }
-            nsurv = sv;
-        } else {
-            heap_replay<BLOCK, DT>(rowp, V, K, sh);
-            /* the heap holds K entries, all with index >= 0 here (M > K) */
-            for (int i = tid; i < K; i += BLOCK) {
-                float hv = reinterpret_cast<float*>(sh.skey)[i];
-                sh.skey[i] = f2key(hv);
+            __syncthreads();
+            const uint32_t tau = (uint32_t)sh.misc[4];
+            general = sh.misc[5] != 0;
+            if (!general) {
+                for (int i = tid; i < M; i += BLOCK) {
+                    const uint64_t c = sh.mc[i];
+                    if (cand_key_of(c) >= tau) sh.surv[atomicAdd(&sh.misc[2], 1)] = c;
+                }
+                nsurv = K;
             }
-            nsurv = K;
+        } else {
+            general = true;
+        }
+    }
+    if (general) {
+        if (M <= K) {
+            /* M < K: fewer than K logits above -1e30 in the whole row; M == K:
+             * the candidates are exactly the top K.  Either way all survive. */
+            for (int i = tid; i < M; i += BLOCK) sh.surv[i] = ent(i);
+            nsurv = M;
+        } else {
+            int G, E;
+            const uint32_t tau = select_kth<BLOCK>(M, K, ekey, sh, &G, &E);
+            const int need = K - G;
+            /* a chunk whose exact select truncated copies of tau */
+            int trunc = 0;
+            if (tid < S) {
+                const ChunkRec r = sh.rec[tid];
+                trunc = (r.mode_e >> 31) && r.bound == tau && (int)(r.mode_e & 0x7FFFFFFFu) > K;
+            }
+            trunc = block_sum_i32<BLOCK>(trunc, sh.scan);
+            int mode = 0; /* 0: all >= tau survive, 1: lowest-index ties, 2: heap replay */
+            int32_t idx_thr = 0x7FFFFFFF;
+            if (E != need || trunc) {
+                /* t* = index of the K-th element >= tau in index order */
+                int g2, e2;
+                const uint32_t tstar_inv = block_radix_kth<BLOCK>(
+                    M, K, [&](int i) { return ~eidx(i); }, [&](int i) { return ekey(i) >= tau; },
+                    sh.hist, sh.misc + 4, &g2, &e2);
+                const int32_t tstar = (int32_t)~tstar_inv;
+                uint32_t mg = 0;
+                for (int i = tid; i < M; i += BLOCK)
+                    if (ekey(i) > tau) mg = (eidx(i) + 1u) > mg ? (eidx(i) + 1u) : mg;
+                mg = block_max_u32<BLOCK>(mg, sh.red);
+                const int32_t max_gt = (int32_t)mg - 1; /* -1 when nothing is above tau */
+                if (max_gt < tstar) {
+                    /* every key above tau precedes the K-th key >= tau: the heap
+                     * keeps them and the first `need` copies of tau */
+                    mode = 1;
+                    const uint32_t thr_inv = block_radix_kth<BLOCK>(
+                        M, need, [&](int i) { return ~eidx(i); },
+                        [&](int i) { return ekey(i) == tau; }, sh.hist, sh.misc + 4, &g2, &e2);
+                    idx_thr = (int32_t)~thr_inv;
+                    flags |= G4S_FLAG_TIE_LOWEST;
+                } else {
+                    mode = 2;
+                    flags |= G4S_FLAG_HEAP_REPLAY;
+                }
+            }
+            if (mode < 2) {
+                auto surv_ok = [&](int i) {
+                    const uint32_t k = ekey(i);
+                    return (k > tau) || (k == tau && (mode == 0 || (int32_t)eidx(i) <= idx_thr));
+                };
+                int take_n = 0;
+                for (int i = tid; i < M; i += BLOCK) take_n += surv_ok(i);
+                int sv;
+                int soff = block_exclusive_scan<BLOCK>(take_n, sh.scan, sv);
+                for (int i = tid; i < M; i += BLOCK)
+                    if (surv_ok(i)) sh.surv[soff++] = ent(i);
+                nsurv = sv;
+            } else {
+                float* hv = reinterpret_cast<float*>(sh.surv);
+                int32_t* hi = reinterpret_cast<int32_t*>(sh.surv) + kMaxTopK;
+                heap_replay<BLOCK, DT>(rowp, V, K, sh, hv, hi);
+                /* the heap holds K entries, all with index >= 0 here (M > K);
+                 * K <= kbound <= BLOCK, so one entry per thread */
+                uint64_t mine_e = 0;
+                if (tid < K) mine_e = cand_pack(f2key(hv[tid]), (uint32_t)hi[tid]);
+                __syncthreads();
+                if (tid < K) sh.surv[tid] = mine_e;
+                nsurv = K;
+            }
         }
     }
     __syncthreads();
 
     if (nsurv == 0) {
-        if (tid == 0) {
-            a.ids[row] = -1;
-            if (a.out.flags) a.out.flags[row] = flags | G4S_FLAG_EMPTY;
-            if (a.out.count) a.out.count[row] = 0;
+        if (wid == 0) {
+            if (lane == 0) {
+                a.ids[row] = -1;
+                if (a.out.flags) a.out.flags[row] = flags | G4S_FLAG_EMPTY;
+                if (a.out.count) a.out.count[row] = 0;
+            }
+            publish_done(a.done, row, a.seq);
         }
         return;
     }
 
-    /* survivors ascending by vocab index (rank by count; indices distinct) */
-    for (int i = tid; i < nsurv; i += BLOCK) {
-        int32_t my = sh.sidx[i];
-        int r = 0;
-        for (int j = 0; j < nsurv; ++j) r += sh.sidx[j] < my;
-        sh.tidx[r] = my;
-        sh.tkey[r] = sh.skey[i];
+    /* one survivor per thread (nsurv <= K <= BLOCK): its slot in vocab-index
+     * order (rank by count; indices are distinct), then the reference's
+     * per-survivor steps */
+    const float cap_v = a.softcap;
+    const float T = rp.temperature;
+    const bool scale = (T > 0.0f) && (T != 1.0f);
+    const float inv_t = scale ? div_cr32(1.0f, T) : 1.0f;               /* :2782 */
+    uint32_t kv = 0u;
+    float vv = 0.0f;
+    int pos = 0;
+    if (tid < nsurv) {
+        const uint64_t my = sh.surv[tid];
+        const uint32_t mi = cand_idx_of(my);
+        int j = 0;
+        for (; j + 8 <= nsurv; j += 8) {
+            uint32_t xx[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) xx[t] = cand_idx_of(sh.surv[j + t]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) pos += xx[t] < mi;
+        }
+        for (; j < nsurv; ++j) pos += cand_idx_of(sh.surv[j]) < mi;
+        sh.sorted[pos] = my;
+        const float x = key2f(cand_key_of(my));                         /* :2774 */
+        vv = (cap_v > 0.0f) ? softcap_topk_cr32(x, cap_v) : x;          /* :2775-2776 */
+        if (scale) vv = vv * inv_t;                                     /* :2783-2784 */
+        kv = f2key(vv);
     }
+    kv = wave_max_u32(kv);
+    if (lane == 0) sh.red[wid] = kv;
+    __syncthreads();
+    uint32_t kmax = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) kmax = g4s_max_u(kmax, sh.red[w]);
+    const float vmax = key2f(kmax);                                     /* :2789-2792 */
+    if (tid < nsurv) sh.val[pos] = exp_diff_cr32(vv, vmax);             /* :2797 */
     __syncthreads();
 
     /* ------------------------------------------------ tail (wave 0 only) */
     if (wid != 0) return;
-    const float cap = a.softcap;
-    const float T = rp.temperature;
-    const bool scale = (T > 0.0f) && (T != 1.0f);
-    const float inv_t = scale ? div_cr32(1.0f, T) : 1.0f;               /* :2782 */
-    float vmax = -__builtin_inff();
-    for (int j = lane; j < nsurv; j += 64) {
-        float x = key2f(sh.tkey[j]);                                    /* :2774 */
-        float v = (cap > 0.0f) ? softcap_topk_cr32(x, cap) : x;         /* :2775-2776 */
-        if (scale) v = v * inv_t;                                       /* :2783-2784 */
-        sh.val[j] = v;
-        vmax = v > vmax ? v : vmax;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float w = __shfl_xor(vmax, o, 64);
-        vmax = w > vmax ? w : vmax;                                     /* :2789-2792 */
-    }
-    for (int j = lane; j < nsurv; j += 64) sh.val[j] = exp_diff_cr32(sh.val[j], vmax); /* :2797 */
-    __builtin_amdgcn_wave_barrier();
+    /* LSum := LSum + LVals[LI], left to right in binary32 (:2798); padding
+     * lanes add +0, which leaves a non-negative sum unchanged */
     float lsum = 0.0f;
-    if (lane == 0) {
-        for (int j = 0; j < nsurv; ++j) lsum = lsum + sh.val[j];        /* :2798 */
+    for (int base = 0; base < nsurv; base += 64) {
+        const float x = (base + lane < nsurv) ? sh.val[base + lane] : 0.0f;
+        const int n = nsurv - base < 64 ? nsurv - base : 64;
+        for (int l = 0; l < n; ++l) lsum = lsum + lane_f(x, l);
     }
-    lsum = __shfl(lsum, 0, 64);
-    float pbest = -1.0f;
+    /* greedy choice: first position of the largest p (p >= 0, so its bits
+     * order like the values) */
+    uint32_t pbest = 0u;
     int jbest = 0x7FFFFFFF;
     for (int j = lane; j < nsurv; j += 64) {
-        float p = div_cr32(sh.val[j], lsum);                            /* :2800-2801 */
+        const float p = div_cr32(sh.val[j], lsum);                      /* :2800-2801 */
         sh.prob[j] = p;
-        if (p > pbest) {
-            pbest = p;
+        if (__float_as_uint(p) > pbest || jbest == 0x7FFFFFFF) {
+            pbest = __float_as_uint(p);
             jbest = j;
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {                                  /* :2804-2807 */
-        float pw = __shfl_xor(pbest, o, 64);
-        int jw = __shfl_xor(jbest, o, 64);
-        if (pw > pbest || (pw == pbest && jw < jbest)) {
-            pbest = pw;
-            jbest = jw;
-        }
-    }
+    const uint32_t pmax = wave_max_u32(jbest == 0x7FFFFFFF ? 0u : pbest); /* :2804-2807 */
+    const int jarg =
+        (int)wave_min_u32((jbest != 0x7FFFFFFF && pbest == pmax) ? (uint32_t)jbest : 0xFFFFFFFFu);
     __builtin_amdgcn_wave_barrier();
-    const int jarg = jbest;
     int chosen = jarg;
     if (T > 0.0f) {                                                     /* :2811-2824 */
         flags |= G4S_FLAG_DREW;
         const float thr = mul_u_p_cr32(u, rp.top_p);
+        /* LCum := LCum + LVals[LI] left to right; lane l keeps the running
+         * sum after term base + l, then one ballot finds the first >= thr */
+        float cum = 0.0f;
         int hit = -1;
-        if (lane == 0) {
-            float cum = 0.0f;
-            for (int j = 0; j < nsurv; ++j) {
-                cum = cum + sh.prob[j];
-                if (cum >= thr) {
-                    hit = j;
-                    break;
-                }
+        for (int base = 0; base < nsurv; base += 64) {
+            const float x = (base + lane < nsurv) ? sh.prob[base + lane] : 0.0f;
+            const int n = nsurv - base < 64 ? nsurv - base : 64;
+            float mine_c = 0.0f;
+            for (int l = 0; l < n; ++l) {
+                cum = cum + lane_f(x, l);
+                mine_c = (lane == l) ? cum : mine_c;
+            }
+            const uint64_t reach = __ballot(base + lane < nsurv && mine_c >= thr);
+            if (reach) {
+                hit = base + (int)__builtin_ctzll(reach);
+                break;
             }
         }
-        hit = __shfl(hit, 0, 64);
         if (hit >= 0) {
             chosen = hit;
             flags |= G4S_FLAG_REACHED;
         }
     }
     if (lane == 0) {
-        a.ids[row] = sh.tidx[chosen];                                   /* :2826 */
+        a.ids[row] = (int32_t)cand_idx_of(sh.sorted[chosen]);           /* :2826 */
         if (a.out.count) a.out.count[row] = nsurv;
-        if (a.out.argmax) a.out.argmax[row] = sh.tidx[jarg];
+        if (a.out.argmax) a.out.argmax[row] = (int32_t)cand_idx_of(sh.sorted[jarg]);
         if (a.out.lsum) a.out.lsum[row] = lsum;
         if (a.out.flags) a.out.flags[row] = flags;
     }
     if (a.out.indices || a.out.probs) {
         const int capn = a.out.capacity < nsurv ? a.out.capacity : nsurv;
         for (int j = lane; j < capn; j += 64) {
-            if (a.out.indices) a.out.indices[(int64_t)row * a.out.capacity + j] = sh.tidx[j];
+            if (a.out.indices)
+                a.out.indices[(int64_t)row * a.out.capacity + j] = (int32_t)cand_idx_of(sh.sorted[j]);
             if (a.out.probs) a.out.probs[(int64_t)row * a.out.capacity + j] = sh.prob[j];
         }
     }
+    publish_done(a.done, row, a.seq);
 }
 
 /* ---------------------------------------------------------------- launch */
@@ -558,16 +696,18 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound)
 {
     TopkConfig c{};
     c.block = kbound <= 64 ? 256 : 1024;
+    c.cap_log2 = 1;
+    while ((1 << c.cap_log2) < 2 * kbound) ++c.cap_log2;
     c.items = 32;
     c.chunk = c.block * c.items;
     c.splits = (vocab + c.chunk - 1) / c.chunk;
-    c.cap_c = 2 * kbound;
-    if (c.splits * c.cap_c > kCandRow || c.splits > kMaxSplits) {
+    if ((c.splits << c.cap_log2) > kCandRow || c.splits > kMaxSplits) {
         c.items = 64;
         c.chunk = c.block * c.items;
         c.splits = (vocab + c.chunk - 1) / c.chunk;
     }
-    c.ok = (c.splits * c.cap_c <= kCandRow) && (c.splits <= kMaxSplits);
+    c.ok = ((c.splits << c.cap_log2) <= kCandRow) && (c.splits <= kMaxSplits) &&
+           (1 << c.cap_log2) <= kMergeLds;
     return c;
 }
 

@@ -29,7 +29,54 @@ inline double now_us()
         .count();
 }
 
+__global__ void g4h_null_kernel(uint32_t* flag, uint32_t seq)
+{
+    if (threadIdx.x == 0 && flag)
+        __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 }  // namespace
+
+/*
+ * Host-side floor of a synchronous single-kernel call: `n` launches of an
+ * empty one-wave kernel, each followed by
+ *   mode 0: hipStreamSynchronize
+ *   mode 1: a host spin on a pinned flag the kernel stores (system scope),
+ *           then hipStreamSynchronize only after the timed region
+ * us[i] = wall clock from before the launch to the end of the wait.
+ */
+G4H_API int g4h_null_roundtrip(void* stream, int32_t n, int32_t mode, double* us)
+{
+    hipStream_t st = (hipStream_t)stream;
+    uint32_t* flag = nullptr;
+    if (hipHostMalloc((void**)&flag, 64, hipHostMallocCoherent) != hipSuccess) return -101;
+    *flag = 0;
+    int rc = 0;
+    for (int32_t i = 0; i < n && rc == 0; ++i) {
+        const uint32_t seq = (uint32_t)i + 1u;
+        double t0 = now_us();
+        hipLaunchKernelGGL(g4h_null_kernel, dim3(1), dim3(64), 0, st, mode == 1 ? flag : nullptr,
+                           seq);
+        if (hipGetLastError() != hipSuccess) {
+            rc = -102;
+            break;
+        }
+        if (mode == 1) {
+            /* bounded spin: ~2 s, then give up and report */
+            uint64_t spins = 0;
+            while (__atomic_load_n(flag, __ATOMIC_ACQUIRE) != seq && ++spins < 2000000000ull) {
+            }
+            if (spins >= 2000000000ull) rc = -103;
+        } else if (hipStreamSynchronize(st) != hipSuccess) {
+            rc = -104;
+        }
+        us[i] = now_us() - t0;
+        if (mode == 1 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    }
+    (void)hipStreamSynchronize(st);
+    (void)hipHostFree(flag);
+    return rc;
+}
 
 /*
  * Decode-style latency: `nrows` single-row samples back to back.  Row r of
