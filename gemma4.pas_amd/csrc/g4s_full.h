@@ -5,12 +5,52 @@
 #define G4S_FULL_H
 
 #include "g4s_device.h"
+#include "g4s_seqsum.h"
 
 namespace g4s {
 
+constexpr int kFullBlock = 1024;                    /* threads per chunk workgroup */
+constexpr int kFullPer = 16;                        /* consecutive terms per thread */
+constexpr int kFullChunk = kFullBlock * kFullPer;   /* terms per chunk */
+constexpr int kFullMaxChunks = 256;                 /* chunks per row: vocab <= 2^22 */
+constexpr int kFullTab = 4096;                      /* bf16 codes with a tabulated e */
+
+/* Per-row state shared by the four kernels (device workspace). */
+struct FullRow {
+    uint32_t maxkey;  /* order-preserving key of the largest raw logit */
+    uint32_t amax;    /* largest |logit| as a key of |x| */
+    float m;          /* max over the row of y = softcap(x) [* 1/T] */
+    float inv_t;      /* fl32(1/T) when scaling, else 1 */
+    int32_t scale;    /* T > 0 and T <> 1 */
+    int32_t win_lo;   /* bf16 exponent field of the table's lowest binade, -1: no table */
+    float lsum;       /* LSum (exact) */
+    float inv;        /* fl32(1/LSum) */
+    float thr;        /* fl32(u * TopP) */
+    int32_t argmax;   /* first index of the largest p */
+    int32_t c_last;   /* last chunk the draw kernel visits, -1: none */
+    int32_t nodraw;   /* T <= 0: the greedy choice, no draw (probabilities still written) */
+};
+
+/* Per-chunk records. */
+struct FullChunk {
+    uint32_t maxkey;  /* max kernel: chunk's largest key */
+    float ymax;       /* approximate y at the chunk's largest logit */
+    float sapx;       /* approximate sum of exp(y - ymax) over the chunk */
+    int32_t beta_l;   /* predicted binade of LSum entering the chunk */
+    ss::PMap lmap;    /* lsum kernel: the chunk's terms in beta_l */
+    double de;        /* sum of the chunk's e in binary64 */
+    int32_t first1;   /* first index with e == 1, or INT_MAX */
+    int32_t first2;   /* first index with e == 1 - 2^-24, or INT_MAX */
+    int32_t beta_c;   /* predicted binade of the running sum entering the chunk */
+    ss::PMap cmap;    /* draw kernel: the chunk's p in beta_c */
+    int32_t pad;
+};
+
 struct FullWorkspace {
-    void* base = nullptr;
-    size_t bytes = 0;
+    FullRow* rows = nullptr;     /* [max_batch] */
+    FullChunk* chunks = nullptr; /* [max_batch][kFullMaxChunks] */
+    float* etab = nullptr;       /* [max_batch][kFullTab] */
+    uint32_t* tickets = nullptr; /* [max_batch][4], zero between launches */
 };
 
 struct FullArgs {
@@ -23,14 +63,18 @@ struct FullArgs {
     g4s_params p0;
     double u0;
     float softcap;
+    int32_t nch;
     FullWorkspace ws;
     int32_t* ids;
+    uint32_t* done;
+    uint32_t seq;
     g4s_outputs out;
 };
 
 hipError_t full_alloc(FullWorkspace& ws, int32_t vocab, int32_t max_batch);
 void full_free(FullWorkspace& ws);
-hipError_t full_init(FullWorkspace& ws, hipStream_t s);
+hipError_t full_init(FullWorkspace& ws, int32_t max_batch, hipStream_t s);
+bool full_supported(int32_t vocab);
 hipError_t full_launch(const FullArgs& a, int dtype, hipStream_t s);
 
 }  // namespace g4s

@@ -158,6 +158,10 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         if (e != hipSuccess) return hip_fail(s, e, "top-k kernel launch");
     }
     if (full_rows) {
+        if (!g4s::full_supported(s->vocab))
+            return fail(s, G4S_ERR_UNSUPPORTED,
+                        "the full-vocabulary path supports vocab <= %d (TopK <= 0 or >= V)",
+                        g4s::kFullChunk * g4s::kFullMaxChunks);
         g4s::FullArgs f{};
         f.logits = d_logits;
         f.row_stride = row_stride;
@@ -168,8 +172,11 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         if (p0) f.p0 = *p0;
         f.u0 = u0;
         f.softcap = s->softcap;
+        f.nch = (s->vocab + g4s::kFullChunk - 1) / g4s::kFullChunk;
         f.ws = s->full;
         f.ids = d_ids;
+        f.done = done;
+        f.seq = seq;
         f.out = out;
         hipError_t e = g4s::full_launch(f, dtype, s->stream);
         if (e != hipSuccess) return hip_fail(s, e, "full-vocabulary kernel launch");
@@ -259,8 +266,11 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
         return fail(nullptr, G4S_ERR_OUT_OF_MEMORY,
                     "workspace allocation failed (vocab %d, max_batch %d)", vocab, max_batch);
     }
+    /* pinned allocations can be recycled memory: the completion words must
+     * start below the first sequence value */
+    std::memset(s->h_done, 0, mb * sizeof(uint32_t));
     hipError_t e = hipMemsetAsync(s->tickets, 0, mb * sizeof(uint32_t), s->stream);
-    if (e == hipSuccess) e = g4s::full_init(s->full, s->stream);
+    if (e == hipSuccess) e = g4s::full_init(s->full, max_batch, s->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) {
         release(s);
@@ -324,8 +334,7 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
         s->h_flags[r] = 0u;
     }
     if (!user_flags) out.flags = s->h_flags;
-    /* rows of the full-vocabulary path do not publish completion words */
-    uint32_t* done = (!user_flags && !full_rows) ? s->h_done : nullptr;
+    uint32_t* done = !user_flags ? s->h_done : nullptr;
 
     if (batch == 1) {
         rc = enqueue(s, d_logits, dtype, row_stride, 1, nullptr, nullptr, &params[0], u[0], kbound,

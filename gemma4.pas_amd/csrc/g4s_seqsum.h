@@ -1,0 +1,155 @@
+/*
+ * g4s_seqsum.h -- exact parallel evaluation of a left-to-right binary32
+ * running sum of non-negative terms, identical on the host and on gfx950.
+ *
+ * The reference accumulates LSum and the index-order running sum of the
+ * sampling draw one term at a time in binary32 (src/Gemma4.Tensors.pas:657-
+ * 663, src/Gemma4.Model.pas:2727-2735): S_0 = 0, S_{i+1} = RN32(S_i + a_i).
+ * Summing in any other order changes the last bits, and over 262144 terms
+ * that changes which token is drawn.  This header restates the recurrence so
+ * that blocks of terms can be evaluated independently and chained:
+ *
+ *  - While S stays inside one binade of width 2^24 units u (u = 2^(E-150),
+ *    E = max(exponent field of S, 1)), S = M*u for an integer M < 2^24 and
+ *    RN32(M*u + a) = u * RNE(M + a/u).  With a/u = k + f (k integer,
+ *    0 <= f < 1) that is M + k when f < 1/2, M + k + 1 when f > 1/2, and at
+ *    f = 1/2 the even one of M + k and M + k + 1.  So every term is the map
+ *    M -> M + d[M & 1] with d[p] = c + t*((p + c) & 1), where
+ *    c = k + (f > 1/2) and t = (f == 1/2).
+ *  - Maps of that form are closed under composition:
+ *    (f then g)[p] = f[p] + g[(p + f[p]) & 1]; the composition is
+ *    associative, so a block of terms reduces to one map by any tree or scan.
+ *  - Applying a block's map is exact as long as no intermediate sum leaves
+ *    the binade.  M only grows, so a result below 2^24 proves it; a result
+ *    >= 2^24 means the block crosses (or may cross) into the next binade,
+ *    and the caller re-evaluates that block at finer grain around the
+ *    crossing, where one plain binary32 addition is exact by definition.
+ *
+ * The subnormal range and [2^-126, 2^-125) share u = 2^-149 (E = 1), so
+ * S = 0 is simply M = 0 in binade E = 1; no special case is needed.
+ */
+#ifndef G4S_SEQSUM_H
+#define G4S_SEQSUM_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define G4S_SS_HD __host__ __device__ __forceinline__
+#else
+#define G4S_SS_HD static inline
+#endif
+
+namespace g4s {
+namespace ss {
+
+constexpr int32_t kTop = 1 << 24; /* M reaching this left the binade */
+
+/* State of a running sum: binade E (>= 1) and significand M in units of
+ * 2^(E-150), 0 <= M < 2^24 (M >= 2^23 unless E == 1). */
+struct State {
+    int32_t e;
+    int32_t m;
+};
+
+/* A block's effect: M -> M + d[M & 1]. */
+struct PMap {
+    int32_t d0, d1;
+};
+
+G4S_SS_HD uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
+G4S_SS_HD float bitsf(uint32_t b) { return __builtin_bit_cast(float, b); }
+
+G4S_SS_HD State state_of(float s)
+{
+    const uint32_t b = fbits(s) & 0x7FFFFFFFu;
+    const int32_t ef = (int32_t)(b >> 23);
+    const int32_t man = (int32_t)(b & 0x7FFFFFu);
+    State st;
+    if (ef == 0) {
+        st.e = 1;
+        st.m = man; /* subnormal or zero: units of 2^-149 */
+    } else {
+        st.e = ef;
+        st.m = man | 0x800000;
+    }
+    return st;
+}
+
+/* The binary32 value of a state (M < 2^24; M == 2^24 is 2^(E-126)). */
+G4S_SS_HD float value_of(State st)
+{
+    if (st.m >= kTop) return bitsf((uint32_t)(st.e + 1) << 23);
+    if (st.m < 0x800000) return bitsf((uint32_t)st.m); /* only for E == 1 */
+    return bitsf(((uint32_t)st.e << 23) + (uint32_t)(st.m - 0x800000));
+}
+
+/* c and t of one term a >= 0 in binade E; c = kTop when a alone leaves the
+ * binade (a >= 2^(E-126)).  Packed as c*2 + t. */
+G4S_SS_HD int32_t term_ct(float a, int32_t e)
+{
+    const uint32_t b = fbits(a);
+    const int32_t ea = (int32_t)(b >> 23);
+    if (ea == 0 && (b & 0x7FFFFFu) == 0u) return 0; /* +0 */
+    const int32_t ma = (int32_t)(b & 0x7FFFFFu) | (ea ? 0x800000 : 0);
+    const int32_t s = e - (ea ? ea : 1);
+    if (s < 0) return kTop * 2;
+    if (s == 0) return ma * 2;
+    if (s > 25) return 0; /* a < u/4 */
+    const int32_t k = ma >> s;
+    const int32_t rem = ma & ((1 << s) - 1);
+    const int32_t half = 1 << (s - 1);
+    return (k + (rem > half)) * 2 + (rem == half);
+}
+
+G4S_SS_HD PMap map_of_ct(int32_t ct)
+{
+    const int32_t c = ct >> 1, t = ct & 1;
+    PMap r;
+    r.d0 = c + (t & c);         /* p = 0: (0 + c) & 1 */
+    r.d1 = c + (t & (c + 1));   /* p = 1: (1 + c) & 1 */
+    return r;
+}
+
+G4S_SS_HD PMap map_identity()
+{
+    PMap r;
+    r.d0 = 0;
+    r.d1 = 0;
+    return r;
+}
+
+/* f then g */
+G4S_SS_HD PMap map_then(PMap f, PMap g)
+{
+    PMap r;
+    r.d0 = f.d0 + (((f.d0) & 1) ? g.d1 : g.d0);
+    r.d1 = f.d1 + (((1 + f.d1) & 1) ? g.d1 : g.d0);
+    return r;
+}
+
+/* Apply a map: the new M (may be >= kTop: the block left the binade). */
+G4S_SS_HD int32_t map_apply(PMap f, int32_t m) { return m + ((m & 1) ? f.d1 : f.d0); }
+
+/* Saturating variant for long blocks: keeps the increments below 2^30 so
+ * compositions cannot overflow; any value >= kTop already means "left". */
+G4S_SS_HD PMap map_sat(PMap f)
+{
+    const int32_t cap = 1 << 26;
+    PMap r;
+    r.d0 = f.d0 > cap ? cap + (f.d0 & 1) : f.d0;
+    r.d1 = f.d1 > cap ? cap + (f.d1 & 1) : f.d1;
+    return r;
+}
+
+/* One reference step, S <- RN32(S + a), on a state (exact by definition). */
+G4S_SS_HD State step_add(State st, float a)
+{
+    const float s = value_of(st);
+    const float r = s + a;
+    return state_of(r);
+}
+
+}  // namespace ss
+}  // namespace g4s
+
+#endif
