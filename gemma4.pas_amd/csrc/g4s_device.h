@@ -111,6 +111,49 @@ __device__ __forceinline__ void load_vec_full(const char* row, int64_t e0, float
     }
 }
 
+/* Cross-workgroup exchange without cache maintenance.  Everything one
+ * workgroup hands to another inside a launch is written with device-scope
+ * coherent stores (st_dev: written through to the device's point of
+ * coherence) and read with device-scope coherent loads (ld_dev), so no L2
+ * writeback or invalidate is ever issued (those act on a whole XCD's L2 and
+ * serialize when thousands of workgroups issue them). */
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(uint64_t* p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p)
+{
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev(const uint64_t* p)
+{
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Elect the last of `count` workgroups that share *ticket.  Each thread's
+ * device-coherent stores have completed (s_waitcnt) before the barrier, so
+ * they are visible to whichever workgroup takes the last ticket; that one
+ * reads them with ld_dev and resets the ticket for the next launch.  `flag`
+ * is an LDS word.  Returns true in the elected workgroup. */
+__device__ __forceinline__ bool elect_last(uint32_t* ticket, uint32_t count, int* flag)
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev =
+            __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev == count - 1u;
+        if (last) st_dev(ticket, 0u);
+        *flag = last;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
 /* Publish a row's completion for a host that spins on `done` instead of
  * synchronizing the stream: every store the calling wave made before this
  * point is visible to the host before done[row] reads `seq`.  Called by all

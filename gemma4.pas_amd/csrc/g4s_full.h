@@ -9,10 +9,10 @@
 
 namespace g4s {
 
-constexpr int kFullBlock = 1024;                    /* threads per chunk workgroup */
+constexpr int kFullBlock = 256;                     /* threads per chunk workgroup */
 constexpr int kFullPer = 16;                        /* consecutive terms per thread */
 constexpr int kFullChunk = kFullBlock * kFullPer;   /* terms per chunk */
-constexpr int kFullMaxChunks = 256;                 /* chunks per row: vocab <= 2^22 */
+constexpr int kFullMaxChunks = 1024;                /* chunks per row: vocab <= 2^22 */
 constexpr int kFullTab = 4096;                      /* bf16 codes with a tabulated e */
 
 /* Per-row state shared by the four kernels (device workspace). */
@@ -29,22 +29,31 @@ struct FullRow {
     int32_t argmax;   /* first index of the largest p */
     int32_t c_last;   /* last chunk the draw kernel visits, -1: none */
     int32_t nodraw;   /* T <= 0: the greedy choice, no draw (probabilities still written) */
+    /* diagnostics: chunks re-evaluated and re-evaluation rounds, LSum chain
+     * then draw chain */
+    int32_t l_reev, l_rounds, c_reev, c_rounds;
 };
 
-/* Per-chunk records. */
+/* Per-chunk records.  Fields exchanged between workgroups of one launch are
+ * aligned 64-bit words written and read with device-coherent accesses. */
 struct FullChunk {
-    uint32_t maxkey;  /* max kernel: chunk's largest key */
-    float ymax;       /* approximate y at the chunk's largest logit */
-    float sapx;       /* approximate sum of exp(y - ymax) over the chunk */
+    uint32_t maxkey;  /* max kernel: chunk's largest key          } word 0 */
+    uint32_t amax;    /* max kernel: largest |x| as a key          }        */
+    float ymax;       /* approximate y at the chunk's largest logit } word 1 */
+    float sapx;       /* approximate sum of exp(y - ymax)           }        */
+    ss::PMap lmap;    /* lsum kernel: the chunk's terms in beta_l     word 2 */
+    ss::PMap cmap;    /* draw kernel: the chunk's p in beta_c         word 3 */
+    double de;        /* lsum kernel: sum of the chunk's e in binary64  word 4 */
+    int32_t first1;   /* lsum kernel: first index with e == 1, or INT_MAX */
     int32_t beta_l;   /* predicted binade of LSum entering the chunk */
-    ss::PMap lmap;    /* lsum kernel: the chunk's terms in beta_l */
-    double de;        /* sum of the chunk's e in binary64 */
-    int32_t first1;   /* first index with e == 1, or INT_MAX */
-    int32_t first2;   /* first index with e == 1 - 2^-24, or INT_MAX */
     int32_t beta_c;   /* predicted binade of the running sum entering the chunk */
-    ss::PMap cmap;    /* draw kernel: the chunk's p in beta_c */
-    int32_t pad;
+    int32_t pad[3];
 };
+
+static_assert(sizeof(FullChunk) == 64, "FullChunk layout");
+static_assert(__builtin_offsetof(FullChunk, ymax) == 8 && __builtin_offsetof(FullChunk, lmap) == 16 &&
+                  __builtin_offsetof(FullChunk, cmap) == 24 && __builtin_offsetof(FullChunk, de) == 32,
+              "FullChunk words");
 
 struct FullWorkspace {
     FullRow* rows = nullptr;     /* [max_batch] */

@@ -12,24 +12,25 @@
  *   index of the largest p;  if T > 0: the first i whose left-to-right
  *   binary32 running sum of p reaches fl32(u * TopP), else the argmax.
  *
- * Rows are cut into chunks of 16384 terms, 16 consecutive terms per thread
- * of a 1024-thread workgroup.  Four launches, each ending in the last
- * workgroup of the row (atomic ticket):
- *   1 max:   raw-logit maximum (softcap and 1/T are monotone, so
- *            m = y(max x)) and approximate chunk sums of exp(y - m), whose
- *            prefix predicts the binade LSum is in when it enters each chunk;
- *   2 table: for bf16 logits, e for the 4096 codes of the 16 largest
- *            exponents of |x| (correctly rounded, once per row), so the
- *            streaming passes look e up instead of evaluating it;
- *   3 lsum:  each chunk's terms as one exact map of the running sum in its
- *            predicted binade (g4s_seqsum.h), plus binary64 chunk sums; the
- *            last workgroup chains the maps, verifying every step, and
- *            re-evaluates any chunk whose map does not apply thread by
- *            thread: LSum, 1/LSum, the argmax, and predicted binades of the
- *            draw's running sum;
- *   4 cdf:   the same for p up to the chunk where the running sum is
- *            predicted to reach fl32(u*TopP); the last workgroup finds the
- *            exact first index and writes the token.
+ * Rows are cut into chunks of 4096 terms, 16 consecutive terms per thread
+ * of a 256-thread workgroup.  Six launches:
+ *   1 max:    raw-logit maximum (softcap and 1/T are monotone, so
+ *             m = y(max x)) and approximate chunk sums of exp(y - m); the
+ *             row's last workgroup (atomic ticket) turns their prefix into
+ *             the predicted binade of LSum entering every chunk;
+ *   2 table:  for bf16 logits, e for the 4096 codes of the 16 largest
+ *             exponents of |x| (correctly rounded, once per row), so the
+ *             streaming passes look e up instead of evaluating it;
+ *   3 lsum:   each chunk's terms as one exact map of the running sum in its
+ *             predicted binade (g4s_seqsum.h), plus binary64 chunk sums;
+ *   4 chain:  one workgroup per row chains the maps left to right,
+ *             verifying every step and re-evaluating any chunk whose map
+ *             does not apply: LSum, 1/LSum, the argmax, and the predicted
+ *             binades of the draw's running sum;
+ *   5 cdf:    the same maps for p, up to the chunk where the running sum is
+ *             predicted to reach fl32(u*TopP);
+ *   6 draw:   one workgroup per row finds the exact first index and writes
+ *             the token.
  * Transcendental steps are correctly rounded (g4s_crmath.h); every running
  * sum is the reference's left-to-right binary32 sum, bit for bit.
  */
@@ -49,10 +50,11 @@ constexpr int NWF = kFullBlock / 64; /* waves per workgroup */
 
 __device__ __forceinline__ bool is_full_row(int K, int V) { return K <= 0 || K >= V; }
 
-/* The 16 terms of one thread: x as binary32 and, for bf16, the 16-bit code. */
+/* The 16 consecutive terms of one thread as raw bits: binary32 bits, or the
+ * 16-bit bf16 code.  Terms at or beyond V are 0 and not counted. */
 template <int DT>
-__device__ __forceinline__ int load16(const char* rowp, int64_t e0, int V, float (&x)[kFullPer],
-                                      uint32_t (&code)[kFullPer])
+__device__ __forceinline__ int load16(const char* rowp, int64_t e0, int V,
+                                      uint32_t (&raw)[kFullPer])
 {
     const int nvalid = (int)(V - e0 < 0 ? 0 : (V - e0 > kFullPer ? kFullPer : V - e0));
     if (nvalid == kFullPer) {
@@ -60,13 +62,11 @@ __device__ __forceinline__ int load16(const char* rowp, int64_t e0, int V, float
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint4 w = reinterpret_cast<const uint4*>(rowp + e0 * 4)[q];
-                x[4 * q] = __uint_as_float(w.x);
-                x[4 * q + 1] = __uint_as_float(w.y);
-                x[4 * q + 2] = __uint_as_float(w.z);
-                x[4 * q + 3] = __uint_as_float(w.w);
+                raw[4 * q] = w.x;
+                raw[4 * q + 1] = w.y;
+                raw[4 * q + 2] = w.z;
+                raw[4 * q + 3] = w.w;
             }
-#pragma unroll
-            for (int j = 0; j < kFullPer; ++j) code[j] = 0u;
         } else {
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
@@ -74,31 +74,30 @@ __device__ __forceinline__ int load16(const char* rowp, int64_t e0, int V, float
                 const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    code[8 * q + 2 * i] = ww[i] & 0xFFFFu;
-                    code[8 * q + 2 * i + 1] = ww[i] >> 16;
+                    raw[8 * q + 2 * i] = ww[i] & 0xFFFFu;
+                    raw[8 * q + 2 * i + 1] = ww[i] >> 16;
                 }
             }
-#pragma unroll
-            for (int j = 0; j < kFullPer; ++j) x[j] = __uint_as_float(code[j] << 16);
         }
     } else {
 #pragma unroll
         for (int j = 0; j < kFullPer; ++j) {
+            raw[j] = 0u;
             if (j < nvalid) {
-                if constexpr (DT == 0) {
-                    x[j] = reinterpret_cast<const float*>(rowp)[e0 + j];
-                    code[j] = 0u;
-                } else {
-                    code[j] = reinterpret_cast<const uint16_t*>(rowp)[e0 + j];
-                    x[j] = __uint_as_float(code[j] << 16);
-                }
-            } else {
-                x[j] = 0.0f;
-                code[j] = 0u;
+                if constexpr (DT == 0)
+                    raw[j] = reinterpret_cast<const uint32_t*>(rowp)[e0 + j];
+                else
+                    raw[j] = reinterpret_cast<const uint16_t*>(rowp)[e0 + j];
             }
         }
     }
     return nvalid;
+}
+
+template <int DT>
+__device__ __forceinline__ float x_of(uint32_t raw)
+{
+    return DT == 0 ? __uint_as_float(raw) : __uint_as_float(raw << 16);
 }
 
 /* y = softcap(x) [* 1/T] exactly as the reference rounds it (Layers.pas:
@@ -110,18 +109,42 @@ __device__ __forceinline__ float y_exact(float x, float cap, float inv_cap, int 
     return y;
 }
 
-/* A cheap approximation of y for the binade predictions only. */
+/* A cheap approximation of y for the binade predictions only (a few ulps
+ * to ~1e-4 relative; the chains verify every step, so a poor prediction
+ * only costs a re-evaluation). */
 __device__ __forceinline__ float y_approx(float x, float cap, float inv_cap, int scale, float inv_t)
 {
     float y = x;
     if (cap > 0.0f) {
-        float w = x * inv_cap;
-        w = w > 12.0f ? 12.0f : (w < -12.0f ? -12.0f : w);
-        const float e2 = __expf(2.0f * w);
-        y = __fdividef(e2 - 1.0f, e2 + 1.0f) * cap;
+        const float w = x * inv_cap;
+        float t;
+        if (__builtin_fabsf(w) < 0.5f) {
+            const float w2 = w * w; /* odd Taylor series of tanh to w^9 */
+            t = w * (1.0f + w2 * (-0.33333334f + w2 * (0.13333334f + w2 * (-0.053968254f +
+                                                                        w2 * 0.021869488f))));
+        } else {
+            const float wc = w > 12.0f ? 12.0f : (w < -12.0f ? -12.0f : w);
+            const float e2 = __builtin_amdgcn_exp2f(wc * 2.8853900817779268f); /* e^(2w) */
+            t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e2 + 1.0f);
+        }
+        y = t * cap;
     }
     if (scale) y = y * inv_t;
     return y;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v)
+{
+#define G4S_FSTEP(ctrl, rmask)                                                                  \
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, rmask, 0xf, false))
+    G4S_FSTEP(0x111, 0xf);
+    G4S_FSTEP(0x112, 0xf);
+    G4S_FSTEP(0x114, 0xf);
+    G4S_FSTEP(0x118, 0xf);
+    G4S_FSTEP(0x142, 0xa);
+    G4S_FSTEP(0x143, 0xc);
+#undef G4S_FSTEP
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 /* Index of a bf16 code in the row's table, or -1 outside the window. */
@@ -137,17 +160,24 @@ struct Ctx {
     int scale, win_lo;
 };
 
+/* e of one term evaluated from x (kept out of line: it is the rare case for
+ * bf16 logits, whose codes are tabulated). */
+__device__ __noinline__ float e_direct(float x, Ctx c)
+{
+    return exp_diff_cr32(y_exact(x, c.cap, c.inv_cap, c.scale, c.inv_t), c.m);
+}
+
 /* e of one term: the table when the code is in the window, else evaluated. */
 template <int DT>
-__device__ __forceinline__ float e_of(float x, uint32_t code, const Ctx& c, const float* tab)
+__device__ __forceinline__ float e_of(uint32_t raw, const Ctx& c, const float* tab)
 {
     if constexpr (DT == 1) {
         if (c.win_lo >= 0) {
-            const int ti = tab_index(code, c.win_lo);
+            const int ti = tab_index(raw, c.win_lo);
             if (ti >= 0) return tab[ti];
         }
     }
-    return exp_diff_cr32(y_exact(x, c.cap, c.inv_cap, c.scale, c.inv_t), c.m);
+    return e_direct(x_of<DT>(raw), c);
 }
 
 /* ------------------------------------------------------ block helpers */
@@ -294,20 +324,21 @@ __device__ __forceinline__ PMap block_chunk_map(PMap f, FullShared& sh)
 /*
  * Exact evaluation of one chunk's running sum from the exact entering state
  * `st`, by the whole workgroup (thread t holds terms t*16 .. t*16+15 of the
- * chunk).  Each round maps every remaining thread's terms in the current
- * binade, finds the first thread whose exit leaves the binade (or reaches
- * `thr`), and steps through that thread's terms with plain binary32
- * additions from its exact entering sum.  Returns the state after the chunk
- * or, when `thr` is reached, the index (chunk-relative) of the first term
- * whose running sum reaches it in *hit.
+ * chunk; threads before `pos` are already accounted for).  Each round maps
+ * every remaining thread's terms in the current binade, finds the first
+ * thread whose exit leaves the binade (or reaches `thr`), and walks that
+ * thread's terms from its exact entering sum: the map step while the sum
+ * stays in its binade, one plain binary32 addition where it leaves it.
+ * Returns the state after the chunk or, when `thr` is reached, the index
+ * (chunk-relative) of the first term whose running sum reaches it in *hit.
+ * Rounds are counted in sh.misc[12].
  */
 __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st, float thr,
-                               int* hit, FullShared& sh)
+                               int pos, int* hit, FullShared& sh)
 {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    int pos = 0; /* first thread not yet accounted for */
     *hit = -1;
-    for (;;) {
+    while (pos < kFullBlock) {
         const int32_t e = st.e;
         const PMap f = (tid >= pos) ? thread_map(t, nvalid, e) : ss::map_identity();
         const PMap incl = wave_scan_maps(f);
@@ -315,6 +346,7 @@ __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st,
         if (lane == 63) sh.wmap[wid] = incl;
         __syncthreads();
         if (tid == 0) {
+            ++sh.misc[12];
             int32_t m = st.m;
             for (int w = 0; w < NWF; ++w) {
                 sh.went[w] = m;
@@ -343,8 +375,15 @@ __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st,
             /* m_in is exact: every earlier thread stayed in the binade */
             State s2{e, m_in};
             int h = -1;
-            for (int j = 0; j < nvalid; ++j) {
-                s2 = ss::step_add(s2, t[j]);
+#pragma unroll
+            for (int j = 0; j < kFullPer; ++j) {
+                if (j >= nvalid) break;
+                const int32_t m2 =
+                    ss::map_apply(ss::map_of_ct(ss::term_ct(t[j], s2.e)), s2.m);
+                if (m2 < ss::kTop)
+                    s2.m = m2;
+                else
+                    s2 = ss::step_add(s2, t[j]);
                 if (ss::value_of(s2) >= thr) {
                     h = tstar * kFullPer + j;
                     break;
@@ -364,22 +403,39 @@ __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st,
             return st;
         }
         pos = tstar + 1;
-        if (pos >= kFullBlock) return st;
+    }
+    return st;
+}
+
+/* The row's first kHead terms (threads 0 .. kHead/16 - 1 of chunk 0), where
+ * the running sum changes binade every few terms, summed left to right in
+ * binary32 by wave 0 (one readlane per term); the result and the first index
+ * reaching `thr` go to sh.misc[9..11] for the whole workgroup. */
+constexpr int kHead = 256;
+__device__ void head_walk(const float (&t)[kFullPer], float thr, FullShared& sh)
+{
+    if (threadIdx.x >= 64) return;
+    float s = 0.0f;
+    int h = -1;
+    for (int l = 0; l < kHead / kFullPer; ++l) {
+#pragma unroll
+        for (int j = 0; j < kFullPer; ++j) {
+            s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[j]), l));
+            if (h < 0 && s >= thr) h = l * kFullPer + j;
+        }
+        if (h >= 0) break;
+    }
+    if (threadIdx.x == 0) {
+        const State st = ss::state_of(s);
+        sh.misc[9] = st.e;
+        sh.misc[10] = st.m;
+        sh.misc[11] = h;
     }
 }
 
-/* Elect the last workgroup of the row (release this workgroup's records,
- * acquire everyone's in the elected one). */
 __device__ __forceinline__ bool last_of_row(uint32_t* ticket, uint32_t count, FullShared& sh)
 {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (threadIdx.x == 0) sh.flag_last = (atomicAdd(ticket, 1u) == count - 1u);
-    __syncthreads();
-    if (!sh.flag_last) return false;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (threadIdx.x == 0) *ticket = 0u;
-    return true;
+    return elect_last(ticket, count, &sh.flag_last);
 }
 
 struct RowIn {
@@ -429,35 +485,56 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
     const int scale = (T > 0.0f) && (T != 1.0f);                       /* Model.pas:2703 */
     const float inv_t = scale ? div_cr32(1.0f, T) : 1.0f;              /* Model.pas:2705 */
 
-    float x[kFullPer];
-    uint32_t code[kFullPer];
-    const int nvalid = load16<DT>(rowp, (int64_t)b * kFullChunk + (int64_t)tid * kFullPer, V, x, code);
+    uint32_t raw[kFullPer];
+    const int nvalid = load16<DT>(rowp, (int64_t)b * kFullChunk + (int64_t)tid * kFullPer, V, raw);
     uint32_t kmax = 0u, amax = 0u, ymk = 0u;
     float ya[kFullPer];
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j) {
-        ya[j] = y_approx(x[j], cap, inv_cap, scale, inv_t);
+        const float xj = x_of<DT>(raw[j]);
+        ya[j] = y_approx(xj, cap, inv_cap, scale, inv_t);
         if (j < nvalid) {
-            kmax = g4s_max_u(kmax, f2key(x[j]));
-            amax = g4s_max_u(amax, f2key(__builtin_fabsf(x[j])));
+            kmax = g4s_max_u(kmax, f2key(xj));
+            amax = g4s_max_u(amax, __float_as_uint(xj) & 0x7FFFFFFFu);
             ymk = g4s_max_u(ymk, f2key(ya[j]));
         }
     }
-    kmax = block_max_key(kmax, sh, 0);
-    amax = block_max_key(amax, sh, 1);
-    ymk = block_max_key(ymk, sh, 2);
+    /* the three maxima in one LDS exchange */
+    {
+        const int lane = tid & 63, wid = tid >> 6;
+        kmax = wave_max_u32(kmax);
+        amax = wave_max_u32(amax);
+        ymk = wave_max_u32(ymk);
+        if (lane == 0) {
+            sh.ured[wid] = kmax;
+            sh.ured[NWF + wid] = amax;
+            sh.ured[2 * NWF + wid] = ymk;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < NWF; ++w) {
+            kmax = g4s_max_u(kmax, sh.ured[w]);
+            amax = g4s_max_u(amax, sh.ured[NWF + w]);
+            ymk = g4s_max_u(ymk, sh.ured[2 * NWF + w]);
+        }
+    }
     const float ymax = key2f(ymk);
+    const float lg2e_ymax = ymax * 1.4426950408889634f;
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j)
-        if (j < nvalid) s += __expf(ya[j] - ymax);
-    s = block_sum_f(s, sh);
+        if (j < nvalid) s += __builtin_amdgcn_exp2f(ya[j] * 1.4426950408889634f - lg2e_ymax);
+    s = wave_sum_f32(s);
+    if ((tid & 63) == 0) sh.fred[tid >> 6] = s;
+    __syncthreads();
+    s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWF; ++w) s += sh.fred[w];
     FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
     if (tid == 0) {
-        rc[b].maxkey = kmax;
-        rc[b].ymax = ymax;
-        rc[b].sapx = s;
-        rc[b].pad = (int32_t)amax;
+        uint64_t* w = reinterpret_cast<uint64_t*>(&rc[b]);
+        st_dev(w, ((uint64_t)amax << 32) | kmax);
+        st_dev(w + 1, ((uint64_t)__float_as_uint(s) << 32) | __float_as_uint(ymax));
     }
     if (!last_of_row(a.ws.tickets + (int64_t)row * 4 + 0, (uint32_t)a.nch, sh)) return;
 
@@ -465,9 +542,10 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
      * entering every chunk */
     const int nch = a.nch;
     uint32_t km = 0u, am = 0u;
-    if (tid < nch) {
-        km = rc[tid].maxkey;
-        am = (uint32_t)rc[tid].pad;
+    for (int c = tid; c < nch; c += kFullBlock) {
+        const uint64_t w = ld_dev(reinterpret_cast<const uint64_t*>(&rc[c]));
+        km = g4s_max_u(km, (uint32_t)w);
+        am = g4s_max_u(am, (uint32_t)(w >> 32));
     }
     km = block_max_key(km, sh, 0);
     am = block_max_key(am, sh, 1);
@@ -478,9 +556,10 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
         for (int c = 0; c < nch; ++c) {
             rc[c].beta_l = ss::state_of((float)pre).e;
             /* a prediction only: chunks without a finite estimate add 0 */
-            double z = (double)rc[c].ymax - (double)m;
+            const uint64_t w = ld_dev(reinterpret_cast<const uint64_t*>(&rc[c]) + 1);
+            double z = (double)__uint_as_float((uint32_t)w) - (double)m;
             z = z > 50.0 ? 50.0 : (z < -700.0 ? -700.0 : z);
-            const double d = (double)rc[c].sapx * exp_fast_d(z);
+            const double d = (double)__uint_as_float((uint32_t)(w >> 32)) * exp_fast_d(z);
             pre += (d >= 0.0 && d < 1e300) ? d : 0.0;
         }
         FullRow r;
@@ -492,7 +571,7 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
         /* table window: the 16 binades of |x| below and at the largest one */
         int win = -1;
         if (DT == 1) {
-            const int eb = (int)((__float_as_uint(key2f(am)) >> 23) & 0xFFu);
+            const int eb = (int)((am >> 23) & 0xFFu); /* am: bits of the largest |x| */
             win = eb - 15 < 0 ? 0 : eb - 15;
         }
         r.win_lo = win;
@@ -538,15 +617,19 @@ __device__ __forceinline__ Ctx load_ctx(const FullArgs& a, int row, const FullRo
     c.scale = r.scale;
     c.win_lo = r.win_lo;
     if (DT == 1 && r.win_lo >= 0) {
-        const float4 v = reinterpret_cast<const float4*>(a.ws.etab + (int64_t)row * kFullTab)
-            [threadIdx.x];
-        reinterpret_cast<float4*>(sh.tab)[threadIdx.x] = v;
+        const float4* src = reinterpret_cast<const float4*>(a.ws.etab + (int64_t)row * kFullTab);
+        float4 v[kFullTab / 4 / kFullBlock];
+#pragma unroll
+        for (int q = 0; q < kFullTab / 4 / kFullBlock; ++q) v[q] = src[threadIdx.x + q * kFullBlock];
+#pragma unroll
+        for (int q = 0; q < kFullTab / 4 / kFullBlock; ++q)
+            reinterpret_cast<float4*>(sh.tab)[threadIdx.x + q * kFullBlock] = v[q];
     }
     __syncthreads();
     return c;
 }
 
-/* ------------------------------------------------------------ 3: lsum */
+/* ------------------------------------------------- 3: lsum chunk maps */
 
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
@@ -563,16 +646,15 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
     const FullRow r = a.ws.rows[row];
     const Ctx c = load_ctx<DT>(a, row, r, sh);
 
-    float x[kFullPer];
-    uint32_t code[kFullPer];
+    uint32_t raw[kFullPer];
     const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
-    const int nvalid = load16<DT>(rowp, e0, V, x, code);
+    const int nvalid = load16<DT>(rowp, e0, V, raw);
     float t[kFullPer];
     double dsum = 0.0;
     uint32_t first1 = 0xFFFFFFFFu;
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j) {
-        t[j] = (j < nvalid) ? e_of<DT>(x[j], code[j], c, sh.tab) : 0.0f;    /* Tensors.pas:660 */
+        t[j] = (j < nvalid) ? e_of<DT>(raw[j], c, sh.tab) : 0.0f;      /* Tensors.pas:660 */
         dsum += (double)t[j];
         if (j < nvalid && t[j] == 1.0f && first1 == 0xFFFFFFFFu) first1 = (uint32_t)(e0 + j);
     }
@@ -584,36 +666,69 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
         rc[b].de = dsum;
         rc[b].first1 = (int32_t)first1;
     }
-    if (!last_of_row(a.ws.tickets + (int64_t)row * 4 + 1, (uint32_t)a.nch, sh)) return;
+}
 
-    /* ---- LSum: chain the chunk maps left to right (Tensors.pas:657-663) */
+/* ------------------------------------------------------- 4: LSum chain */
+
+/* One workgroup per row: LSum by chaining the chunk maps left to right
+ * (Tensors.pas:657-663), re-evaluating the chunks whose map does not apply;
+ * then 1/LSum, the argmax, and the predictions for the draw. */
+template <int DT>
+__global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
+{
+    __shared__ FullShared sh;
+    const int tid = threadIdx.x;
+    const int row = blockIdx.y;
+    const int V = a.vocab;
+    const RowIn ri = row_in(a, row);
+    if (!is_full_row(ri.p.top_k, V)) return;
+    const char* rowp = reinterpret_cast<const char*>(a.logits) +
+                       (int64_t)row * a.row_stride * Elem<DT>::SIZE;
+    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
+    const FullRow r = a.ws.rows[row];
     const int nch = a.nch;
-    if (tid < nch) {
-        sh.cmap[tid] = rc[tid].lmap;
-        sh.cbeta[tid] = rc[tid].beta_l;
+    for (int cb = tid; cb < nch; cb += kFullBlock) {
+        sh.cmap[cb] = rc[cb].lmap;
+        sh.cbeta[cb] = rc[cb].beta_l;
     }
-    __syncthreads();
+    if (tid == 0) sh.misc[12] = 0;
+    const Ctx c = load_ctx<DT>(a, row, r, sh); /* ends with a barrier */
+
+    uint32_t raw[kFullPer];
+    float t[kFullPer];
     State st = ss::state_of(0.0f);
+    int reev = 0;
     for (int cb = 0; cb < nch; ++cb) {
-        if (st.e == sh.cbeta[cb]) {
+        if (cb > 0 && st.e == sh.cbeta[cb]) {
             const int32_t m2 = ss::map_apply(sh.cmap[cb], st.m);
             if (m2 < ss::kTop) {
                 st.m = m2;
                 continue;
             }
         }
+        ++reev;
         const int64_t f0 = (int64_t)cb * kFullChunk + (int64_t)tid * kFullPer;
-        const int nv = load16<DT>(rowp, f0, V, x, code);
+        const int nv = load16<DT>(rowp, f0, V, raw);
 #pragma unroll
-        for (int j = 0; j < kFullPer; ++j) t[j] = (j < nv) ? e_of<DT>(x[j], code[j], c, sh.tab) : 0.0f;
+        for (int j = 0; j < kFullPer; ++j) t[j] = (j < nv) ? e_of<DT>(raw[j], c, sh.tab) : 0.0f;
+        int pos = 0;
+        if (cb == 0) {
+            head_walk(t, __builtin_inff(), sh);
+            __syncthreads();
+            st.e = sh.misc[9];
+            st.m = sh.misc[10];
+            __syncthreads();
+            pos = kHead / kFullPer;
+        }
         int h;
-        st = resolve_chunk(t, nv, st, __builtin_inff(), &h, sh);
+        st = resolve_chunk(t, nv, st, __builtin_inff(), pos, &h, sh);
     }
     const float lsum = ss::value_of(st);
     const float inv = div_cr32(1.0f, lsum);                            /* Tensors.pas:668 */
     /* argmax of p: p = fl32(e * inv) <= inv with equality exactly at e == 1
      * (the next float below 1 gives a p below inv), so the first e == 1 */
-    uint32_t f1 = tid < nch ? (uint32_t)rc[tid].first1 : 0xFFFFFFFFu;
+    uint32_t f1 = 0xFFFFFFFFu;
+    for (int cb = tid; cb < nch; cb += kFullBlock) f1 = g4s_min_u(f1, (uint32_t)rc[cb].first1);
     f1 = block_min_u(f1, sh);
     const int32_t argmax = (int32_t)f1;                                 /* Model.pas:2712-2721 */
     const float T = ri.p.temperature;
@@ -646,11 +761,15 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
         w.argmax = argmax;
         w.c_last = all ? nch - 1 : last;
         w.nodraw = nodraw ? 1 : 0;
+        w.l_reev = reev;
+        w.l_rounds = sh.misc[12];
+        w.c_reev = 0;
+        w.c_rounds = 0;
         a.ws.rows[row] = w;
     }
 }
 
-/* ------------------------------------------------------------ 4: cdf */
+/* -------------------------------------------------- 5: draw chunk maps */
 
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
@@ -669,14 +788,13 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
     const Ctx c = load_ctx<DT>(a, row, r, sh);
     const float inv = r.inv;
 
-    float x[kFullPer];
-    uint32_t code[kFullPer];
+    uint32_t raw[kFullPer];
     const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
-    const int nvalid = load16<DT>(rowp, e0, V, x, code);
+    const int nvalid = load16<DT>(rowp, e0, V, raw);
     float t[kFullPer];
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j)
-        t[j] = (j < nvalid) ? e_of<DT>(x[j], code[j], c, sh.tab) * inv : 0.0f; /* Tensors.pas:671 */
+        t[j] = (j < nvalid) ? e_of<DT>(raw[j], c, sh.tab) * inv : 0.0f; /* Tensors.pas:671 */
     if (a.out.probs && a.out.capacity >= V) {
         float* po = a.out.probs + (int64_t)row * a.out.capacity;
         int32_t* io = a.out.indices ? a.out.indices + (int64_t)row * a.out.capacity : nullptr;
@@ -685,44 +803,86 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
             if (io) io[e0 + j] = (int32_t)(e0 + j);
         }
     }
+    if (r.nodraw) return;
     const PMap cm = block_chunk_map(thread_map(t, nvalid, rc[b].beta_c), sh);
     if (tid == 0) rc[b].cmap = cm;
-    if (!last_of_row(a.ws.tickets + (int64_t)row * 4 + 2, (uint32_t)(r.c_last + 1), sh)) return;
+}
 
+/* -------------------------------------------------------- 6: the draw */
+
+/* One workgroup per row: the first index whose left-to-right binary32
+ * running sum of p reaches thr (Model.pas:2727-2735), else the argmax. */
+template <int DT>
+__global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
+{
+    __shared__ FullShared sh;
+    const int tid = threadIdx.x;
+    const int row = blockIdx.y;
+    const int V = a.vocab;
+    const RowIn ri = row_in(a, row);
+    if (!is_full_row(ri.p.top_k, V)) return;
+    const FullRow r = a.ws.rows[row];
+    if (r.c_last < 0) return;
     if (r.nodraw) {
         if (tid < 64) write_row_outputs(a, row, r.argmax, r.argmax, r.lsum, G4S_FLAG_FULL_PATH);
         return;
     }
-    /* ---- the draw: first index whose running sum of p reaches thr
-     * (Model.pas:2727-2735) */
+    const char* rowp = reinterpret_cast<const char*>(a.logits) +
+                       (int64_t)row * a.row_stride * Elem<DT>::SIZE;
+    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
     const int nch = a.nch;
-    if (tid < nch) {
-        sh.cmap[tid] = tid <= r.c_last ? rc[tid].cmap : ss::map_identity();
-        sh.cbeta[tid] = tid <= r.c_last ? rc[tid].beta_c : -1;
+    for (int cb = tid; cb < nch; cb += kFullBlock) {
+        sh.cmap[cb] = cb <= r.c_last ? rc[cb].cmap : ss::map_identity();
+        sh.cbeta[cb] = cb <= r.c_last ? rc[cb].beta_c : -1;
     }
-    __syncthreads();
+    if (tid == 0) sh.misc[12] = 0;
+    const Ctx c = load_ctx<DT>(a, row, r, sh); /* ends with a barrier */
+    const float inv = r.inv;
     const float thr = r.thr;
+
+    uint32_t raw[kFullPer];
+    float t[kFullPer];
     State st = ss::state_of(0.0f);
     int64_t hit = -1;
+    int reev = 0;
     for (int cb = 0; cb < nch; ++cb) {
-        if (st.e == sh.cbeta[cb]) {
+        if (cb > 0 && st.e == sh.cbeta[cb]) {
             const int32_t m2 = ss::map_apply(sh.cmap[cb], st.m);
             if (m2 < ss::kTop && ss::value_of(State{st.e, m2}) < thr) {
                 st.m = m2;
                 continue;
             }
         }
+        ++reev;
         const int64_t f0 = (int64_t)cb * kFullChunk + (int64_t)tid * kFullPer;
-        const int nv = load16<DT>(rowp, f0, V, x, code);
+        const int nv = load16<DT>(rowp, f0, V, raw);
 #pragma unroll
         for (int j = 0; j < kFullPer; ++j)
-            t[j] = (j < nv) ? e_of<DT>(x[j], code[j], c, sh.tab) * inv : 0.0f;
+            t[j] = (j < nv) ? e_of<DT>(raw[j], c, sh.tab) * inv : 0.0f;
+        int pos = 0;
+        if (cb == 0) {
+            head_walk(t, thr, sh);
+            __syncthreads();
+            st.e = sh.misc[9];
+            st.m = sh.misc[10];
+            const int hh = sh.misc[11];
+            __syncthreads();
+            if (hh >= 0) {
+                hit = hh;
+                break;
+            }
+            pos = kHead / kFullPer;
+        }
         int h;
-        st = resolve_chunk(t, nv, st, thr, &h, sh);
+        st = resolve_chunk(t, nv, st, thr, pos, &h, sh);
         if (h >= 0) {
             hit = (int64_t)cb * kFullChunk + h;
             break;
         }
+    }
+    if (tid == 0) {
+        a.ws.rows[row].c_reev = reev;
+        a.ws.rows[row].c_rounds = sh.misc[12];
     }
     uint32_t flags = G4S_FLAG_FULL_PATH | G4S_FLAG_DREW;
     int32_t id = r.argmax;
@@ -773,8 +933,11 @@ static hipError_t launch_dt(const FullArgs& a, hipStream_t s)
     if (DT == 1)
         hipLaunchKernelGGL(full_table_kernel, dim3(kFullTab / kFullBlock, (unsigned)a.batch),
                            dim3(kFullBlock), 0, s, a);
+    const dim3 rows(1u, (unsigned)a.batch);
     hipLaunchKernelGGL((full_lsum_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_lsum_chain_kernel<DT>), rows, dim3(kFullBlock), 0, s, a);
     hipLaunchKernelGGL((full_cdf_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_cdf_chain_kernel<DT>), rows, dim3(kFullBlock), 0, s, a);
     return hipGetLastError();
 }
 

@@ -272,8 +272,8 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
                 const uint32_t k = keys[j * VW + q];
                 if (k >= theta) {
                     if (pos < cap)
-                        gcand[pos] =
-                            cand_pack(k, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q));
+                        st_dev(&gcand[pos],
+                               cand_pack(k, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q)));
                     ++pos;
                 }
             }
@@ -305,7 +305,8 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
             for (int q = 0; q < VW; ++q) {
                 const uint32_t k = keys[j * VW + q];
                 if (k > tau_c) {
-                    gcand[goff] = cand_pack(k, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q));
+                    st_dev(&gcand[goff],
+                           cand_pack(k, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q)));
                     ++goff;
                 }
             }
@@ -325,8 +326,9 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
             for (int q = 0; q < VW; ++q) {
                 if (keys[j * VW + q] == tau_c) {
                     if (taken + r < want)
-                        gcand[base + taken + r] = cand_pack(
-                            tau_c, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q));
+                        st_dev(&gcand[base + taken + r],
+                               cand_pack(tau_c,
+                                         (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q)));
                     ++r;
                 }
             }
@@ -337,27 +339,13 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         rec_mode_e = 0x80000000u | (uint32_t)eq_c;
     }
     if (tid == 0) {
-        ChunkRec r;
-        r.count = (uint32_t)emitted;
-        r.bound = rec_bound;
-        r.rc = rc;
-        r.mode_e = rec_mode_e;
-        a.recs[(int64_t)row * kMaxSplits + chunk] = r;
+        uint64_t* rp64 = reinterpret_cast<uint64_t*>(a.recs + (int64_t)row * kMaxSplits + chunk);
+        st_dev(rp64, ((uint64_t)rec_bound << 32) | (uint32_t)emitted);
+        st_dev(rp64 + 1, ((uint64_t)rec_mode_e << 32) | rc);
     }
 
     /* ----------------------------------------------- last workgroup elects */
-    /* release this chunk's slots and record; only the elected workgroup
-     * acquires (an acquire at agent scope invalidates the XCD's L2) */
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.tickets[row], 1u);
-        sh.flag_last = (prev == (uint32_t)(S - 1));
-    }
-    __syncthreads();
-    if (!sh.flag_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (tid == 0) a.tickets[row] = 0u;
+    if (!elect_last(&a.tickets[row], (uint32_t)S, &sh.flag_last)) return;
 
     /* ------------------------------------------------------------ merge */
     uint32_t flags = G4S_FLAG_TOPK_PATH;
@@ -367,12 +355,22 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 
     /* one round trip: the chunk records and the first batch of slots (the
      * index is clamped instead of branched on, so every load is issued) */
-    if (tid < S) sh.rec[tid] = a.recs[(int64_t)row * kMaxSplits + tid];
+    if (tid < S) {
+        const uint64_t* rp64 =
+            reinterpret_cast<const uint64_t*>(a.recs + (int64_t)row * kMaxSplits + tid);
+        const uint64_t w0 = ld_dev(rp64), w1 = ld_dev(rp64 + 1);
+        ChunkRec r;
+        r.count = (uint32_t)w0;
+        r.bound = (uint32_t)(w0 >> 32);
+        r.rc = (uint32_t)w1;
+        r.mode_e = (uint32_t)(w1 >> 32);
+        sh.rec[tid] = r;
+    }
     uint64_t v[kBatchLoads];
 #pragma unroll
     for (int i = 0; i < kBatchLoads; ++i) {
         const int f = tid + i * BLOCK;
-        v[i] = rcand[f < span ? f : span - 1];
+        v[i] = ld_dev(&rcand[f < span ? f : span - 1]);
     }
     __syncthreads();
     uint32_t lb, lr;
@@ -419,7 +417,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 #pragma unroll
             for (int i = 0; i < kBatchLoads; ++i) {
                 const int f = b0 + tid + i * BLOCK;
-                v[i] = rcand[f < span ? f : span - 1];
+                v[i] = ld_dev(&rcand[f < span ? f : span - 1]);
             }
         }
         int cnt = 0;
