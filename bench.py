@@ -40,6 +40,20 @@ SEED = 4242
 V = 262144
 
 
+def profiled_traffic():
+    """HBM bytes per launch of the B=1 top-k kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the calibration copy),
+    or None when the summary is absent."""
+    import re
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_counters.md")
+    try:
+        with open(path) as f:
+            m = re.search(r"traffic_bytes_per_launch = (\d+)", f.read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -58,6 +72,7 @@ def harness():
     H.g4h_null_roundtrip.argtypes = [vp, i32, i32, vp]
     H.g4h_batch_throughput.argtypes = [vp, vp, vp, i32, i64, i32, vp, vp, i32, i32, vp, i32,
                                        i32, vp, vp, vp]
+    H.g4h_copy_throughput.argtypes = [vp, vp, vp, i64, i32, vp]
     return H
 
 
@@ -112,6 +127,69 @@ def check_decode_ids(rows0, ids, threads, time_rows):
     return bad, np.asarray(lat)
 
 
+def check_full_rows(seed, batch, params, u, ids, threads):
+    """Full-vocabulary rows against the CPU oracle: (mismatching ids, draws
+    whose threshold lies within 1e-6 of a running-sum boundary)."""
+    from concurrent.futures import ThreadPoolExecutor
+    from gemma4_sampler import workload as wl
+    from oracle import oracle as orc
+    b16 = wl.host_flat_bf16_rows(seed, 0, batch, V)
+    rows = (b16.astype(np.uint32) << 16).view(np.float32)
+    t, k, p = params
+
+    def one(r):
+        tok, det, _, _ = orc.do_sample(rows[r], t[r], k[r], p[r], u[r],
+                                       softcap=wl.SOFTCAP_GEMMA4, want_probs=False)
+        near = False
+        if det["drew"] and det["reached"]:
+            th = det["threshold"]
+            lo = th - det["cum_prev"] if det["chosen_pos"] > 0 else np.inf
+            near = min(lo, det["cum_at"] - th) < 1e-6
+        return int(tok != ids[r]), int(near)
+
+    with ThreadPoolExecutor(threads) as ex:
+        res = list(ex.map(one, range(batch)))
+    return sum(a for a, _ in res), sum(b for _, b in res)
+
+
+def probe(H, stream, name, steps):
+    """One workload alone, `steps` launches, for hardware-counter runs:
+    copy (128 MiB calibration copy), topk1 (top-k path B=1 fp32),
+    full256 (full path B=256 bf16)."""
+    from gemma4_sampler import hip, native, workload as wl
+    if name == "copy":
+        nbytes = 128 << 20
+        a, b = hip.Buffer(nbytes), hip.Buffer(nbytes)
+        us = np.zeros(steps, np.float32)
+        rc = H.g4h_copy_throughput(stream.handle, a.ptr, b.ptr, nbytes, steps, _vp(us))
+        if rc != 0:
+            raise RuntimeError(f"g4h_copy_throughput failed: {rc}")
+        res = {"probe": name, "bytes_read": nbytes, "bytes_written": nbytes,
+               "us_median": float(np.median(us))}
+    elif name == "topk1":
+        d = hip.Buffer(V * 4)
+        wl.dev_peaky_rows(d, SEED, 0, 1, V, stream=stream)
+        stream.synchronize()
+        us, _, _, _ = batch_throughput(H, stream, d, native.DTYPE_F32, 1,
+                                       [native.TSamplingParams.make(0.7, 64, 0.95)], [0.5], 64,
+                                       0, 10, steps)
+        res = {"probe": name, "bytes_read": V * 4, "us_median": float(np.median(us))}
+    elif name == "full256":
+        B = 256
+        d = hip.Buffer(B * V * 2)
+        wl.dev_flat_bf16_rows(d, SEED + 4, 0, B, V, stream=stream)
+        stream.synchronize()
+        t, k, p = wl.flat_params(B)
+        par = [native.TSamplingParams.make(a, b, c) for a, b, c in zip(t, k, p)]
+        us, _, _, _ = batch_throughput(H, stream, d, native.DTYPE_BF16, B, par,
+                                       wl.host_row_u(SEED + 4, 0, B), 0, 1, 2, steps)
+        res = {"probe": name, "bytes_read": B * V * 2, "us_median": float(np.median(us))}
+    else:
+        raise ValueError(f"unknown probe {name}")
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def batch_throughput(H, stream, d_logits, dtype, batch, params, u, k_bound, full_rows, warmup,
                      steps):
     from gemma4_sampler import hip, native, workload as wl
@@ -143,6 +221,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=10000)
     ap.add_argument("--batch-steps", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="small run for profiling")
+    ap.add_argument("--probe", choices=["copy", "topk1", "full256"],
+                    help="run one workload alone (for hardware-counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the sampler is a single-GPU path (rows are "
@@ -158,6 +238,8 @@ def main():
         raise RuntimeError("no HIP device: the sampler has no CPU path")
     stream = hip.Stream()
     threads = min(16, os.cpu_count() or 1)
+    if args.probe:
+        return probe(H, stream, args.probe, min(args.steps, 200))
 
     # ---- host floor of a synchronous single-kernel call --------------------
     floor = {}
@@ -230,10 +312,13 @@ def main():
                                              10, args.batch_steps)
         med4 = float(np.median(s4_us))
         gbps4 = B4 * V * 2 / (med4 * 1e-6) / 1e9
+        bad4, nb4 = check_full_rows(SEED + 4, B4, (t4, k4, p4), u4, ids4, threads)
         b256 = {"batch": B4, "dtype": "bf16", "us_per_batch_p50": med4,
                 "rows_per_s": B4 / (med4 * 1e-6), "hbm_gbps": gbps4,
-                "frac_hbm": gbps4 / HBM_PEAK_GBPS}
-        log(f"B=256 bf16 full path: {med4:.2f} us/batch, {gbps4:.0f} GB/s")
+                "frac_hbm": gbps4 / HBM_PEAK_GBPS, "id_mismatches": bad4,
+                "boundary_draws": nb4}
+        log(f"B=256 bf16 full path: {med4:.2f} us/batch, {gbps4:.0f} GB/s, mismatches {bad4}, "
+            f"boundary draws {nb4}")
         d4.free()
     except (native.SamplerError, RuntimeError) as e:
         b256["status"] = f"not available: {e}"
@@ -276,14 +361,14 @@ def main():
         "null_kernel_roundtrip": floor,
         "roofline": {"bound": "hbm", "kernel": "topk_kernel (B=1)", "achieved": achieved,
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
-                     "traffic": None, "kernel_us_mean": k_mean, "kernel_us_median": k_med,
+                     "traffic": profiled_traffic(), "kernel_us_mean": k_mean, "kernel_us_median": k_med,
                      "algorithmic_bytes": algo_bytes},
         "b64_mixed": b64,
         "b256_flat_full": b256,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
-    return 0 if (bad + bad_async + bad3) == 0 else 1
+    return 0 if (bad + bad_async + bad3 + b256.get("id_mismatches", 0)) == 0 else 1
 
 
 if __name__ == "__main__":

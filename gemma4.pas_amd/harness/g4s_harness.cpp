@@ -10,6 +10,7 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdint>
 #include <cstring>
@@ -216,6 +217,52 @@ G4H_API int g4h_batch_throughput(g4s_sampler* s, void* stream, const void* d_log
         *total_us = ms * 1000.0f;
         *wall_us = t1 - t0;
     }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    return rc;
+}
+
+namespace {
+
+/* Plain streaming copy, 16 bytes per lane per step: the calibration kernel
+ * for HBM traffic counters (its bytes read and written are known exactly). */
+__global__ void g4h_copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = src[i];
+}
+
+}  // namespace
+
+/*
+ * `steps` launches of the calibration copy of `bytes` (a multiple of 16)
+ * from src to dst on `stream`; us[i] = event time of launch i.
+ */
+G4H_API int g4h_copy_throughput(void* stream, const void* src, void* dst, int64_t bytes,
+                                int32_t steps, float* us)
+{
+    hipStream_t st = (hipStream_t)stream;
+    if (bytes <= 0 || (bytes & 15) || steps <= 0) return -1;
+    const int64_t n = bytes / 16;
+    std::vector<hipEvent_t> ev((size_t)steps + 1);
+    for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) return -100;
+    int rc = 0;
+    const int grid = (int)std::min<int64_t>((n + 255) / 256, 4096);
+    (void)hipEventRecord(ev[0], st);
+    for (int32_t i = 0; i < steps && rc == 0; ++i) {
+        hipLaunchKernelGGL(g4h_copy_kernel, dim3(grid), dim3(256), 0, st, (const uint4*)src,
+                           (uint4*)dst, n);
+        if (hipGetLastError() != hipSuccess) rc = -102;
+        (void)hipEventRecord(ev[(size_t)i + 1], st);
+    }
+    if (hipStreamSynchronize(st) != hipSuccess && rc == 0) rc = -104;
+    if (rc == 0)
+        for (int32_t i = 0; i < steps; ++i) {
+            float ms = 0.0f;
+            (void)hipEventElapsedTime(&ms, ev[(size_t)i], ev[(size_t)i + 1]);
+            us[i] = ms * 1000.0f;
+        }
     for (auto& e : ev) (void)hipEventDestroy(e);
     return rc;
 }
