@@ -1,5 +1,7 @@
 /*
- * g4s_full.h -- launch interface of the full-vocabulary path (g4s_full.hip).
+ * g4s_full.h -- launch interface of the softmax-path kernels (g4s_full.hip):
+ * full-vocabulary rows (TopK <= 0 or TopK >= V) and wide top-k rows
+ * (g4s_max_top_k() < TopK < V).
  */
 #ifndef G4S_FULL_H
 #define G4S_FULL_H
@@ -14,8 +16,15 @@ constexpr int kFullPer = 16;                        /* consecutive terms per thr
 constexpr int kFullChunk = kFullBlock * kFullPer;   /* terms per chunk */
 constexpr int kFullMaxChunks = 1024;                /* chunks per row: vocab <= 2^22 */
 constexpr int kFullTab = 4096;                      /* bf16 codes with a tabulated e */
+constexpr int kFullCPW = 4;                         /* chunks per workgroup, lsum/cdf passes */
+constexpr int kNear = 8;  /* e = 1 - j*2^-24 (j < kNear): the values whose p can tie the
+                             largest p under the top-k tail's division */
+constexpr int kWideBins = 2048;                     /* radix-select histogram bins */
 
-/* Per-row state shared by the four kernels (device workspace). */
+/* Row classes (DoSample's dispatch, src/Gemma4.Model.pas:2756). */
+enum : int32_t { kRowTopk = 0, kRowFull = 1, kRowWide = 2 };
+
+/* Per-row state shared by the kernels (device workspace). */
 struct FullRow {
     uint32_t maxkey;  /* order-preserving key of the largest raw logit */
     uint32_t amax;    /* largest |logit| as a key of |x| */
@@ -29,37 +38,72 @@ struct FullRow {
     int32_t argmax;   /* first index of the largest p */
     int32_t c_last;   /* last chunk the draw kernel visits, -1: none */
     int32_t nodraw;   /* T <= 0: the greedy choice, no draw (probabilities still written) */
+    int32_t count;    /* terms that take part: V, or the wide row's survivors */
+    int32_t first;    /* index of the first term that takes part */
+    int32_t near[kNear]; /* first index with e == 1 - j*2^-24 (atomic min), INT_MAX: none */
     /* diagnostics: chunks re-evaluated and re-evaluation rounds, LSum chain
      * then draw chain */
     int32_t l_reev, l_rounds, c_reev, c_rounds;
 };
 
-/* Per-chunk records.  Fields exchanged between workgroups of one launch are
- * aligned 64-bit words written and read with device-coherent accesses. */
+/* Per-chunk records. */
 struct FullChunk {
-    uint32_t maxkey;  /* max kernel: chunk's largest key          } word 0 */
-    uint32_t amax;    /* max kernel: largest |x| as a key          }        */
-    float ymax;       /* approximate y at the chunk's largest logit } word 1 */
-    float sapx;       /* approximate sum of exp(y - ymax)           }        */
-    ss::PMap lmap;    /* lsum kernel: the chunk's terms in beta_l     word 2 */
-    ss::PMap cmap;    /* draw kernel: the chunk's p in beta_c         word 3 */
-    double de;        /* lsum kernel: sum of the chunk's e in binary64  word 4 */
-    int32_t first1;   /* lsum kernel: first index with e == 1, or INT_MAX */
+    uint32_t maxkey;  /* max kernel: chunk's largest key */
+    uint32_t amax;    /* max kernel: largest |x| as a key */
+    float ymax;       /* approximate y at the chunk's largest logit */
+    float sapx;       /* approximate sum of exp(y - ymax) over the terms taking part */
+    ss::PMap lmap;    /* lsum kernel: the chunk's terms in beta_l */
+    ss::PMap cmap;    /* draw kernel: the chunk's p in beta_c */
+    double de;        /* lsum kernel: sum of the chunk's e in binary64 */
     int32_t beta_l;   /* predicted binade of LSum entering the chunk */
     int32_t beta_c;   /* predicted binade of the running sum entering the chunk */
-    int32_t pad[3];
+    int32_t nsurv;    /* max kernel: terms of the chunk taking part */
+    int32_t fsurv;    /* max kernel: first index taking part, INT_MAX: none */
+    int32_t soff;     /* LSum chain: terms taking part before the chunk */
+    int32_t pad;
+};
+static_assert(sizeof(FullChunk) == 64, "FullChunk layout");
+
+/* Radix select of a wide row's K-th largest key and its tie resolution. */
+struct WideSel {
+    uint32_t prefix;  /* key digits fixed so far */
+    int32_t krem;     /* rank still to find among keys with that prefix */
+    int32_t state;    /* kSel* */
+    uint32_t tau;     /* the K-th largest key */
+    int32_t need;     /* copies of tau that survive */
+    int32_t eq;       /* copies of tau in the row */
+    int32_t idx_thr;  /* lowest-index rule: copies with index <= idx_thr survive */
+    int32_t count;    /* survivors */
+};
+enum : int32_t {
+    kSelSearch = 0,   /* digits being fixed */
+    kSelAll = 1,      /* every key >= tau survives */
+    kSelTies = 2,     /* tau tied beyond the remaining slots: resolution pending */
+    kSelLowest = 3,   /* the first `need` copies of tau in index order survive */
+    kSelReplay = 4,   /* the min-heap decides: replay pending */
+    kSelBits = 5,     /* the surviving copies of tau are marked in the row's bitmask */
+    kSelEmpty = 6     /* no logit above -1e30 */
 };
 
-static_assert(sizeof(FullChunk) == 64, "FullChunk layout");
-static_assert(__builtin_offsetof(FullChunk, ymax) == 8 && __builtin_offsetof(FullChunk, lmap) == 16 &&
-                  __builtin_offsetof(FullChunk, cmap) == 24 && __builtin_offsetof(FullChunk, de) == 32,
-              "FullChunk words");
+struct TieRec {
+    int32_t cge;      /* keys >= tau in the chunk */
+    int32_t ceq;      /* keys == tau in the chunk */
+    int32_t maxgt;    /* last index with key > tau, -1: none */
+    int32_t pad;
+};
 
 struct FullWorkspace {
     FullRow* rows = nullptr;     /* [max_batch] */
     FullChunk* chunks = nullptr; /* [max_batch][kFullMaxChunks] */
     float* etab = nullptr;       /* [max_batch][kFullTab] */
-    uint32_t* tickets = nullptr; /* [max_batch][4], zero between launches */
+    /* wide rows */
+    WideSel* sel = nullptr;      /* [max_batch] */
+    uint32_t* hist = nullptr;    /* [max_batch][kWideBins], zero between launches */
+    TieRec* ties = nullptr;      /* [max_batch][kFullMaxChunks] */
+    uint32_t* bits = nullptr;    /* [max_batch][ceil(vocab/32)] surviving tied copies */
+    float* heap_v = nullptr;     /* [vocab] replay heap (one row at a time) */
+    int32_t* heap_i = nullptr;   /* [vocab] */
+    int32_t bits_stride = 0;     /* words per row of `bits` */
 };
 
 struct FullArgs {
@@ -73,6 +117,7 @@ struct FullArgs {
     double u0;
     float softcap;
     int32_t nch;
+    int32_t wide_on;  /* wide rows are handled by this launch */
     FullWorkspace ws;
     int32_t* ids;
     uint32_t* done;

@@ -1,8 +1,8 @@
 /*
- * g4s_full.hip -- the full-vocabulary sampling path on gfx950
- * (rows with TopK <= 0 or TopK >= V).
+ * g4s_full.hip -- the softmax sampling path on gfx950: full-vocabulary rows
+ * (TopK <= 0 or TopK >= V) and wide top-k rows (g4s_max_top_k() < TopK < V).
  *
- * Replaces the TopK <= 0 branch of DoSample with CpuLogitSoftcap,
+ * Full rows replace the TopK <= 0 branch of DoSample with CpuLogitSoftcap,
  * DoSampleTopP and CpuSoftmaxF32 (src/Gemma4.Model.pas:2756-2763,
  * 2691-2737; src/Gemma4.Layers.pas:300-316; src/Gemma4.Tensors.pas:638-673):
  *   y_i = RN32(tanh(x_i * fl32(1/cap)) * cap)      (when cap > 0)
@@ -12,23 +12,41 @@
  *   index of the largest p;  if T > 0: the first i whose left-to-right
  *   binary32 running sum of p reaches fl32(u * TopP), else the argmax.
  *
+ * Wide top-k rows replace DoSelectTopKIndices + the top-k tail
+ * (Model.pas:2615-2689, 2765-2826) when K is beyond what the single-launch
+ * top-k kernel holds on chip.  The survivors are found by a three-pass
+ * radix select of the K-th largest key tau over the whole row, with the
+ * reference's min-heap tie semantics (lowest index when the heap layout
+ * cannot matter, a replay of the heap otherwise).  The tail then runs on
+ * the same machinery as a full row with every non-survivor contributing 0
+ * (adding +0 leaves a binary32 running sum unchanged), the top-k forms of
+ * the arithmetic (y = RN32(cap * tanh(x / cap)), p_i = RN32(e_i / LSum)),
+ * and the first survivor as the draw when fl32(u * TopP) <= 0.
+ *
  * Rows are cut into chunks of 4096 terms, 16 consecutive terms per thread
- * of a 256-thread workgroup.  Six launches:
+ * of a 256-thread workgroup.  Launches (the wide ones only when wide rows
+ * can occur):
+ *   wide hist/find x3: 11+11+10-bit MSD radix select of tau (LDS
+ *             histograms added into a per-row histogram, one workgroup per
+ *             row fixes each digit);
+ *   wide ties, ties-find, replay: when tau is tied beyond the slots left,
+ *             per-chunk counts locate the K-th key >= tau and the last key
+ *             above tau in index order; the rare heap-dependent rows replay
+ *             the heap exactly;
  *   1 max:    raw-logit maximum (softcap and 1/T are monotone, so
- *             m = y(max x)) and approximate chunk sums of exp(y - m); the
- *             row's last workgroup (atomic ticket) turns their prefix into
- *             the predicted binade of LSum entering every chunk;
- *   2 table:  for bf16 logits, e for the 4096 codes of the 16 largest
- *             exponents of |x| (correctly rounded, once per row), so the
- *             streaming passes look e up instead of evaluating it;
+ *             m = y(max x)) and approximate chunk sums of exp(y - m);
+ *   2 row:    the row's m; for bf16 logits, e for the 4096 codes of the 16
+ *             largest exponents of |x| (correctly rounded, once per row), so
+ *             the streaming passes look e up; the predicted binade of LSum
+ *             entering every chunk (a parallel prefix of the estimates);
  *   3 lsum:   each chunk's terms as one exact map of the running sum in its
  *             predicted binade (g4s_seqsum.h), plus binary64 chunk sums;
  *   4 chain:  one workgroup per row chains the maps left to right,
  *             verifying every step and re-evaluating any chunk whose map
- *             does not apply: LSum, 1/LSum, the argmax, and the predicted
- *             binades of the draw's running sum;
- *   5 cdf:    the same maps for p, up to the chunk where the running sum is
- *             predicted to reach fl32(u*TopP);
+ *             does not apply: LSum, the argmax, and the predicted binades of
+ *             the draw's running sum;
+ *   5 cdf:    p for the outputs and the same maps for p, up to the chunk
+ *             where the running sum is predicted to reach fl32(u*TopP);
  *   6 draw:   one workgroup per row finds the exact first index and writes
  *             the token.
  * Transcendental steps are correctly rounded (g4s_crmath.h); every running
@@ -46,9 +64,70 @@ using ss::State;
 
 namespace {
 
-constexpr int NWF = kFullBlock / 64; /* waves per workgroup */
+constexpr int NWF = kFullBlock / 64;                 /* waves per workgroup */
+constexpr int CPT = kFullMaxChunks / kFullBlock;     /* chunk records per thread */
 
-__device__ __forceinline__ bool is_full_row(int K, int V) { return K <= 0 || K >= V; }
+struct RowIn {
+    g4s_params p;
+    double u;
+};
+__device__ __forceinline__ RowIn row_in(const FullArgs& a, int row)
+{
+    RowIn r;
+    r.p = a.params ? a.params[row] : a.p0;
+    r.u = a.u ? a.u[row] : a.u0;
+    return r;
+}
+
+/* DoSample's dispatch (Model.pas:2756) as this launch sees it. */
+__device__ __forceinline__ int row_class(const FullArgs& a, int K)
+{
+    if (K <= 0 || K >= a.vocab) return kRowFull;
+    if (K > kMaxTopK && a.wide_on) return kRowWide;
+    return kRowTopk;
+}
+
+/* Which terms of a row take part in the softmax: all of a full row; the
+ * survivors of a wide row. */
+struct Mask {
+    int32_t cls;
+    int32_t state;
+    uint32_t tau;
+    int32_t idx_thr;
+    const uint32_t* bits;
+};
+
+/* The row's class and mask; false when these kernels have nothing to do
+ * with the row (a top-k row, or a wide row without survivors). */
+__device__ __forceinline__ bool row_mask(const FullArgs& a, int row, const RowIn& ri, Mask& k)
+{
+    k.cls = row_class(a, ri.p.top_k);
+    k.state = kSelAll;
+    k.tau = 0u;
+    k.idx_thr = INT_MAX;
+    k.bits = nullptr;
+    if (k.cls == kRowTopk) return false;
+    if (k.cls == kRowWide) {
+        const WideSel s = a.ws.sel[row];
+        k.state = s.state;
+        k.tau = s.tau;
+        k.idx_thr = s.idx_thr;
+        k.bits = a.ws.bits + (int64_t)row * a.ws.bits_stride;
+        if (s.state == kSelEmpty) return false;
+    }
+    return true;
+}
+
+__device__ __forceinline__ bool takes_part(const Mask& k, float x, int64_t idx)
+{
+    if (k.cls == kRowFull) return true;
+    const uint32_t key = cand_key(x); /* 0: at or below -1e30, never a survivor */
+    if (key > k.tau) return true;
+    if (key != k.tau) return false;
+    if (k.state == kSelLowest) return idx <= k.idx_thr;
+    if (k.state == kSelBits) return (k.bits[idx >> 5] >> (idx & 31)) & 1u;
+    return true;
+}
 
 /* The 16 consecutive terms of one thread as raw bits: binary32 bits, or the
  * 16-bit bf16 code.  Terms at or beyond V are 0 and not counted. */
@@ -100,11 +179,22 @@ __device__ __forceinline__ float x_of(uint32_t raw)
     return DT == 0 ? __uint_as_float(raw) : __uint_as_float(raw << 16);
 }
 
-/* y = softcap(x) [* 1/T] exactly as the reference rounds it (Layers.pas:
- * 309-314, Model.pas:2703-2708). */
-__device__ __forceinline__ float y_exact(float x, float cap, float inv_cap, int scale, float inv_t)
+template <int DT>
+__device__ __forceinline__ const char* row_ptr(const FullArgs& a, int row)
 {
-    float y = (cap > 0.0f) ? softcap_full_cr32(x, inv_cap, cap) : x;
+    return reinterpret_cast<const char*>(a.logits) + (int64_t)row * a.row_stride * Elem<DT>::SIZE;
+}
+
+/* y = softcap(x) [* 1/T] exactly as the reference rounds it: the full-row
+ * form Tanh(x * fl32(1/cap)) * cap (Layers.pas:309-314) or the top-k form
+ * cap * Tanh(x / cap) (Model.pas:2776), then * fl32(1/T) (Model.pas:
+ * 2703-2708, 2780-2785). */
+__device__ __forceinline__ float y_exact(float x, int cls, float cap, float inv_cap, int scale,
+                                         float inv_t)
+{
+    float y = x;
+    if (cap > 0.0f)
+        y = cls == kRowWide ? softcap_topk_cr32(x, cap) : softcap_full_cr32(x, inv_cap, cap);
     if (scale) y = y * inv_t;
     return y;
 }
@@ -157,14 +247,14 @@ __device__ __forceinline__ int tab_index(uint32_t code, int win_lo)
 
 struct Ctx {
     float cap, inv_cap, inv_t, m;
-    int scale, win_lo;
+    int scale, win_lo, cls;
 };
 
 /* e of one term evaluated from x (kept out of line: it is the rare case for
  * bf16 logits, whose codes are tabulated). */
 __device__ __noinline__ float e_direct(float x, Ctx c)
 {
-    return exp_diff_cr32(y_exact(x, c.cap, c.inv_cap, c.scale, c.inv_t), c.m);
+    return exp_diff_cr32(y_exact(x, c.cls, c.cap, c.inv_cap, c.scale, c.inv_t), c.m);
 }
 
 /* e of one term: the table when the code is in the window, else evaluated. */
@@ -180,24 +270,53 @@ __device__ __forceinline__ float e_of(uint32_t raw, const Ctx& c, const float* t
     return e_direct(x_of<DT>(raw), c);
 }
 
+/* The e of one thread's 16 terms (0 for terms that do not take part). */
+template <int DT>
+__device__ __forceinline__ void terms_e(const uint32_t (&raw)[kFullPer], int nvalid, int64_t e0,
+                                        const Ctx& c, const Mask& k, const float* tab,
+                                        float (&t)[kFullPer])
+{
+#pragma unroll
+    for (int j = 0; j < kFullPer; ++j)
+        t[j] = (j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j)) ? e_of<DT>(raw[j], c, tab)
+                                                                        : 0.0f;
+}
+
+/* p of one term from its e: RN32(e * fl32(1/LSum)) on a full row
+ * (Tensors.pas:666-672), RN32(e / LSum) on a wide row (Model.pas:2800-2801). */
+__device__ __forceinline__ float p_of(float e, int cls, float inv, float lsum)
+{
+    return cls == kRowWide ? div_cr32(e, lsum) : e * inv;
+}
+
 /* ------------------------------------------------------ block helpers */
 
-struct FullShared {
-    float tab[kFullTab];
+struct Scratch {
     PMap wmap[NWF];
     int32_t went[NWF];
     int32_t tcand[NWF];
     uint32_t ured[3 * NWF];
     float fred[NWF];
     double dred[NWF];
+    int32_t iscan[NWF];
     int32_t misc[16];
-    int flag_last;
-    /* chain: per-chunk records of the row */
+};
+
+template <int DT>
+struct TabShared {
+    Scratch s;
+    float tab[DT == 1 ? kFullTab : 1];
+};
+
+template <int DT>
+struct ChainShared {
+    Scratch s;
+    float tab[DT == 1 ? kFullTab : 1];
     PMap cmap[kFullMaxChunks];
     int32_t cbeta[kFullMaxChunks];
 };
 
-__device__ __forceinline__ uint32_t block_max_key(uint32_t v, FullShared& sh, int slot)
+__device__ __forceinline__ uint32_t block_max_key(uint32_t v, Scratch& sh, int slot)
 {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     v = wave_max_u32(v);
@@ -210,7 +329,7 @@ __device__ __forceinline__ uint32_t block_max_key(uint32_t v, FullShared& sh, in
     return r;
 }
 
-__device__ __forceinline__ uint32_t block_min_u(uint32_t v, FullShared& sh)
+__device__ __forceinline__ uint32_t block_min_u(uint32_t v, Scratch& sh)
 {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     v = wave_min_u32(v);
@@ -223,21 +342,20 @@ __device__ __forceinline__ uint32_t block_min_u(uint32_t v, FullShared& sh)
     return r;
 }
 
-__device__ __forceinline__ float block_sum_f(float v, FullShared& sh)
+__device__ __forceinline__ int block_sum_int(int v, Scratch& sh)
 {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    if (lane == 0) sh.fred[wid] = v;
+    v = wave_sum_i32(v);
+    if (lane == 0) sh.iscan[wid] = v;
     __syncthreads();
-    float r = 0.0f;
+    int r = 0;
 #pragma unroll
-    for (int w = 0; w < NWF; ++w) r += sh.fred[w];
+    for (int w = 0; w < NWF; ++w) r += sh.iscan[w];
     __syncthreads();
     return r;
 }
 
-__device__ __forceinline__ double block_sum_d(double v, FullShared& sh)
+__device__ __forceinline__ double block_sum_d(double v, Scratch& sh)
 {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 #pragma unroll
@@ -249,6 +367,43 @@ __device__ __forceinline__ double block_sum_d(double v, FullShared& sh)
     for (int w = 0; w < NWF; ++w) r += sh.dred[w];
     __syncthreads();
     return r;
+}
+
+/* Exclusive prefix over the workgroup in thread order (doubles). */
+__device__ __forceinline__ double block_excl_scan_d(double v, Scratch& sh)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    double x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) sh.dred[wid] = x;
+    __syncthreads();
+    double off = 0.0;
+#pragma unroll
+    for (int w = 0; w < NWF; ++w) off += (w < wid) ? sh.dred[w] : 0.0;
+    __syncthreads();
+    return off + x - v;
+}
+
+/* Exclusive prefix over the workgroup in thread order (ints). */
+__device__ __forceinline__ int block_excl_scan_i(int v, Scratch& sh, int& total)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int x = wave_inclusive_scan(v);
+    if (lane == 63) sh.iscan[wid] = x;
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NWF; ++w) {
+        off += (w < wid) ? sh.iscan[w] : 0;
+        tot += sh.iscan[w];
+    }
+    total = tot;
+    __syncthreads();
+    return off + x - v;
 }
 
 /* Inclusive scan of running-sum maps over the wave, in lane order (lane i
@@ -282,7 +437,7 @@ __device__ __forceinline__ PMap wave_shift_map(PMap f)
     return o;
 }
 
-/* The map of one thread's terms in binade e (terms before `from` skipped). */
+/* The map of one thread's terms in binade e. */
 __device__ __forceinline__ PMap thread_map(const float (&t)[kFullPer], int nvalid, int32_t e)
 {
     int32_t csum = 0, ties = 0;
@@ -308,7 +463,7 @@ __device__ __forceinline__ PMap thread_map(const float (&t)[kFullPer], int nvali
 
 /* The whole workgroup's map of a chunk (thread maps scanned over the wave,
  * wave totals composed in order); valid in thread 0. */
-__device__ __forceinline__ PMap block_chunk_map(PMap f, FullShared& sh)
+__device__ __forceinline__ PMap block_chunk_map(PMap f, Scratch& sh)
 {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const PMap incl = wave_scan_maps(f);
@@ -334,7 +489,7 @@ __device__ __forceinline__ PMap block_chunk_map(PMap f, FullShared& sh)
  * Rounds are counted in sh.misc[12].
  */
 __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st, float thr,
-                               int pos, int* hit, FullShared& sh)
+                               int pos, int* hit, Scratch& sh)
 {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     *hit = -1;
@@ -412,7 +567,7 @@ __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st,
  * binary32 by wave 0 (one readlane per term); the result and the first index
  * reaching `thr` go to sh.misc[9..11] for the whole workgroup. */
 constexpr int kHead = 256;
-__device__ void head_walk(const float (&t)[kFullPer], float thr, FullShared& sh)
+__device__ void head_walk(const float (&t)[kFullPer], float thr, Scratch& sh)
 {
     if (threadIdx.x >= 64) return;
     float s = 0.0f;
@@ -433,30 +588,13 @@ __device__ void head_walk(const float (&t)[kFullPer], float thr, FullShared& sh)
     }
 }
 
-__device__ __forceinline__ bool last_of_row(uint32_t* ticket, uint32_t count, FullShared& sh)
-{
-    return elect_last(ticket, count, &sh.flag_last);
-}
-
-struct RowIn {
-    g4s_params p;
-    double u;
-};
-__device__ __forceinline__ RowIn row_in(const FullArgs& a, int row)
-{
-    RowIn r;
-    r.p = a.params ? a.params[row] : a.p0;
-    r.u = a.u ? a.u[row] : a.u0;
-    return r;
-}
-
-/* Final outputs of a row (called by wave 0 of the row's last workgroup). */
+/* Final outputs of a row (called by wave 0 of the row's workgroup). */
 __device__ void write_row_outputs(const FullArgs& a, int row, int32_t id, int32_t argmax, float lsum,
-                                  uint32_t flags)
+                                  int32_t count, uint32_t flags)
 {
     if ((threadIdx.x & 63) == 0) {
         a.ids[row] = id;
-        if (a.out.count) a.out.count[row] = a.vocab;
+        if (a.out.count) a.out.count[row] = count;
         if (a.out.argmax) a.out.argmax[row] = argmax;
         if (a.out.lsum) a.out.lsum[row] = lsum;
         if (a.out.flags) a.out.flags[row] = flags;
@@ -464,21 +602,409 @@ __device__ void write_row_outputs(const FullArgs& a, int row, int32_t id, int32_
     publish_done(a.done, row, a.seq);
 }
 
+__device__ __forceinline__ uint32_t row_flags(const Mask& k)
+{
+    if (k.cls == kRowFull) return G4S_FLAG_FULL_PATH;
+    uint32_t f = G4S_FLAG_TOPK_PATH | G4S_FLAG_WIDE_K;
+    if (k.state == kSelLowest) f |= G4S_FLAG_TIE_LOWEST;
+    if (k.state == kSelBits) f |= G4S_FLAG_HEAP_REPLAY;
+    return f;
+}
+
+/* Are outputs per term requested?  Full rows: every p when capacity >= V;
+ * wide rows: the first `capacity` survivors. */
+__device__ __forceinline__ bool term_outputs(const FullArgs& a, int cls)
+{
+    if (cls == kRowFull) return a.out.probs && a.out.capacity >= a.vocab;
+    return (a.out.probs || a.out.indices) && a.out.capacity >= 1;
+}
+
+/* Context of the e evaluation: the row's formula, m and table window. */
+__device__ __forceinline__ Ctx make_ctx(const FullArgs& a, const FullRow& r, int cls)
+{
+    Ctx c;
+    c.cap = a.softcap;
+    c.inv_cap = c.cap > 0.0f ? div_cr32(1.0f, c.cap) : 1.0f;
+    c.inv_t = r.inv_t;
+    c.m = r.m;
+    c.scale = r.scale;
+    c.win_lo = r.win_lo;
+    c.cls = cls;
+    return c;
+}
+
+/* Copy the row's e table into LDS (ends with a barrier). */
+template <int DT>
+__device__ __forceinline__ void load_tab(const FullArgs& a, int row, const FullRow& r, float* tab)
+{
+    if (DT == 1 && r.win_lo >= 0) {
+        const float4* src = reinterpret_cast<const float4*>(a.ws.etab + (int64_t)row * kFullTab);
+        float4 v[kFullTab / 4 / kFullBlock];
+#pragma unroll
+        for (int q = 0; q < kFullTab / 4 / kFullBlock; ++q) v[q] = src[threadIdx.x + q * kFullBlock];
+#pragma unroll
+        for (int q = 0; q < kFullTab / 4 / kFullBlock; ++q)
+            reinterpret_cast<float4*>(tab)[threadIdx.x + q * kFullBlock] = v[q];
+    }
+    __syncthreads();
+}
+
+/* Index of the r-th (1-based) term of chunk cb, in index order, whose key
+ * satisfies pred; every thread gets it. */
+template <int DT, typename Pred>
+__device__ int kth_in_chunk(const FullArgs& a, const char* rowp, int cb, int r, Pred pred,
+                            Scratch& sh)
+{
+    uint32_t raw[kFullPer];
+    const int64_t e0 = (int64_t)cb * kFullChunk + (int64_t)threadIdx.x * kFullPer;
+    const int nv = load16<DT>(rowp, e0, a.vocab, raw);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < kFullPer; ++j) cnt += (j < nv && pred(cand_key(x_of<DT>(raw[j])))) ? 1 : 0;
+    int total;
+    const int off = block_excl_scan_i(cnt, sh, total);
+    if (off < r && r <= off + cnt) {
+        int seen = off;
+        for (int j = 0; j < nv; ++j)
+            if (pred(cand_key(x_of<DT>(raw[j]))) && ++seen == r) {
+                sh.misc[13] = (int)(e0 + j);
+                break;
+            }
+    }
+    __syncthreads();
+    const int res = sh.misc[13];
+    __syncthreads();
+    return res;
+}
+
 }  // namespace
+
+/* ------------------------------------------------ wide rows: radix select */
+
+/* Histogram of one digit of the keys that match the digits fixed so far
+ * (pass 0: bits 31-21, pass 1: bits 20-10, pass 2: bits 9-0). */
+template <int DT>
+__global__ __launch_bounds__(kFullBlock) void wide_hist_kernel(FullArgs a, int pass)
+{
+    __shared__ uint32_t hist[kWideBins];
+    const int tid = threadIdx.x;
+    const int row = blockIdx.y, b = blockIdx.x;
+    const RowIn ri = row_in(a, row);
+    if (row_class(a, ri.p.top_k) != kRowWide) return;
+    uint32_t prefix = 0u;
+    if (pass > 0) {
+        const WideSel s = a.ws.sel[row];
+        if (s.state != kSelSearch) return;
+        prefix = s.prefix;
+    }
+    for (int i = tid; i < kWideBins; i += kFullBlock) hist[i] = 0u;
+    __syncthreads();
+    uint32_t raw[kFullPer];
+    const int nv = load16<DT>(row_ptr<DT>(a, row), (int64_t)b * kFullChunk + (int64_t)tid * kFullPer,
+                              a.vocab, raw);
+#pragma unroll
+    for (int j = 0; j < kFullPer; ++j) {
+        const uint32_t key = cand_key(x_of<DT>(raw[j]));
+        if (j >= nv || key == 0u) continue;
+        bool match;
+        uint32_t d;
+        if (pass == 0) {
+            match = true;
+            d = key >> 21;
+        } else if (pass == 1) {
+            match = (key >> 21) == prefix;
+            d = (key >> 10) & 0x7FFu;
+        } else {
+            match = (key >> 10) == prefix;
+            d = key & 0x3FFu;
+        }
+        if (match) atomicAdd(&hist[d], 1u);
+    }
+    __syncthreads();
+    uint32_t* gh = a.ws.hist + (int64_t)row * kWideBins;
+    for (int i = tid; i < kWideBins; i += kFullBlock)
+        if (hist[i]) atomicAdd(&gh[i], hist[i]);
+}
+
+/* Fix one digit: the bin holding the rank-krem key counted from the top
+ * (the heap keeps the K largest as a multiset, Model.pas:2615-2664).
+ * Clears the row's histogram for the next pass. */
+__global__ __launch_bounds__(kFullBlock) void wide_find_kernel(FullArgs a, int pass)
+{
+    __shared__ Scratch sh;
+    const int tid = threadIdx.x;
+    const int row = blockIdx.y;
+    const RowIn ri = row_in(a, row);
+    if (row_class(a, ri.p.top_k) != kRowWide) return;
+    const int K = ri.p.top_k;
+    WideSel* sp = a.ws.sel + row;
+    WideSel s;
+    if (pass == 0) {
+        s.prefix = 0u;
+        s.krem = K;
+        s.state = kSelSearch;
+    } else {
+        s = *sp;
+        if (s.state != kSelSearch) return;
+    }
+    const int nb = pass == 2 ? 1024 : kWideBins;
+    const int per = nb / kFullBlock;
+    uint32_t* gh = a.ws.hist + (int64_t)row * kWideBins;
+    /* thread t holds bins nb-1-t*per down to nb-per-t*per (highest first) */
+    uint32_t c[kWideBins / kFullBlock];
+    int tsum = 0;
+    for (int q = 0; q < per; ++q) {
+        const int bin = nb - 1 - tid * per - q;
+        c[q] = gh[bin];
+        gh[bin] = 0u;
+        tsum += (int)c[q];
+    }
+    int total;
+    int above = block_excl_scan_i(tsum, sh, total);
+    if (pass == 0 && total <= K) {
+        /* at most K logits above -1e30: every one survives (the -1e30
+         * fillers are dropped, Model.pas:2668-2676) */
+        if (tid == 0) {
+            sp->state = total == 0 ? kSelEmpty : kSelAll;
+            sp->tau = 1u;
+            sp->idx_thr = INT_MAX;
+            sp->count = total;
+        }
+        if (total == 0 && tid < 64) {
+            if (tid == 0) {
+                a.ids[row] = -1;
+                if (a.out.count) a.out.count[row] = 0;
+                if (a.out.flags)
+                    a.out.flags[row] = G4S_FLAG_TOPK_PATH | G4S_FLAG_WIDE_K | G4S_FLAG_EMPTY;
+            }
+            publish_done(a.done, row, a.seq);
+        }
+        return;
+    }
+    const int krem = s.krem;
+    for (int q = 0; q < per; ++q) {
+        const int bin = nb - 1 - tid * per - q;
+        if (above < krem && krem <= above + (int)c[q]) {
+            const int k2 = krem - above;
+            if (pass < 2) {
+                sp->prefix = pass == 0 ? (uint32_t)bin : ((s.prefix << 11) | (uint32_t)bin);
+                sp->krem = k2;
+                sp->state = kSelSearch;
+                sp->idx_thr = INT_MAX;
+            } else {
+                sp->tau = (s.prefix << 10) | (uint32_t)bin;
+                sp->need = k2;
+                sp->eq = (int)c[q];
+                sp->count = K;
+                sp->state = k2 == (int)c[q] ? kSelAll : kSelTies;
+            }
+        }
+        above += (int)c[q];
+    }
+}
+
+/* Per chunk: keys >= tau, keys == tau, the last index above tau. */
+template <int DT>
+__global__ __launch_bounds__(kFullBlock) void wide_ties_kernel(FullArgs a)
+{
+    __shared__ Scratch sh;
+    const int tid = threadIdx.x;
+    const int row = blockIdx.y, b = blockIdx.x;
+    const RowIn ri = row_in(a, row);
+    if (row_class(a, ri.p.top_k) != kRowWide) return;
+    const WideSel s = a.ws.sel[row];
+    if (s.state != kSelTies) return;
+    uint32_t raw[kFullPer];
+    const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
+    const int nv = load16<DT>(row_ptr<DT>(a, row), e0, a.vocab, raw);
+    int ge = 0, eq = 0;
+    uint32_t gt = 0u; /* last index above tau, plus one */
+#pragma unroll
+    for (int j = 0; j < kFullPer; ++j) {
+        const uint32_t key = cand_key(x_of<DT>(raw[j]));
+        if (j >= nv) continue;
+        ge += key >= s.tau;
+        eq += key == s.tau;
+        if (key > s.tau) gt = (uint32_t)(e0 + j) + 1u;
+    }
+    ge = block_sum_int(ge, sh);
+    eq = block_sum_int(eq, sh);
+    gt = block_max_key(gt, sh, 0);
+    if (tid == 0) {
+        TieRec t;
+        t.cge = ge;
+        t.ceq = eq;
+        t.maxgt = (int32_t)gt - 1;
+        t.pad = 0;
+        a.ws.ties[(int64_t)row * kFullMaxChunks + b] = t;
+    }
+}
+
+/* The tie rule.  t* = index of the K-th key >= tau in index order.  When
+ * every key above tau precedes t*, the heap holds exactly the first K keys
+ * >= tau once it has passed t*, and rejects every later copy of tau
+ * (v <= root, Model.pas:2643): the survivors are the keys above tau and the
+ * first `need` copies of tau.  Otherwise the heap's layout decides: replay. */
+template <int DT>
+__global__ __launch_bounds__(kFullBlock) void wide_ties_find_kernel(FullArgs a)
+{
+    __shared__ Scratch sh;
+    const int tid = threadIdx.x;
+    const int row = blockIdx.y;
+    const RowIn ri = row_in(a, row);
+    if (row_class(a, ri.p.top_k) != kRowWide) return;
+    WideSel* sp = a.ws.sel + row;
+    const WideSel s = *sp;
+    if (s.state != kSelTies) return;
+    const int nch = a.nch;
+    const int K = ri.p.top_k;
+    const TieRec* tr = a.ws.ties + (int64_t)row * kFullMaxChunks;
+    int ge[CPT], eq[CPT];
+    int sge = 0, seqn = 0, mgt = -1;
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int cb = tid * CPT + q;
+        ge[q] = eq[q] = 0;
+        if (cb < nch) {
+            const TieRec t = tr[cb];
+            ge[q] = t.cge;
+            eq[q] = t.ceq;
+            mgt = t.maxgt > mgt ? t.maxgt : mgt;
+        }
+        sge += ge[q];
+        seqn += eq[q];
+    }
+    int tot;
+    int run_ge = block_excl_scan_i(sge, sh, tot);
+    int run_eq = block_excl_scan_i(seqn, sh, tot);
+    const int32_t max_gt = (int32_t)block_max_key((uint32_t)(mgt + 1), sh, 1) - 1;
+    const int need = s.need;
+    if (tid == 0) {
+        sh.misc[0] = sh.misc[2] = -1;
+        sh.misc[1] = sh.misc[3] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int cb = tid * CPT + q;
+        if (run_ge < K && K <= run_ge + ge[q]) {
+            sh.misc[0] = cb;
+            sh.misc[1] = K - run_ge;
+        }
+        if (run_eq < need && need <= run_eq + eq[q]) {
+            sh.misc[2] = cb;
+            sh.misc[3] = need - run_eq;
+        }
+        run_ge += ge[q];
+        run_eq += eq[q];
+    }
+    __syncthreads();
+    const int c1 = sh.misc[0], r1 = sh.misc[1], c2 = sh.misc[2], r2 = sh.misc[3];
+    __syncthreads();
+    if (c1 < 0 || c1 >= nch || c2 < 0 || c2 >= nch) {
+        /* counts inconsistent with the select (not expected): the replay
+         * decides from the row itself */
+        if (tid == 0) sp->state = kSelReplay;
+        return;
+    }
+    const char* rowp = row_ptr<DT>(a, row);
+    const uint32_t tau = s.tau;
+    const int tstar = kth_in_chunk<DT>(a, rowp, c1, r1, [&](uint32_t k) { return k >= tau; }, sh);
+    if (max_gt < tstar) {
+        const int thr = kth_in_chunk<DT>(a, rowp, c2, r2, [&](uint32_t k) { return k == tau; }, sh);
+        if (tid == 0) {
+            sp->idx_thr = thr;
+            sp->state = kSelLowest;
+        }
+    } else if (tid == 0) {
+        sp->state = kSelReplay;
+    }
+}
+
+/* Exact replay of the reference's min-heap pass (Model.pas:2632-2664) for
+ * the rows whose tie at tau depends on the heap layout, one row at a time
+ * with the heap in device memory.  One wave screens 64 logits per step
+ * against the current root; lane 0 inserts the ones that pass, in index
+ * order.  The surviving copies of tau are then marked in the row's bitmask.
+ * Cost: about (K + K ln(V/K)) log2(K) dependent heap steps per row. */
+template <int DT>
+__global__ __launch_bounds__(64) void wide_replay_kernel(FullArgs a)
+{
+    const int lane = threadIdx.x;
+    const int V = a.vocab;
+    float* hv = a.ws.heap_v;
+    int32_t* hi = a.ws.heap_i;
+    for (int row = 0; row < a.batch; ++row) {
+        const RowIn ri = row_in(a, row);
+        if (row_class(a, ri.p.top_k) != kRowWide) continue;
+        WideSel* sp = a.ws.sel + row;
+        const WideSel s = *sp;
+        if (s.state != kSelReplay) continue;
+        const int K = ri.p.top_k;
+        const char* rowp = row_ptr<DT>(a, row);
+        if (lane == 0) {
+            for (int i = 0; i < K; ++i) { /* :2634-2638 */
+                hv[i] = -1e30f;
+                hi[i] = -1;
+            }
+        }
+        float root = -1e30f;
+        for (int base = 0; base < V; base += 64) {
+            const int e = base + lane;
+            float x = 0.0f;
+            if (e < V) {
+                if constexpr (DT == 0)
+                    x = reinterpret_cast<const float*>(rowp)[e];
+                else
+                    x = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(rowp)[e] << 16);
+            }
+            uint64_t take = __ballot(e < V && !(x <= root));
+            while (take) {
+                const int l = (int)__builtin_ctzll(take);
+                take &= take - 1;
+                const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+                if (lane == 0 && !(v <= hv[0])) { /* :2643-2644 */
+                    int p = 0;
+                    for (;;) { /* :2647-2661 */
+                        int c = p * 2 + 1;
+                        if (c >= K) break;
+                        if (c + 1 < K && hv[c + 1] < hv[c]) c += 1;
+                        if (hv[c] >= v) break;
+                        hv[p] = hv[c];
+                        hi[p] = hi[c];
+                        p = c;
+                    }
+                    hv[p] = v;
+                    hi[p] = base + l;
+                }
+            }
+            const float r0 = lane == 0 ? hv[0] : 0.0f;
+            root = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r0), 0));
+        }
+        if (lane == 0) {
+            uint32_t* bits = a.ws.bits + (int64_t)row * a.ws.bits_stride;
+            for (int w = 0; w < a.ws.bits_stride; ++w) bits[w] = 0u;
+            for (int i = 0; i < K; ++i) {
+                const int32_t idx = hi[i];
+                if (idx >= 0 && cand_key(hv[i]) == s.tau) bits[idx >> 5] |= 1u << (idx & 31);
+            }
+            sp->state = kSelBits;
+        }
+    }
+}
 
 /* ------------------------------------------------------------ 1: max */
 
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
 {
-    __shared__ FullShared sh;
+    __shared__ Scratch sh;
     const int tid = threadIdx.x;
     const int row = blockIdx.y, b = blockIdx.x;
     const int V = a.vocab;
     const RowIn ri = row_in(a, row);
-    if (!is_full_row(ri.p.top_k, V)) return;
-    const char* rowp = reinterpret_cast<const char*>(a.logits) +
-                       (int64_t)row * a.row_stride * Elem<DT>::SIZE;
+    Mask k;
+    if (!row_mask(a, row, ri, k)) return;
     const float cap = a.softcap;
     const float inv_cap = cap > 0.0f ? div_cr32(1.0f, cap) : 1.0f;      /* Layers.pas:309 */
     const float T = ri.p.temperature;
@@ -486,20 +1012,26 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
     const float inv_t = scale ? div_cr32(1.0f, T) : 1.0f;              /* Model.pas:2705 */
 
     uint32_t raw[kFullPer];
-    const int nvalid = load16<DT>(rowp, (int64_t)b * kFullChunk + (int64_t)tid * kFullPer, V, raw);
-    uint32_t kmax = 0u, amax = 0u, ymk = 0u;
+    const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
+    const int nvalid = load16<DT>(row_ptr<DT>(a, row), e0, V, raw);
+    uint32_t kmax = 0u, amax = 0u, ymk = 0u, fs = 0xFFFFFFFFu;
+    int ns = 0;
     float ya[kFullPer];
+    bool part[kFullPer];
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j) {
         const float xj = x_of<DT>(raw[j]);
+        part[j] = j < nvalid && takes_part(k, xj, e0 + j);
         ya[j] = y_approx(xj, cap, inv_cap, scale, inv_t);
-        if (j < nvalid) {
-            kmax = g4s_max_u(kmax, f2key(xj));
+        if (j < nvalid) kmax = g4s_max_u(kmax, f2key(xj));
+        if (part[j]) {
             amax = g4s_max_u(amax, __float_as_uint(xj) & 0x7FFFFFFFu);
             ymk = g4s_max_u(ymk, f2key(ya[j]));
+            ns += 1;
+            fs = g4s_min_u(fs, (uint32_t)(e0 + j));
         }
     }
-    /* the three maxima in one LDS exchange */
+    /* the maxima in one LDS exchange */
     {
         const int lane = tid & 63, wid = tid >> 6;
         kmax = wave_max_u32(kmax);
@@ -523,57 +1055,118 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j)
-        if (j < nvalid) s += __builtin_amdgcn_exp2f(ya[j] * 1.4426950408889634f - lg2e_ymax);
+        if (part[j]) s += __builtin_amdgcn_exp2f(ya[j] * 1.4426950408889634f - lg2e_ymax);
     s = wave_sum_f32(s);
     if ((tid & 63) == 0) sh.fred[tid >> 6] = s;
-    __syncthreads();
+    ns = block_sum_int(ns, sh); /* its barriers also cover fred */
+    fs = block_min_u(fs, sh);
     s = 0.0f;
 #pragma unroll
     for (int w = 0; w < NWF; ++w) s += sh.fred[w];
-    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
     if (tid == 0) {
-        uint64_t* w = reinterpret_cast<uint64_t*>(&rc[b]);
-        st_dev(w, ((uint64_t)amax << 32) | kmax);
-        st_dev(w + 1, ((uint64_t)__float_as_uint(s) << 32) | __float_as_uint(ymax));
+        FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks + b;
+        rc->maxkey = kmax;
+        rc->amax = amax;
+        rc->ymax = ymax;
+        rc->sapx = s;
+        rc->nsurv = ns;
+        rc->fsurv = fs == 0xFFFFFFFFu ? INT_MAX : (int32_t)fs;
     }
-    if (!last_of_row(a.ws.tickets + (int64_t)row * 4 + 0, (uint32_t)a.nch, sh)) return;
+}
 
-    /* the row's maximum, m = y(max x), and the predicted binade of LSum
-     * entering every chunk */
+/* ------------------------------------------------------------ 2: row */
+
+/* Every workgroup of a row reduces the chunk records to the row's m; for
+ * bf16 logits workgroup g fills entries g*256 .. g*256+255 of the e table;
+ * workgroup 0 also writes the row record, the predicted binades and the
+ * survivor offsets. */
+template <int DT>
+__global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
+{
+    __shared__ Scratch sh;
+    const int tid = threadIdx.x;
+    const int row = blockIdx.y, g = blockIdx.x;
+    const RowIn ri = row_in(a, row);
+    Mask k;
+    if (!row_mask(a, row, ri, k)) return;
     const int nch = a.nch;
+    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
     uint32_t km = 0u, am = 0u;
-    for (int c = tid; c < nch; c += kFullBlock) {
-        const uint64_t w = ld_dev(reinterpret_cast<const uint64_t*>(&rc[c]));
-        km = g4s_max_u(km, (uint32_t)w);
-        am = g4s_max_u(am, (uint32_t)(w >> 32));
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int cb = tid * CPT + q;
+        if (cb < nch) {
+            km = g4s_max_u(km, rc[cb].maxkey);
+            am = g4s_max_u(am, rc[cb].amax);
+        }
     }
     km = block_max_key(km, sh, 0);
     am = block_max_key(am, sh, 1);
-    const float xmax = key2f(km);
-    const float m = y_exact(xmax, cap, inv_cap, scale, inv_t);        /* Tensors.pas:648-654 */
-    if (tid == 0) {
-        double pre = 0.0;
-        for (int c = 0; c < nch; ++c) {
-            rc[c].beta_l = ss::state_of((float)pre).e;
-            /* a prediction only: chunks without a finite estimate add 0 */
-            const uint64_t w = ld_dev(reinterpret_cast<const uint64_t*>(&rc[c]) + 1);
-            double z = (double)__uint_as_float((uint32_t)w) - (double)m;
+    const float cap = a.softcap;
+    const float inv_cap = cap > 0.0f ? div_cr32(1.0f, cap) : 1.0f;
+    const float T = ri.p.temperature;
+    const int scale = (T > 0.0f) && (T != 1.0f);
+    const float inv_t = scale ? div_cr32(1.0f, T) : 1.0f;
+    const float m = y_exact(key2f(km), k.cls, cap, inv_cap, scale, inv_t); /* Tensors.pas:648-654 */
+    /* table window: the 16 binades of |x| below and at the largest one */
+    int win = -1;
+    if (DT == 1) {
+        const int eb = (int)((am >> 23) & 0xFFu);
+        win = eb - 15 < 0 ? 0 : eb - 15;
+        const int i = g * kFullBlock + tid;
+        const uint32_t ebi = (uint32_t)win + (((uint32_t)i >> 7) & 15u);
+        const uint32_t code = (((uint32_t)i >> 11) << 15) | (ebi << 7) | ((uint32_t)i & 0x7Fu);
+        const float x = __uint_as_float(code << 16);
+        a.ws.etab[(int64_t)row * kFullTab + i] =
+            exp_diff_cr32(y_exact(x, k.cls, cap, inv_cap, scale, inv_t), m);
+    }
+    if (g != 0) return;
+
+    /* predicted binade of LSum entering every chunk: exclusive prefix of the
+     * chunk estimates (a prediction only: non-finite estimates add 0); the
+     * survivor offsets and the first survivor */
+    double d[CPT];
+    int ns[CPT];
+    double tsum = 0.0;
+    int tns = 0;
+    uint32_t fs = 0xFFFFFFFFu;
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int cb = tid * CPT + q;
+        d[q] = 0.0;
+        ns[q] = 0;
+        if (cb < nch) {
+            double z = (double)rc[cb].ymax - (double)m;
             z = z > 50.0 ? 50.0 : (z < -700.0 ? -700.0 : z);
-            const double d = (double)__uint_as_float((uint32_t)(w >> 32)) * exp_fast_d(z);
-            pre += (d >= 0.0 && d < 1e300) ? d : 0.0;
+            const double v = (double)rc[cb].sapx * exp_fast_d(z);
+            d[q] = (v >= 0.0 && v < 1e300) ? v : 0.0;
+            ns[q] = rc[cb].nsurv;
+            fs = g4s_min_u(fs, (uint32_t)rc[cb].fsurv);
         }
+        tsum += d[q];
+        tns += ns[q];
+    }
+    double pre = block_excl_scan_d(tsum, sh);
+    int count;
+    int soff = block_excl_scan_i(tns, sh, count);
+    fs = block_min_u(fs, sh);
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int cb = tid * CPT + q;
+        if (cb < nch) {
+            rc[cb].beta_l = ss::state_of((float)pre).e;
+            rc[cb].soff = soff;
+        }
+        pre += d[q];
+        soff += ns[q];
+    }
+    if (tid == 0) {
         FullRow r;
         r.maxkey = km;
         r.amax = am;
         r.m = m;
         r.inv_t = inv_t;
         r.scale = scale;
-        /* table window: the 16 binades of |x| below and at the largest one */
-        int win = -1;
-        if (DT == 1) {
-            const int eb = (int)((am >> 23) & 0xFFu); /* am: bits of the largest |x| */
-            win = eb - 15 < 0 ? 0 : eb - 15;
-        }
         r.win_lo = win;
         r.lsum = 0.0f;
         r.inv = 0.0f;
@@ -581,52 +1174,12 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
         r.argmax = 0;
         r.c_last = -1;
         r.nodraw = 0;
+        r.count = count;
+        r.first = (int32_t)fs;
+        for (int j = 0; j < kNear; ++j) r.near[j] = INT_MAX;
+        r.l_reev = r.l_rounds = r.c_reev = r.c_rounds = 0;
         a.ws.rows[row] = r;
     }
-}
-
-/* ------------------------------------------------------------ 2: table */
-
-__global__ __launch_bounds__(kFullBlock) void full_table_kernel(FullArgs a)
-{
-    const int row = blockIdx.y;
-    const int i = blockIdx.x * kFullBlock + threadIdx.x;
-    const RowIn ri = row_in(a, row);
-    if (!is_full_row(ri.p.top_k, a.vocab) || i >= kFullTab) return;
-    const FullRow r = a.ws.rows[row];
-    if (r.win_lo < 0) return;
-    const float cap = a.softcap;
-    const float inv_cap = cap > 0.0f ? div_cr32(1.0f, cap) : 1.0f;
-    const uint32_t eb = (uint32_t)r.win_lo + (((uint32_t)i >> 7) & 15u);
-    const uint32_t code = (((uint32_t)i >> 11) << 15) | (eb << 7) | ((uint32_t)i & 0x7Fu);
-    const float x = __uint_as_float(code << 16);
-    a.ws.etab[(int64_t)row * kFullTab + i] =
-        exp_diff_cr32(y_exact(x, cap, inv_cap, r.scale, r.inv_t), r.m);
-}
-
-/* Load the row's table and context into LDS / registers. */
-template <int DT>
-__device__ __forceinline__ Ctx load_ctx(const FullArgs& a, int row, const FullRow& r,
-                                        FullShared& sh)
-{
-    Ctx c;
-    c.cap = a.softcap;
-    c.inv_cap = c.cap > 0.0f ? div_cr32(1.0f, c.cap) : 1.0f;
-    c.inv_t = r.inv_t;
-    c.m = r.m;
-    c.scale = r.scale;
-    c.win_lo = r.win_lo;
-    if (DT == 1 && r.win_lo >= 0) {
-        const float4* src = reinterpret_cast<const float4*>(a.ws.etab + (int64_t)row * kFullTab);
-        float4 v[kFullTab / 4 / kFullBlock];
-#pragma unroll
-        for (int q = 0; q < kFullTab / 4 / kFullBlock; ++q) v[q] = src[threadIdx.x + q * kFullBlock];
-#pragma unroll
-        for (int q = 0; q < kFullTab / 4 / kFullBlock; ++q)
-            reinterpret_cast<float4*>(sh.tab)[threadIdx.x + q * kFullBlock] = v[q];
-    }
-    __syncthreads();
-    return c;
 }
 
 /* ------------------------------------------------- 3: lsum chunk maps */
@@ -634,56 +1187,69 @@ __device__ __forceinline__ Ctx load_ctx(const FullArgs& a, int row, const FullRo
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
 {
-    __shared__ FullShared sh;
+    __shared__ TabShared<DT> sh;
     const int tid = threadIdx.x;
-    const int row = blockIdx.y, b = blockIdx.x;
+    const int row = blockIdx.y;
     const int V = a.vocab;
     const RowIn ri = row_in(a, row);
-    if (!is_full_row(ri.p.top_k, V)) return;
-    const char* rowp = reinterpret_cast<const char*>(a.logits) +
-                       (int64_t)row * a.row_stride * Elem<DT>::SIZE;
+    Mask k;
+    if (!row_mask(a, row, ri, k)) return;
+    const char* rowp = row_ptr<DT>(a, row);
     FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
-    const FullRow r = a.ws.rows[row];
-    const Ctx c = load_ctx<DT>(a, row, r, sh);
+    FullRow* rr = a.ws.rows + row;
+    const FullRow r = *rr;
+    const Ctx c = make_ctx(a, r, k.cls);
+    load_tab<DT>(a, row, r, sh.tab);
 
-    uint32_t raw[kFullPer];
-    const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
-    const int nvalid = load16<DT>(rowp, e0, V, raw);
-    float t[kFullPer];
-    double dsum = 0.0;
-    uint32_t first1 = 0xFFFFFFFFu;
+    for (int q = 0; q < kFullCPW; ++q) {
+        const int b = blockIdx.x * kFullCPW + q;
+        if (b >= a.nch) break;
+        uint32_t raw[kFullPer];
+        const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
+        const int nvalid = load16<DT>(rowp, e0, V, raw);
+        float t[kFullPer];
+        terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t);                  /* Tensors.pas:660 */
+        double dsum = 0.0;
+        uint32_t first1 = 0xFFFFFFFFu;
 #pragma unroll
-    for (int j = 0; j < kFullPer; ++j) {
-        t[j] = (j < nvalid) ? e_of<DT>(raw[j], c, sh.tab) : 0.0f;      /* Tensors.pas:660 */
-        dsum += (double)t[j];
-        if (j < nvalid && t[j] == 1.0f && first1 == 0xFFFFFFFFu) first1 = (uint32_t)(e0 + j);
-    }
-    const PMap cm = block_chunk_map(thread_map(t, nvalid, rc[b].beta_l), sh);
-    dsum = block_sum_d(dsum, sh);
-    first1 = block_min_u(first1, sh);
-    if (tid == 0) {
-        rc[b].lmap = cm;
-        rc[b].de = dsum;
-        rc[b].first1 = (int32_t)first1;
+        for (int j = 0; j < kFullPer; ++j) {
+            dsum += (double)t[j];
+            if (t[j] >= 1.0f - (float)(kNear - 1) * 0x1p-24f && t[j] <= 1.0f) {
+                /* e = 1 - jj*2^-24 exactly, jj < kNear */
+                const int jj = (int)((1.0f - t[j]) * 0x1p24f);
+                if (jj == 0)
+                    first1 = g4s_min_u(first1, (uint32_t)(e0 + j));
+                else if (k.cls == kRowWide)
+                    atomicMin(&rr->near[jj], (int32_t)(e0 + j));
+            }
+        }
+        const PMap cm = block_chunk_map(thread_map(t, nvalid, rc[b].beta_l), sh.s);
+        dsum = block_sum_d(dsum, sh.s);
+        first1 = block_min_u(first1, sh.s);
+        if (tid == 0) {
+            rc[b].lmap = cm;
+            rc[b].de = dsum;
+            if (first1 != 0xFFFFFFFFu) atomicMin(&rr->near[0], (int32_t)first1);
+        }
     }
 }
 
 /* ------------------------------------------------------- 4: LSum chain */
 
 /* One workgroup per row: LSum by chaining the chunk maps left to right
- * (Tensors.pas:657-663), re-evaluating the chunks whose map does not apply;
- * then 1/LSum, the argmax, and the predictions for the draw. */
+ * (Tensors.pas:657-663; Model.pas:2794-2799), re-evaluating the chunks whose
+ * map does not apply; then the argmax and the predictions for the draw. */
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
 {
-    __shared__ FullShared sh;
+    __shared__ ChainShared<DT> sh;
     const int tid = threadIdx.x;
     const int row = blockIdx.y;
     const int V = a.vocab;
     const RowIn ri = row_in(a, row);
-    if (!is_full_row(ri.p.top_k, V)) return;
-    const char* rowp = reinterpret_cast<const char*>(a.logits) +
-                       (int64_t)row * a.row_stride * Elem<DT>::SIZE;
+    Mask k;
+    if (!row_mask(a, row, ri, k)) return;
+    const char* rowp = row_ptr<DT>(a, row);
     FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
     const FullRow r = a.ws.rows[row];
     const int nch = a.nch;
@@ -691,8 +1257,9 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
         sh.cmap[cb] = rc[cb].lmap;
         sh.cbeta[cb] = rc[cb].beta_l;
     }
-    if (tid == 0) sh.misc[12] = 0;
-    const Ctx c = load_ctx<DT>(a, row, r, sh); /* ends with a barrier */
+    if (tid == 0) sh.s.misc[12] = 0;
+    const Ctx c = make_ctx(a, r, k.cls);
+    load_tab<DT>(a, row, r, sh.tab); /* ends with a barrier */
 
     uint32_t raw[kFullPer];
     float t[kFullPer];
@@ -709,60 +1276,77 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
         ++reev;
         const int64_t f0 = (int64_t)cb * kFullChunk + (int64_t)tid * kFullPer;
         const int nv = load16<DT>(rowp, f0, V, raw);
-#pragma unroll
-        for (int j = 0; j < kFullPer; ++j) t[j] = (j < nv) ? e_of<DT>(raw[j], c, sh.tab) : 0.0f;
+        terms_e<DT>(raw, nv, f0, c, k, sh.tab, t);
         int pos = 0;
         if (cb == 0) {
-            head_walk(t, __builtin_inff(), sh);
+            head_walk(t, __builtin_inff(), sh.s);
             __syncthreads();
-            st.e = sh.misc[9];
-            st.m = sh.misc[10];
+            st.e = sh.s.misc[9];
+            st.m = sh.s.misc[10];
             __syncthreads();
             pos = kHead / kFullPer;
         }
         int h;
-        st = resolve_chunk(t, nv, st, __builtin_inff(), pos, &h, sh);
+        st = resolve_chunk(t, nv, st, __builtin_inff(), pos, &h, sh.s);
     }
     const float lsum = ss::value_of(st);
     const float inv = div_cr32(1.0f, lsum);                            /* Tensors.pas:668 */
-    /* argmax of p: p = fl32(e * inv) <= inv with equality exactly at e == 1
-     * (the next float below 1 gives a p below inv), so the first e == 1 */
-    uint32_t f1 = 0xFFFFFFFFu;
-    for (int cb = tid; cb < nch; cb += kFullBlock) f1 = g4s_min_u(f1, (uint32_t)rc[cb].first1);
-    f1 = block_min_u(f1, sh);
-    const int32_t argmax = (int32_t)f1;                                 /* Model.pas:2712-2721 */
+    /* argmax of p.  Full row: p = fl32(e * inv) <= inv with equality exactly
+     * at e == 1 (the next float below 1 gives a p below inv), so the first
+     * e == 1.  Wide row: p = fl32(e / LSum) can also equal fl32(1 / LSum) for
+     * e = 1 - j*2^-24 with small j (never for j >= kNear): the first index
+     * among the values whose quotient ties (Model.pas:2804-2807). */
+    int32_t argmax = r.near[0];
+    if (k.cls == kRowWide) {
+        for (int j = 1; j < kNear; ++j)
+            if (r.near[j] < argmax && div_cr32(1.0f - (float)j * 0x1p-24f, lsum) == inv)
+                argmax = r.near[j];
+    }
     const float T = ri.p.temperature;
-    const bool all = a.out.probs && a.out.capacity >= V; /* every p is an output */
+    const bool all = term_outputs(a, k.cls);
     const bool nodraw = !(T > 0.0f);
-    if (nodraw && !all) {
-        /* no draw: the greedy choice (Model.pas:2723) */
-        if (tid < 64) write_row_outputs(a, row, argmax, argmax, lsum, G4S_FLAG_FULL_PATH);
+    const float thr = nodraw ? __builtin_inff() : mul_u_p_cr32(ri.u, ri.p.top_p); /* :2726 */
+    /* fl32(u*TopP) <= 0: the first term's running sum already reaches it */
+    const bool direct = !nodraw && !(thr > 0.0f);
+    if ((nodraw || direct) && !all) {
+        if (tid < 64) {
+            uint32_t f = row_flags(k);
+            if (direct) f |= G4S_FLAG_DREW | G4S_FLAG_REACHED;
+            write_row_outputs(a, row, direct ? r.first : argmax, argmax, lsum, r.count, f);
+        }
         return;
     }
-    const float thr = nodraw ? __builtin_inff() : mul_u_p_cr32(ri.u, ri.p.top_p); /* :2726 */
+    /* predicted binade of the running sum entering each chunk, and the
+     * chunk where it is predicted to reach thr (with margin) */
+    double d[CPT];
+    double tsum = 0.0;
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int cb = tid * CPT + q;
+        d[q] = cb < nch ? rc[cb].de : 0.0;
+        tsum += d[q];
+    }
+    double pre = block_excl_scan_d(tsum, sh.s);
+    uint32_t last = (uint32_t)(nch - 1);
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int cb = tid * CPT + q;
+        if (cb < nch) rc[cb].beta_c = ss::state_of((float)(pre * (double)inv)).e;
+        pre += d[q];
+        if (cb < nch && pre * (double)inv >= (double)thr * (1.0 + 0x1p-10))
+            last = g4s_min_u(last, (uint32_t)cb);
+    }
+    last = block_min_u(last, sh.s);
     if (tid == 0) {
-        /* predicted binade of the running sum entering each chunk, and the
-         * chunk where it is predicted to reach thr (with margin) */
-        double pre = 0.0;
-        int last = nch - 1;
-        bool found = false;
-        for (int cb = 0; cb < nch; ++cb) {
-            rc[cb].beta_c = ss::state_of((float)(pre * (double)inv)).e;
-            pre += rc[cb].de;
-            if (!found && pre * (double)inv >= (double)thr * (1.0 + 0x1p-10)) {
-                last = cb;
-                found = true;
-            }
-        }
         FullRow w = r;
         w.lsum = lsum;
         w.inv = inv;
         w.thr = thr;
         w.argmax = argmax;
-        w.c_last = all ? nch - 1 : last;
-        w.nodraw = nodraw ? 1 : 0;
+        w.c_last = (all || direct) ? nch - 1 : (int32_t)last;
+        w.nodraw = nodraw ? 1 : (direct ? 2 : 0);
         w.l_reev = reev;
-        w.l_rounds = sh.misc[12];
+        w.l_rounds = sh.s.misc[12];
         w.c_reev = 0;
         w.c_rounds = 0;
         a.ws.rows[row] = w;
@@ -774,70 +1358,107 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
 {
-    __shared__ FullShared sh;
+    __shared__ TabShared<DT> sh;
     const int tid = threadIdx.x;
-    const int row = blockIdx.y, b = blockIdx.x;
+    const int row = blockIdx.y;
     const int V = a.vocab;
     const RowIn ri = row_in(a, row);
-    if (!is_full_row(ri.p.top_k, V)) return;
+    Mask k;
+    if (!row_mask(a, row, ri, k)) return;
     const FullRow r = a.ws.rows[row];
-    if (r.c_last < 0 || b > r.c_last) return;
-    const char* rowp = reinterpret_cast<const char*>(a.logits) +
-                       (int64_t)row * a.row_stride * Elem<DT>::SIZE;
+    if (r.c_last < 0 || (int)blockIdx.x * kFullCPW > r.c_last) return;
+    const char* rowp = row_ptr<DT>(a, row);
     FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
-    const Ctx c = load_ctx<DT>(a, row, r, sh);
-    const float inv = r.inv;
+    const Ctx c = make_ctx(a, r, k.cls);
+    load_tab<DT>(a, row, r, sh.tab);
+    const bool all = term_outputs(a, k.cls);
 
-    uint32_t raw[kFullPer];
-    const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
-    const int nvalid = load16<DT>(rowp, e0, V, raw);
-    float t[kFullPer];
+    for (int q = 0; q < kFullCPW; ++q) {
+        const int b = blockIdx.x * kFullCPW + q;
+        if (b > r.c_last) break;
+        uint32_t raw[kFullPer];
+        const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
+        const int nvalid = load16<DT>(rowp, e0, V, raw);
+        float t[kFullPer];
+        terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t);
 #pragma unroll
-    for (int j = 0; j < kFullPer; ++j)
-        t[j] = (j < nvalid) ? e_of<DT>(raw[j], c, sh.tab) * inv : 0.0f; /* Tensors.pas:671 */
-    if (a.out.probs && a.out.capacity >= V) {
-        float* po = a.out.probs + (int64_t)row * a.out.capacity;
-        int32_t* io = a.out.indices ? a.out.indices + (int64_t)row * a.out.capacity : nullptr;
-        for (int j = 0; j < nvalid; ++j) {
-            po[e0 + j] = t[j];
-            if (io) io[e0 + j] = (int32_t)(e0 + j);
+        for (int j = 0; j < kFullPer; ++j) t[j] = p_of(t[j], k.cls, r.inv, r.lsum);
+        if (all) {
+            float* po = a.out.probs ? a.out.probs + (int64_t)row * a.out.capacity : nullptr;
+            int32_t* io = a.out.indices ? a.out.indices + (int64_t)row * a.out.capacity : nullptr;
+            if (k.cls == kRowFull) {
+#pragma unroll
+                for (int j = 0; j < kFullPer; ++j)
+                    if (j < nvalid) {
+                        po[e0 + j] = t[j]; /* Tensors.pas:671 */
+                        if (io) io[e0 + j] = (int32_t)(e0 + j);
+                    }
+            } else {
+                /* the survivors in index order (Model.pas:2678-2688) */
+                int cnt = 0;
+                bool part[kFullPer];
+#pragma unroll
+                for (int j = 0; j < kFullPer; ++j) {
+                    part[j] = j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j);
+                    cnt += part[j] ? 1 : 0;
+                }
+                int tot;
+                int pos = rc[b].soff + block_excl_scan_i(cnt, sh.s, tot);
+#pragma unroll
+                for (int j = 0; j < kFullPer; ++j)
+                    if (part[j]) {
+                        if (pos < a.out.capacity) {
+                            if (po) po[pos] = t[j];
+                            if (io) io[pos] = (int32_t)(e0 + j);
+                        }
+                        ++pos;
+                    }
+            }
         }
+        if (r.nodraw) continue;
+        const PMap cm = block_chunk_map(thread_map(t, nvalid, rc[b].beta_c), sh.s);
+        if (tid == 0) rc[b].cmap = cm;
     }
-    if (r.nodraw) return;
-    const PMap cm = block_chunk_map(thread_map(t, nvalid, rc[b].beta_c), sh);
-    if (tid == 0) rc[b].cmap = cm;
 }
 
 /* -------------------------------------------------------- 6: the draw */
 
 /* One workgroup per row: the first index whose left-to-right binary32
- * running sum of p reaches thr (Model.pas:2727-2735), else the argmax. */
+ * running sum of p reaches thr (Model.pas:2727-2735, 2811-2824), else the
+ * argmax. */
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
 {
-    __shared__ FullShared sh;
+    __shared__ ChainShared<DT> sh;
     const int tid = threadIdx.x;
     const int row = blockIdx.y;
     const int V = a.vocab;
     const RowIn ri = row_in(a, row);
-    if (!is_full_row(ri.p.top_k, V)) return;
+    Mask k;
+    if (!row_mask(a, row, ri, k)) return;
     const FullRow r = a.ws.rows[row];
     if (r.c_last < 0) return;
-    if (r.nodraw) {
-        if (tid < 64) write_row_outputs(a, row, r.argmax, r.argmax, r.lsum, G4S_FLAG_FULL_PATH);
+    const uint32_t fl = row_flags(k);
+    if (r.nodraw == 1) {
+        if (tid < 64) write_row_outputs(a, row, r.argmax, r.argmax, r.lsum, r.count, fl);
         return;
     }
-    const char* rowp = reinterpret_cast<const char*>(a.logits) +
-                       (int64_t)row * a.row_stride * Elem<DT>::SIZE;
+    if (r.nodraw == 2) {
+        if (tid < 64)
+            write_row_outputs(a, row, r.first, r.argmax, r.lsum, r.count,
+                              fl | G4S_FLAG_DREW | G4S_FLAG_REACHED);
+        return;
+    }
+    const char* rowp = row_ptr<DT>(a, row);
     FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
     const int nch = a.nch;
     for (int cb = tid; cb < nch; cb += kFullBlock) {
         sh.cmap[cb] = cb <= r.c_last ? rc[cb].cmap : ss::map_identity();
         sh.cbeta[cb] = cb <= r.c_last ? rc[cb].beta_c : -1;
     }
-    if (tid == 0) sh.misc[12] = 0;
-    const Ctx c = load_ctx<DT>(a, row, r, sh); /* ends with a barrier */
-    const float inv = r.inv;
+    if (tid == 0) sh.s.misc[12] = 0;
+    const Ctx c = make_ctx(a, r, k.cls);
+    load_tab<DT>(a, row, r, sh.tab); /* ends with a barrier */
     const float thr = r.thr;
 
     uint32_t raw[kFullPer];
@@ -856,16 +1477,16 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
         ++reev;
         const int64_t f0 = (int64_t)cb * kFullChunk + (int64_t)tid * kFullPer;
         const int nv = load16<DT>(rowp, f0, V, raw);
+        terms_e<DT>(raw, nv, f0, c, k, sh.tab, t);
 #pragma unroll
-        for (int j = 0; j < kFullPer; ++j)
-            t[j] = (j < nv) ? e_of<DT>(raw[j], c, sh.tab) * inv : 0.0f;
+        for (int j = 0; j < kFullPer; ++j) t[j] = p_of(t[j], k.cls, r.inv, r.lsum);
         int pos = 0;
         if (cb == 0) {
-            head_walk(t, thr, sh);
+            head_walk(t, thr, sh.s);
             __syncthreads();
-            st.e = sh.misc[9];
-            st.m = sh.misc[10];
-            const int hh = sh.misc[11];
+            st.e = sh.s.misc[9];
+            st.m = sh.s.misc[10];
+            const int hh = sh.s.misc[11];
             __syncthreads();
             if (hh >= 0) {
                 hit = hh;
@@ -874,7 +1495,7 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
             pos = kHead / kFullPer;
         }
         int h;
-        st = resolve_chunk(t, nv, st, thr, pos, &h, sh);
+        st = resolve_chunk(t, nv, st, thr, pos, &h, sh.s);
         if (h >= 0) {
             hit = (int64_t)cb * kFullChunk + h;
             break;
@@ -882,15 +1503,15 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
     }
     if (tid == 0) {
         a.ws.rows[row].c_reev = reev;
-        a.ws.rows[row].c_rounds = sh.misc[12];
+        a.ws.rows[row].c_rounds = sh.s.misc[12];
     }
-    uint32_t flags = G4S_FLAG_FULL_PATH | G4S_FLAG_DREW;
+    uint32_t flags = fl | G4S_FLAG_DREW;
     int32_t id = r.argmax;
     if (hit >= 0) {
         id = (int32_t)hit;
         flags |= G4S_FLAG_REACHED;
     }
-    if (tid < 64) write_row_outputs(a, row, id, r.argmax, r.lsum, flags);
+    if (tid < 64) write_row_outputs(a, row, id, r.argmax, r.lsum, r.count, flags);
 }
 
 /* ---------------------------------------------------------------- host */
@@ -902,41 +1523,57 @@ bool full_supported(int32_t vocab)
 
 hipError_t full_alloc(FullWorkspace& ws, int32_t vocab, int32_t max_batch)
 {
-    (void)vocab;
     const size_t mb = (size_t)max_batch;
+    ws.bits_stride = (vocab + 31) / 32;
     hipError_t e = hipMalloc((void**)&ws.rows, mb * sizeof(FullRow));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.chunks, mb * kFullMaxChunks * sizeof(FullChunk));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.etab, mb * kFullTab * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void**)&ws.tickets, mb * 4 * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.sel, mb * sizeof(WideSel));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.hist, mb * kWideBins * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.ties, mb * kFullMaxChunks * sizeof(TieRec));
+    if (e == hipSuccess)
+        e = hipMalloc((void**)&ws.bits, mb * (size_t)ws.bits_stride * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.heap_v, (size_t)vocab * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.heap_i, (size_t)vocab * sizeof(int32_t));
     return e;
 }
 
 void full_free(FullWorkspace& ws)
 {
-    if (ws.rows) (void)hipFree(ws.rows);
-    if (ws.chunks) (void)hipFree(ws.chunks);
-    if (ws.etab) (void)hipFree(ws.etab);
-    if (ws.tickets) (void)hipFree(ws.tickets);
+    void* ptrs[] = {ws.rows, ws.chunks, ws.etab, ws.sel, ws.hist,
+                    ws.ties, ws.bits, ws.heap_v, ws.heap_i};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
     ws = FullWorkspace{};
 }
 
 hipError_t full_init(FullWorkspace& ws, int32_t max_batch, hipStream_t s)
 {
-    return hipMemsetAsync(ws.tickets, 0, (size_t)max_batch * 4 * sizeof(uint32_t), s);
+    return hipMemsetAsync(ws.hist, 0, (size_t)max_batch * kWideBins * sizeof(uint32_t), s);
 }
 
 template <int DT>
 static hipError_t launch_dt(const FullArgs& a, hipStream_t s)
 {
     const dim3 grid((unsigned)a.nch, (unsigned)a.batch);
-    hipLaunchKernelGGL((full_max_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
-    if (DT == 1)
-        hipLaunchKernelGGL(full_table_kernel, dim3(kFullTab / kFullBlock, (unsigned)a.batch),
-                           dim3(kFullBlock), 0, s, a);
     const dim3 rows(1u, (unsigned)a.batch);
-    hipLaunchKernelGGL((full_lsum_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
+    const dim3 grid4((unsigned)((a.nch + kFullCPW - 1) / kFullCPW), (unsigned)a.batch);
+    if (a.wide_on) {
+        for (int pass = 0; pass < 3; ++pass) {
+            hipLaunchKernelGGL((wide_hist_kernel<DT>), grid, dim3(kFullBlock), 0, s, a, pass);
+            hipLaunchKernelGGL(wide_find_kernel, rows, dim3(kFullBlock), 0, s, a, pass);
+        }
+        hipLaunchKernelGGL((wide_ties_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
+        hipLaunchKernelGGL((wide_ties_find_kernel<DT>), rows, dim3(kFullBlock), 0, s, a);
+        hipLaunchKernelGGL((wide_replay_kernel<DT>), dim3(1), dim3(64), 0, s, a);
+    }
+    hipLaunchKernelGGL((full_max_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_row_kernel<DT>),
+                       dim3(DT == 1 ? (unsigned)(kFullTab / kFullBlock) : 1u, (unsigned)a.batch),
+                       dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_lsum_kernel<DT>), grid4, dim3(kFullBlock), 0, s, a);
     hipLaunchKernelGGL((full_lsum_chain_kernel<DT>), rows, dim3(kFullBlock), 0, s, a);
-    hipLaunchKernelGGL((full_cdf_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_cdf_kernel<DT>), grid4, dim3(kFullBlock), 0, s, a);
     hipLaunchKernelGGL((full_cdf_chain_kernel<DT>), rows, dim3(kFullBlock), 0, s, a);
     return hipGetLastError();
 }

@@ -123,8 +123,8 @@ int check_logits(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t ro
  * (or inline p0/u0 when d_params is NULL). */
 int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride, int32_t batch,
             const g4s_params* d_params, const double* d_u, const g4s_params* p0, double u0,
-            int32_t kbound, bool full_rows, int32_t* d_ids, const g4s_outputs* outputs,
-            uint32_t* done = nullptr, uint32_t seq = 0)
+            int32_t kbound, bool full_rows, bool wide, int32_t* d_ids,
+            const g4s_outputs* outputs, uint32_t* done = nullptr, uint32_t seq = 0)
 {
     g4s_outputs out{};
     if (outputs) out = *outputs;
@@ -145,6 +145,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         a.splits = cfg.splits;
         a.cap_log2 = cfg.cap_log2;
         a.kbound = kbound;
+        a.wide_on = wide ? 1 : 0;
         a.softcap = s->softcap;
         a.cand = s->cand;
         a.merge = s->merge;
@@ -157,11 +158,12 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         hipError_t e = g4s::topk_launch(cfg, a, dtype, s->stream);
         if (e != hipSuccess) return hip_fail(s, e, "top-k kernel launch");
     }
-    if (full_rows) {
+    if (full_rows || wide) {
         if (!g4s::full_supported(s->vocab))
             return fail(s, G4S_ERR_UNSUPPORTED,
-                        "the full-vocabulary path supports vocab <= %d (TopK <= 0 or >= V)",
-                        g4s::kFullChunk * g4s::kFullMaxChunks);
+                        "the softmax path (TopK <= 0, TopK >= V, or TopK > %d) supports vocab "
+                        "<= %d",
+                        g4s::kMaxTopK, g4s::kFullChunk * g4s::kFullMaxChunks);
         g4s::FullArgs f{};
         f.logits = d_logits;
         f.row_stride = row_stride;
@@ -173,6 +175,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         f.u0 = u0;
         f.softcap = s->softcap;
         f.nch = (s->vocab + g4s::kFullChunk - 1) / g4s::kFullChunk;
+        f.wide_on = wide ? 1 : 0;
         f.ws = s->full;
         f.ids = d_ids;
         f.done = done;
@@ -301,15 +304,13 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
     if (!params || !u || !ids)
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "params, u and ids must be non-NULL");
     int32_t kbound = 0;
-    bool full_rows = false;
+    bool full_rows = false, wide = false;
     for (int32_t r = 0; r < batch; ++r) {
         if (is_topk_row(params[r], s->vocab)) {
             if (params[r].top_k > g4s::kMaxTopK)
-                return fail(s, G4S_ERR_UNSUPPORTED,
-                            "row %d: TopK %d exceeds the top-k path limit %d (TopK <= 0 or >= V "
-                            "selects the full-vocabulary path)",
-                            r, params[r].top_k, g4s::kMaxTopK);
-            kbound = params[r].top_k > kbound ? params[r].top_k : kbound;
+                wide = true;
+            else
+                kbound = params[r].top_k > kbound ? params[r].top_k : kbound;
         } else {
             full_rows = true;
         }
@@ -338,7 +339,7 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
 
     if (batch == 1) {
         rc = enqueue(s, d_logits, dtype, row_stride, 1, nullptr, nullptr, &params[0], u[0], kbound,
-                     full_rows, s->h_ids, &out, done, seq);
+                     full_rows, wide, s->h_ids, &out, done, seq);
     } else {
         std::memcpy(s->h_params, params, sizeof(g4s_params) * batch);
         std::memcpy(s->h_u, u, sizeof(double) * batch);
@@ -349,7 +350,7 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
                                s->stream);
         if (e != hipSuccess) return hip_fail(s, e, "parameter upload");
         rc = enqueue(s, d_logits, dtype, row_stride, batch, s->d_params, s->d_u, nullptr, 0.0,
-                     kbound, full_rows, s->h_ids, &out, done, seq);
+                     kbound, full_rows, wide, s->h_ids, &out, done, seq);
     }
     if (rc) return rc;
     hipError_t e = hipSuccess;
@@ -400,12 +401,13 @@ G4S_API int g4s_sample_async(g4s_sampler* s, const void* d_logits, int32_t dtype
     if (rc) return rc;
     if (!d_params || !d_u || !d_ids)
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "d_params, d_u and d_ids must be non-NULL");
-    if (k_bound < 0 || k_bound > g4s::kMaxTopK)
-        return fail(s, G4S_ERR_UNSUPPORTED, "k_bound %d outside [0, %d]", k_bound, g4s::kMaxTopK);
+    if (k_bound < 0 || k_bound >= s->vocab)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "k_bound %d outside [0, %d)", k_bound, s->vocab);
     if (k_bound == 0 && !full_rows)
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "k_bound == 0 and full_rows == 0: nothing to do");
-    return enqueue(s, d_logits, dtype, row_stride, batch, d_params, d_u, nullptr, 0.0, k_bound,
-                   full_rows != 0, d_ids, outputs);
+    const bool wide = k_bound > g4s::kMaxTopK;
+    return enqueue(s, d_logits, dtype, row_stride, batch, d_params, d_u, nullptr, 0.0,
+                   wide ? g4s::kMaxTopK : k_bound, full_rows != 0, wide, d_ids, outputs);
 }
 
 G4S_API int g4s_lmhead_q4_0(g4s_sampler* s, const void* d_weights, int32_t rows, int32_t cols,

@@ -36,6 +36,7 @@ struct TopkArgs {
     int32_t splits;
     int32_t cap_log2; /* candidate slots per chunk = 1 << cap_log2 (>= 2 * kbound) */
     int32_t kbound;   /* every top-k row has TopK <= kbound */
+    int32_t wide_on;  /* rows with TopK > kMaxTopK are left to the wide launches */
     float softcap;
     uint64_t* cand;   /* [batch][kCandRow] chunk candidates */
     uint64_t* merge;  /* [batch][kCandRow] merge candidates beyond what LDS holds */

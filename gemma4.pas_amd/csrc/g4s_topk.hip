@@ -186,6 +186,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     const int K = rp.top_k;
     if (!(K >= 1 && K < V)) return; /* full-vocabulary row (Model.pas:2756) */
     if (K > a.kbound) {
+        if (a.wide_on && K > kMaxTopK) return; /* a wide row (g4s_full.hip) */
         if (chunk == 0 && wid == 0) {
             if (lane == 0) {
                 a.ids[row] = -1;

@@ -36,6 +36,7 @@ FLAG_TIE_LOWEST = 0x10
 FLAG_HEAP_REPLAY = 0x20
 FLAG_CHUNK_EXACT = 0x40
 FLAG_WIDE_MERGE = 0x80
+FLAG_WIDE_K = 0x100
 FLAG_EMPTY = 0x40000000
 FLAG_ERROR = 0x80000000
 

@@ -46,7 +46,7 @@ typedef enum g4s_dtype {
 typedef enum g4s_status {
     G4S_OK = 0,
     G4S_ERR_INVALID_ARGUMENT = -1, /* null pointer, bad size, misaligned logits, ... */
-    G4S_ERR_UNSUPPORTED = -2,      /* e.g. 1024 < TopK < V (see g4s_max_top_k) */
+    G4S_ERR_UNSUPPORTED = -2,      /* e.g. a vocabulary above 2^22 on the softmax path */
     G4S_ERR_NO_DEVICE = -3,        /* no HIP device / wrong architecture */
     G4S_ERR_OUT_OF_MEMORY = -4,    /* workspace allocation failed at create */
     G4S_ERR_HIP = -5,              /* a HIP runtime call failed */
@@ -72,6 +72,7 @@ typedef struct g4s_params {
 #define G4S_FLAG_HEAP_REPLAY 0x20u  /* K-th value tied; resolved by replaying the min-heap */
 #define G4S_FLAG_CHUNK_EXACT 0x40u  /* a vocabulary chunk needed the exact per-chunk select */
 #define G4S_FLAG_WIDE_MERGE 0x80u   /* the merge candidate set exceeded on-chip memory */
+#define G4S_FLAG_WIDE_K 0x100u      /* TopK above g4s_max_top_k(): radix select over the whole row */
 #define G4S_FLAG_EMPTY 0x40000000u  /* no logit above -1e30 on the top-k path */
 #define G4S_FLAG_ERROR 0x80000000u  /* row rejected (e.g. TopK above the launch bound) */
 
@@ -101,7 +102,10 @@ const char* g4s_version(void);
  * T = 1.0, TopK = 64, TopP = 0.95, RepetitionPenalty = 1.0. */
 void g4s_params_set_defaults(g4s_params* params);
 
-/* Largest TopK the top-k path accepts (TopK <= 0 or >= V selects the full path). */
+/* Largest TopK of the single-launch top-k kernel.  Rows with a larger TopK
+ * (below V) take the wide top-k path: a radix select over the whole row with
+ * the same semantics (G4S_FLAG_WIDE_K).  TopK <= 0 or >= V selects the full
+ * path. */
 int32_t g4s_max_top_k(void);
 
 /* Create a sampler for `vocab` logits per row and up to `max_batch` rows per
@@ -140,7 +144,8 @@ int g4s_sample_ex(g4s_sampler* sampler, const void* d_logits, int32_t dtype, int
 /* Stream-ordered variant for callers that keep parameters on the device
  * (graph capture, serving loops).  d_params, d_u and d_ids are device
  * arrays of `batch` entries.  `k_bound` >= every TopK of a top-k-path row
- * (1..g4s_max_top_k(); 0 when no row takes the top-k path) sizes the launch;
+ * (0 < TopK < V; k_bound 0 when no row takes the top-k path) sizes the
+ * launch: above g4s_max_top_k() the wide top-k launches are added;
  * `full_rows` != 0 when some row may take the full-vocabulary path.  Rows
  * that violate k_bound get id -1 and G4S_FLAG_ERROR.  Returns after
  * enqueueing; results are valid once the stream reaches this point. */

@@ -240,9 +240,22 @@ def test_bf16_logits_topk(orc):
 
 
 def test_argument_errors_on_device(big):
-    d = hip.Buffer(V * 4)
-    rc, _ = big.sample(d, 1, [native.TSamplingParams.make(1.0, 2000, 0.9)], [0.5], check=False)
-    assert rc == native.G4S_ERR_UNSUPPORTED and "TopK" in big.last_error()
+    d = hip.Buffer.from_array(np.zeros(V, F32))
+    # TopK above g4s_max_top_k() takes the wide path: all-equal logits keep
+    # the first 2000 indices (lowest-index tie rule), each p = fl32(1/2000);
+    # u=0.5 picks the first index whose binary32 running sum reaches 0.5
+    rc, ids = big.sample(d, 1, [native.TSamplingParams.make(1.0, 2000, 1.0)], [0.5], check=False)
+    p, c, want = F32(1.0) / F32(2000.0), F32(0.0), -1
+    for i in range(2000):
+        c = F32(c + p)
+        if c >= F32(0.5):
+            want = i
+            break
+    assert rc == native.G4S_OK and ids[0] == want, (rc, ids, want, big.last_error())
+    di = hip.Buffer(4)
+    rc = native.load().g4s_sample_async(big.h, d.addr, native.DTYPE_F32, V, 1, d.addr, d.addr,
+                                        V, 0, di.addr, None)
+    assert rc == native.G4S_ERR_INVALID_ARGUMENT and "k_bound" in big.last_error()
     rc, _ = big.sample(d, 1, [native.TSamplingParams.make(1.0, 5, 0.9)], [1.0], check=False)
     assert rc == native.G4S_ERR_INVALID_ARGUMENT
     rc, _ = big.sample(d.offset(4), 1, [native.TSamplingParams.make(1.0, 5, 0.9)], [0.5],
