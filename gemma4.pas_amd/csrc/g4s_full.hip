@@ -527,23 +527,18 @@ __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st,
             return st;
         }
         if (tid == tstar) {
-            /* m_in is exact: every earlier thread stayed in the binade */
-            State s2{e, m_in};
+            /* m_in is exact (every earlier thread stayed in the binade), so
+             * the thread's terms are plain binary32 additions from there */
+            float sum = ss::value_of(State{e, m_in});
             int h = -1;
 #pragma unroll
             for (int j = 0; j < kFullPer; ++j) {
-                if (j >= nvalid) break;
-                const int32_t m2 =
-                    ss::map_apply(ss::map_of_ct(ss::term_ct(t[j], s2.e)), s2.m);
-                if (m2 < ss::kTop)
-                    s2.m = m2;
-                else
-                    s2 = ss::step_add(s2, t[j]);
-                if (ss::value_of(s2) >= thr) {
-                    h = tstar * kFullPer + j;
-                    break;
+                if (j < nvalid && h < 0) {
+                    sum = sum + t[j];
+                    if (sum >= thr) h = tstar * kFullPer + j;
                 }
             }
+            const State s2 = ss::state_of(sum);
             sh.misc[9] = s2.e;
             sh.misc[10] = s2.m;
             sh.misc[11] = h;
@@ -560,6 +555,44 @@ __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st,
         pos = tstar + 1;
     }
     return st;
+}
+
+/* Chain the chunk maps from chunk cb on, while they apply: a chunk's map
+ * applies when the sum enters it in the predicted binade and the result
+ * stays in that binade (and, for the draw, below thr).  Wave 0 walks the
+ * chunks with the maps held one per lane (readlane per chunk); the state
+ * after the last accepted chunk goes to sh.misc[9..10] and the first chunk
+ * that does not apply (nch: none) to sh.misc[14].  Ends with a barrier. */
+__device__ void chain_maps(const PMap* cmap, const int32_t* cbeta, int cb, int nch, State st,
+                           float thr, Scratch& sh)
+{
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        int stop = nch;
+        for (int g = cb; g < nch && stop == nch; g += 64) {
+            const int c = g + lane;
+            const PMap f = c < nch ? cmap[c] : ss::map_identity();
+            const int32_t be = c < nch ? cbeta[c] : -1;
+            const int n = nch - g < 64 ? nch - g : 64;
+            for (int l = 0; l < n; ++l) {
+                const int32_t bl = __builtin_amdgcn_readlane(be, l);
+                const int32_t d0 = __builtin_amdgcn_readlane(f.d0, l);
+                const int32_t d1 = __builtin_amdgcn_readlane(f.d1, l);
+                const int32_t m2 = st.m + ((st.m & 1) ? d1 : d0);
+                if (st.e != bl || m2 >= ss::kTop || ss::value_of(State{st.e, m2}) >= thr) {
+                    stop = g + l;
+                    break;
+                }
+                st.m = m2;
+            }
+        }
+        if (lane == 0) {
+            sh.misc[9] = st.e;
+            sh.misc[10] = st.m;
+            sh.misc[14] = stop;
+        }
+    }
+    __syncthreads();
 }
 
 /* The row's first kHead terms (threads 0 .. kHead/16 - 1 of chunk 0), where
@@ -1265,13 +1298,14 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
     float t[kFullPer];
     State st = ss::state_of(0.0f);
     int reev = 0;
-    for (int cb = 0; cb < nch; ++cb) {
-        if (cb > 0 && st.e == sh.cbeta[cb]) {
-            const int32_t m2 = ss::map_apply(sh.cmap[cb], st.m);
-            if (m2 < ss::kTop) {
-                st.m = m2;
-                continue;
-            }
+    for (int cb = 0; cb < nch;) {
+        if (cb > 0) {
+            chain_maps(sh.cmap, sh.cbeta, cb, nch, st, __builtin_inff(), sh.s);
+            st.e = sh.s.misc[9];
+            st.m = sh.s.misc[10];
+            cb = sh.s.misc[14];
+            __syncthreads();
+            if (cb >= nch) break;
         }
         ++reev;
         const int64_t f0 = (int64_t)cb * kFullChunk + (int64_t)tid * kFullPer;
@@ -1288,6 +1322,7 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
         }
         int h;
         st = resolve_chunk(t, nv, st, __builtin_inff(), pos, &h, sh.s);
+        ++cb;
     }
     const float lsum = ss::value_of(st);
     const float inv = div_cr32(1.0f, lsum);                            /* Tensors.pas:668 */
@@ -1467,12 +1502,13 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
     int64_t hit = -1;
     int reev = 0;
     for (int cb = 0; cb < nch; ++cb) {
-        if (cb > 0 && st.e == sh.cbeta[cb]) {
-            const int32_t m2 = ss::map_apply(sh.cmap[cb], st.m);
-            if (m2 < ss::kTop && ss::value_of(State{st.e, m2}) < thr) {
-                st.m = m2;
-                continue;
-            }
+        if (cb > 0) {
+            chain_maps(sh.cmap, sh.cbeta, cb, nch, st, thr, sh.s);
+            st.e = sh.s.misc[9];
+            st.m = sh.s.misc[10];
+            cb = sh.s.misc[14];
+            __syncthreads();
+            if (cb >= nch) break;
         }
         ++reev;
         const int64_t f0 = (int64_t)cb * kFullChunk + (int64_t)tid * kFullPer;
