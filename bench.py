@@ -13,10 +13,11 @@ synchronous call (entry to token id on the host), in microseconds.
 Also reported on the same line: p99, the batched mixed-settings workload
 (B=64 fp32, per-row T/K/P) as rows/s and GB/s, the flat bf16 full-vocabulary
 workload (B=256, TopK disabled, P=0.99) as rows/s, GB/s and the fraction of
-the HBM roofline, the roofline of the dominant kernel measured with HIP
-events on the sampler's stream, and the CPU oracle's per-row latency on the
-host (one core, a bounded sample of the same rows).  Every sampled id of the
-timed rows is checked against the CPU oracle.
+the HBM roofline, the Q4_0 LM head + sampler workload (B=32 hidden vectors,
+262144 x 2560 weights) as us per batch, the roofline of the dominant kernel
+measured with HIP events on the sampler's stream, and the CPU oracle's
+per-row latency on the host (one core, a bounded sample of the same rows).
+Every sampled id of the timed rows is checked against the CPU oracle.
 """
 import argparse
 import ctypes
@@ -73,6 +74,8 @@ def harness():
     H.g4h_batch_throughput.argtypes = [vp, vp, vp, i32, i64, i32, vp, vp, i32, i32, vp, i32,
                                        i32, vp, vp, vp]
     H.g4h_copy_throughput.argtypes = [vp, vp, vp, i64, i32, vp]
+    H.g4h_lmhead_sampler.argtypes = [vp, vp, vp, i32, i32, vp, i32, vp, vp, vp, i32, vp, i32, i32,
+                                     vp, vp]
     return H
 
 
@@ -188,6 +191,57 @@ def probe(H, stream, name, steps):
         raise ValueError(f"unknown probe {name}")
     print(json.dumps(res), flush=True)
     return 0
+
+
+def lmhead_sampler(H, stream, threads, steps):
+    """LM head + sampler: 32 hidden vectors ~ N(0,1), 262144 x 2560 Q4_0
+    weights (fp16 scales U(0.001, 0.02)), then T=0.7, K=64, P=0.95.  Every
+    id is checked against the CPU oracle's sampler on the same logits, and
+    the logits of 256 weight rows against the oracle's CpuMatVecQ4."""
+    from gemma4_sampler import hip, native, workload as wl
+    from oracle import oracle as orc
+    B, rows, cols = 32, V, wl.HIDDEN_GEMMA4
+    s = native.Sampler(V, max_batch=B, softcap=wl.SOFTCAP_GEMMA4, stream=stream)
+    dw = hip.Buffer(rows * (cols // 32) * 18)
+    wl.dev_q4_weights(dw, SEED + 5, rows, cols, stream=stream)
+    hidden = wl.host_hidden(SEED + 6, B, cols)
+    dh = hip.Buffer.from_array(hidden)
+    dl = hip.Buffer(4 * B * rows)
+    par = [native.TSamplingParams.make(0.7, 64, 0.95)] * B
+    parr = native.params_array(par)
+    dp = hip.Buffer(ctypes.sizeof(parr))
+    hip.check(hip.lib().hipMemcpy(dp.ptr, parr, ctypes.sizeof(parr), hip.H2D))
+    u = wl.host_row_u(SEED + 7, 0, B)
+    du = hip.Buffer.from_array(u)
+    di = hip.Buffer(4 * B)
+    stream.synchronize()
+    lm = np.zeros(steps, np.float32)
+    tot = np.zeros(steps, np.float32)
+    rc = H.g4h_lmhead_sampler(s.h, stream.handle, dw.ptr, rows, cols, dh.ptr, B, dl.ptr, dp.ptr,
+                              du.ptr, 64, di.ptr, 2, steps, _vp(lm), _vp(tot))
+    if rc != 0:
+        raise RuntimeError(f"g4h_lmhead_sampler failed: {rc} {s.last_error()}")
+    logits = dl.download(np.float32).reshape(B, rows)
+    ids = di.download(np.int32)
+    want = orc.sample_batch(logits, 0, V, V, (np.full(B, 0.7, np.float32), np.full(B, 64, np.int32),
+                                              np.full(B, 0.95, np.float32)), u,
+                            softcap=wl.SOFTCAP_GEMMA4, threads=threads)
+    w_part = wl.host_q4_weights(SEED + 5, 256, cols, block0=123456 * (cols // 32))
+    ref = orc.matvec_q4_batch(w_part, hidden, 256, cols, threads=threads)
+    logit_bad = int(np.sum(logits[:, 123456:123456 + 256].view(np.uint32) != ref.view(np.uint32)))
+    s.close()
+    for b in (dw, dh, dl, dp, du, di):
+        b.free()
+    lm50, tot50 = float(np.median(lm)), float(np.median(tot))
+    wbytes = rows * (cols // 32) * 18
+    flops = 2.0 * B * rows * cols
+    return {"batch": B, "us_per_batch_p50": tot50, "lmhead_us_p50": lm50,
+            "sampler_us_p50": tot50 - lm50, "weights_bytes": wbytes,
+            "lmhead_hbm_gbps": wbytes / (lm50 * 1e-6) / 1e9,
+            "lmhead_tflops": flops / (lm50 * 1e-6) / 1e12,
+            "lmhead_frac_fp32_peak": flops / (lm50 * 1e-6) / 157.3e12,
+            "id_mismatches": int(np.sum(ids != want)),
+            "logit_mismatches_in_256_checked_rows": logit_bad}
 
 
 def batch_throughput(H, stream, d_logits, dtype, batch, params, u, k_bound, full_rows, warmup,
@@ -324,6 +378,17 @@ def main():
         b256["status"] = f"not available: {e}"
         log(f"B=256 bf16 full path: {e}")
 
+    # ---- LM head (Q4_0, B=32) + sampler --------------------------------------
+    c5 = {"batch": 32, "status": "not measured"}
+    try:
+        c5 = lmhead_sampler(H, stream, threads, max(10, args.batch_steps // 5))
+        log(f"LM head + sampler B=32: {c5['us_per_batch_p50']:.1f} us/batch (LM head "
+            f"{c5['lmhead_us_p50']:.1f} us, {c5['lmhead_tflops']:.1f} TFLOP/s), mismatches "
+            f"{c5['id_mismatches']}")
+    except (native.SamplerError, RuntimeError) as e:
+        c5["status"] = f"not available: {e}"
+        log(f"LM head + sampler: {e}")
+
     # ---- CPU baseline (timed above, on the same rows) ---------------------
     cpu = None
     if not args.no_cpu and len(cpu_lat):
@@ -365,10 +430,12 @@ def main():
                      "algorithmic_bytes": algo_bytes},
         "b64_mixed": b64,
         "b256_flat_full": b256,
+        "c5_lmhead_sampler": c5,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
-    return 0 if (bad + bad_async + bad3 + b256.get("id_mismatches", 0)) == 0 else 1
+    return 0 if (bad + bad_async + bad3 + b256.get("id_mismatches", 0) +
+                 c5.get("id_mismatches", 0)) == 0 else 1
 
 
 if __name__ == "__main__":

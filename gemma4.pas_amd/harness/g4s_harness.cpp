@@ -266,3 +266,48 @@ G4H_API int g4h_copy_throughput(void* stream, const void* src, void* dst, int64_
     for (auto& e : ev) (void)hipEventDestroy(e);
     return rc;
 }
+
+/*
+ * LM head + sampler, stream-ordered: per step g4s_lmhead_q4_0 into d_logits
+ * then g4s_sample_async on them.  lm_us[i] / total_us[i] = event times of the
+ * LM head alone and of the whole step i.  `warmup` untimed steps first.
+ */
+G4H_API int g4h_lmhead_sampler(g4s_sampler* s, void* stream, const void* d_weights, int32_t rows,
+                               int32_t cols, const float* d_hidden, int32_t batch, float* d_logits,
+                               const g4s_params* d_params, const double* d_u, int32_t k_bound,
+                               int32_t* d_ids, int32_t warmup, int32_t steps, float* lm_us,
+                               float* total_us)
+{
+    hipStream_t st = (hipStream_t)stream;
+    std::vector<hipEvent_t> ev((size_t)steps * 3);
+    for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) return -100;
+    int rc = 0;
+    for (int32_t i = 0; rc == 0 && i < warmup; ++i) {
+        rc = g4s_lmhead_q4_0(s, d_weights, rows, cols, d_hidden, batch, d_logits, rows);
+        if (rc == 0)
+            rc = g4s_sample_async(s, d_logits, G4S_DTYPE_F32, rows, batch, d_params, d_u, k_bound,
+                                  0, d_ids, nullptr);
+    }
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    for (int32_t i = 0; rc == 0 && i < steps; ++i) {
+        (void)hipEventRecord(ev[(size_t)i * 3], st);
+        rc = g4s_lmhead_q4_0(s, d_weights, rows, cols, d_hidden, batch, d_logits, rows);
+        (void)hipEventRecord(ev[(size_t)i * 3 + 1], st);
+        if (rc == 0)
+            rc = g4s_sample_async(s, d_logits, G4S_DTYPE_F32, rows, batch, d_params, d_u, k_bound,
+                                  0, d_ids, nullptr);
+        (void)hipEventRecord(ev[(size_t)i * 3 + 2], st);
+    }
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    if (rc == 0)
+        for (int32_t i = 0; i < steps; ++i) {
+            float a = 0.0f, b = 0.0f;
+            (void)hipEventElapsedTime(&a, ev[(size_t)i * 3], ev[(size_t)i * 3 + 1]);
+            (void)hipEventElapsedTime(&b, ev[(size_t)i * 3], ev[(size_t)i * 3 + 2]);
+            lm_us[i] = a * 1000.0f;
+            total_us[i] = b * 1000.0f;
+        }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    return rc;
+}

@@ -1,0 +1,97 @@
+"""GPU parity of the Q4_0 LM head (g4s_lmhead_q4_0) against the oracle's
+CpuMatVecQ4 restatement (src/Gemma4.Tensors.pas:546-598), and of the
+LM head + sampler workload (B=32 hidden vectors, 262144 x 2560 weights, the
+decode-stream sampling settings) through the C ABI.
+
+Logits must equal the oracle's bit for bit: the kernel evaluates every
+term in the reference's order with one binary32 fma, which is what the
+reference's Extended-precision step rounds to for these magnitudes.  The
+sampled ids are then the sampler's, compared against the oracle sampler on
+the same logits.
+"""
+import numpy as np
+import pytest
+
+from gemma4_sampler import hip, native, workload as wl
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+D = wl.HIDDEN_GEMMA4
+V = wl.V_GEMMA4
+
+
+def _lmhead(s, w_host_or_buf, rows, cols, hidden):
+    B = hidden.shape[0]
+    dw = w_host_or_buf if isinstance(w_host_or_buf, hip.Buffer) else \
+        hip.Buffer.from_array(w_host_or_buf)
+    dh = hip.Buffer.from_array(np.ascontiguousarray(hidden, F32))
+    dl = hip.Buffer(4 * B * rows)
+    s.lmhead_q4_0(dw, rows, cols, dh, B, dl, rows)
+    hip.synchronize()
+    return dl.download(F32).reshape(B, rows)
+
+
+@pytest.mark.parametrize("batch", [1, 5, 32, 40])
+def test_lmhead_small_bit_exact(orc, batch):
+    rows, cols = 700, D
+    w = wl.host_q4_weights(77, rows, cols)
+    hidden = wl.host_hidden(78 + batch, batch, cols)
+    s = native.Sampler(V, max_batch=1, softcap=30.0)
+    got = _lmhead(s, w, rows, cols, hidden)
+    want = orc.matvec_q4_batch(w, hidden, rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+        f"{np.sum(got != want)} logits differ"
+    s.close()
+
+
+def test_lmhead_scale_edge_cases(orc):
+    """fp16 scales that are zero, subnormal (the reference's own decoding of
+    them, Types.pas:452-466), the largest finite, and negative; tiny and
+    large hidden values."""
+    rows, cols = 64, 256
+    rng = np.random.default_rng(5)
+    w = wl.host_q4_weights(79, rows, cols).reshape(rows * cols // 32, 18)
+    specials = [0x0000, 0x8000, 0x0001, 0x0200, 0x03FF, 0x8155, 0x0400, 0x7BFF, 0xFBFF, 0x3C00]
+    for i in range(w.shape[0]):
+        if i % 3 == 0:
+            v = specials[(i // 3) % len(specials)]
+            w[i, 0], w[i, 1] = v & 0xFF, v >> 8
+    w = w.reshape(-1)
+    hidden = rng.normal(0, 1, (3, cols)).astype(F32)
+    hidden[1] *= 1e-20
+    hidden[2] *= 1e3
+    s = native.Sampler(V, max_batch=1, softcap=30.0)
+    got = _lmhead(s, w, rows, cols, hidden)
+    want = orc.matvec_q4_batch(w, hidden, rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    s.close()
+
+
+def test_lmhead_plus_sampler_full_size(orc):
+    """The full LM head + sampler workload: 32 hidden vectors ~ N(0,1),
+    262144 x 2560 Q4_0 weights (generated on the device), T=0.7, K=64,
+    P=0.95.  Logits of 1024 weight rows checked against the oracle; every
+    sampled id checked against the oracle sampler on the same logits."""
+    B, rows, cols = 32, V, D
+    nblocks = rows * (cols // 32)
+    dw = hip.Buffer(nblocks * 18)
+    wl.dev_q4_weights(dw, 80, rows, cols)
+    hidden = wl.host_hidden(81, B, cols)
+    s = native.Sampler(V, max_batch=B, softcap=30.0)
+    logits = _lmhead(s, dw, rows, cols, hidden)
+    # rows 0..511 and 200000..200511 against the oracle
+    for r0 in (0, 200000):
+        w_part = wl.host_q4_weights(80, 512, cols, block0=r0 * (cols // 32))
+        want = orc.matvec_q4_batch(w_part, hidden, 512, cols)
+        got = logits[:, r0:r0 + 512]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"rows {r0}+"
+    # sampling on the device-resident logits
+    dl = hip.Buffer.from_array(logits)
+    t = np.full(B, 0.7, F32)
+    k = np.full(B, 64, np.int32)
+    p = np.full(B, 0.95, F32)
+    u = wl.host_row_u(82, 0, B)
+    _, ids = s.sample(dl, B, [native.TSamplingParams.make(0.7, 64, 0.95)] * B, u)
+    want = orc.sample_batch(logits, 0, V, V, (t, k, p), u, softcap=30.0, threads=8)
+    assert np.array_equal(ids, want)
+    s.close()
