@@ -220,10 +220,15 @@ __device__ __forceinline__ int wave_sum_i32(int v)
 __device__ __forceinline__ void wave_kth_largest2(uint32_t v, int k1, int k2, uint32_t& r1,
                                                   uint32_t& r2)
 {
-    uint32_t p1 = 0, p2 = 0;
+    /* both results lie in [min v, max v]: their bits above the highest bit
+     * in which min and max differ are the common prefix */
+    const uint32_t hi = wave_max_u32(v), lo = wave_min_u32(v);
+    const int top = hi == lo ? -1 : 31 - __builtin_clz(hi ^ lo);
+    const uint32_t pre = top < 0 ? hi : (top >= 31 ? 0u : (hi & ~((2u << top) - 1u)));
+    uint32_t p1 = pre, p2 = pre;
     const bool on1 = k1 >= 1 && k1 <= 64, on2 = k2 >= 1 && k2 <= 64;
 #pragma unroll 4
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = top; bit >= 0; --bit) {
         const uint32_t c1 = p1 | (1u << bit), c2 = p2 | (1u << bit);
         const int n1 = __popcll(__ballot(v >= c1));
         const int n2 = __popcll(__ballot(v >= c2));
@@ -234,15 +239,28 @@ __device__ __forceinline__ void wave_kth_largest2(uint32_t v, int k1, int k2, ui
     r2 = on2 ? p2 : 0u;
 }
 
-/* k-th largest key (1 <= k <= 64*NG) over NG keys per lane of one wave,
+/* k-th largest key (1 <= k <= the number of non-zero keys <= 64*NG) over NG
+ * keys per lane of one wave,
  * zero keys ignored (all 64 lanes active), by an MSB-first ballot search;
  * *gt / *eq = how many keys are above / equal to it.  Uniform results. */
 template <int NG>
 __device__ __forceinline__ uint32_t wave_select_kth(const uint32_t (&v)[NG], int k, int* gt,
                                                     int* eq)
 {
-    uint32_t p = 0;
-    for (int bit = 31; bit >= 0; --bit) {
+    /* with k <= the number of non-zero keys the result lies between the
+     * smallest non-zero key and the largest key: search only the bits below
+     * their common prefix */
+    uint32_t vmax = 0u, vmin = 0xFFFFFFFFu;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        vmax = v[q] > vmax ? v[q] : vmax;
+        vmin = (v[q] != 0u && v[q] < vmin) ? v[q] : vmin;
+    }
+    vmax = wave_max_u32(vmax);
+    vmin = wave_min_u32(vmin);
+    const int top = vmax <= vmin ? -1 : 31 - __builtin_clz(vmax ^ vmin);
+    uint32_t p = top < 0 ? vmax : (top >= 31 ? 0u : (vmax & ~((2u << top) - 1u)));
+    for (int bit = top; bit >= 0; --bit) {
         const uint32_t c = p | (1u << bit);
         int n = 0;
 #pragma unroll
@@ -257,6 +275,36 @@ __device__ __forceinline__ uint32_t wave_select_kth(const uint32_t (&v)[NG], int
     }
     *gt = g;
     *eq = e;
+    return p;
+}
+
+/* A lower bound of the k-th largest non-zero key over NG keys per lane of
+ * one wave (1 <= k <= the number of non-zero keys): the MSB-first ballot
+ * search of wave_select_kth stopped after `bits` bits below the keys' common
+ * prefix.  Every prefix of that search keeps #{keys >= p} >= k, so the
+ * result is a valid bound, within 2^(top-bits) of the exact value. */
+template <int NG>
+__device__ __forceinline__ uint32_t wave_kth_bound(const uint32_t (&v)[NG], int k, int bits)
+{
+    uint32_t vmax = 0u, vmin = 0xFFFFFFFFu;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        vmax = v[q] > vmax ? v[q] : vmax;
+        vmin = (v[q] != 0u && v[q] < vmin) ? v[q] : vmin;
+    }
+    vmax = wave_max_u32(vmax);
+    vmin = wave_min_u32(vmin);
+    if (vmax <= vmin) return vmax;
+    const int top = 31 - __builtin_clz(vmax ^ vmin);
+    uint32_t p = top >= 31 ? 0u : (vmax & ~((2u << top) - 1u));
+    const int stop = top - bits < -1 ? -1 : top - bits;
+    for (int bit = top; bit > stop; --bit) {
+        const uint32_t c = p | (1u << bit);
+        int n = 0;
+#pragma unroll
+        for (int q = 0; q < NG; ++q) n += __popcll(__ballot(v[q] >= c));
+        if (n >= k) p = c;
+    }
     return p;
 }
 

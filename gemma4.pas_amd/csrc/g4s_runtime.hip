@@ -40,6 +40,7 @@ struct g4s_sampler {
     uint64_t* cand = nullptr;
     uint64_t* merge = nullptr;
     g4s::ChunkRec* recs = nullptr;
+    uint32_t* wbounds = nullptr;
     uint32_t* tickets = nullptr;
     /* full path workspace */
     g4s::FullWorkspace full{};
@@ -86,6 +87,7 @@ void release(g4s_sampler* s)
     f(s->cand);
     f(s->merge);
     f(s->recs);
+    f(s->wbounds);
     f(s->tickets);
     g4s::full_free(s->full);
     f(s->d_params);
@@ -150,6 +152,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         a.cand = s->cand;
         a.merge = s->merge;
         a.recs = s->recs;
+        a.wbounds = s->wbounds;
         a.tickets = s->tickets;
         a.ids = d_ids;
         a.done = done;
@@ -252,6 +255,7 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
     dm((void**)&s->cand, mb * g4s::kCandRow * sizeof(uint64_t));
     dm((void**)&s->merge, mb * g4s::kCandRow * sizeof(uint64_t));
     dm((void**)&s->recs, mb * g4s::kMaxSplits * sizeof(g4s::ChunkRec));
+    dm((void**)&s->wbounds, mb * g4s::kWaveBounds * sizeof(uint32_t));
     dm((void**)&s->tickets, mb * sizeof(uint32_t));
     dm((void**)&s->d_params, mb * sizeof(g4s_params));
     dm((void**)&s->d_u, mb * sizeof(double));

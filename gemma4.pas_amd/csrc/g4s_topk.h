@@ -8,11 +8,13 @@
 
 namespace g4s {
 
+constexpr int kWaveBounds = 256; /* per-wave bounds kept per row (splits * waves) */
+
 /* Per-chunk record written by phase 1 (16 bytes). */
 struct ChunkRec {
     uint32_t count;  /* candidates emitted */
     uint32_t bound;  /* lower bound of the chunk's K-th largest key (exact when mode bit set) */
-    uint32_t rc;     /* ceil(K/splits)-th largest key of the chunk, 0 if fewer keys */
+    uint32_t rsv;    /* reserved (0) */
     uint32_t mode_e; /* bit 31: exact select; bits 0-30: copies of the K-th key in the chunk */
 };
 
@@ -41,6 +43,7 @@ struct TopkArgs {
     uint64_t* cand;   /* [batch][kCandRow] chunk candidates */
     uint64_t* merge;  /* [batch][kCandRow] merge candidates beyond what LDS holds */
     ChunkRec* recs;   /* [batch][kMaxSplits] */
+    uint32_t* wbounds; /* [batch][kWaveBounds]: per wave, the r-th largest thread maximum */
     uint32_t* tickets; /* [batch], zero between launches */
     int32_t* ids;      /* [batch] (device or host-pinned) */
     uint32_t* done;    /* [batch] host-pinned completion words, or NULL */

@@ -16,15 +16,16 @@
  *      if more than the chunk's slot count qualify (heavy ties), an exact
  *      per-chunk radix select emits the keys above the chunk's K-th value
  *      plus its first K copies in index order;
- *    - rc, a value the chunk holds at least ceil(K/splits) keys >= (the
- *      largest over waves of that order statistic of the thread maxima):
- *      min over chunks of rc is a second lower bound of the row's K-th
- *      largest;
+ *    - per wave, the r-th largest of its 64 thread maxima, r =
+ *      ceil(2K / waves in the row): the wave holds at least r distinct keys
+ *      >= it, so the ceil(K/r)-th largest of these over the row's waves is a
+ *      second lower bound of the row's K-th largest (a tight one: the top
+ *      keys of a row rarely share a thread);
  *    - an atomic ticket elects the last workgroup of the row.
  *  merge + tail (last workgroup of each row)
  *    - loads every chunk record and candidate slot of the row with
  *      independent loads (one memory round trip), keeps candidates
- *      >= max(max bound, min rc), selects the exact K-th value tau,
+ *      >= the larger bound, selects the exact K-th value tau,
  *      resolves ties at tau like the reference's min-heap (lowest index when
  *      the heap layout cannot matter, a full heap replay otherwise), and
  *      sorts the survivors by vocab index;
@@ -51,6 +52,7 @@ struct TopkShared {
     int flag_last;
     uint32_t hist[256];
     ChunkRec rec[kMaxSplits];
+    uint32_t wb[kWaveBounds];
     uint64_t mc[kMergeLds];     /* phase-1 emission, then merge candidates, then replay tiles */
     uint64_t surv[kMaxTopK];    /* survivors (unsorted); min-heap storage during a replay */
     uint64_t sorted[kMaxTopK];  /* survivors ascending by vocab index */
@@ -114,6 +116,36 @@ __device__ void heap_replay(const char* row, int vocab, int K, TopkShared& sh, f
         }
         __syncthreads();
     }
+}
+
+/* One wave: the K-th largest key tau of the M <= 64*NG candidates (K < M).
+ * When exactly K candidates are >= tau they are the survivors: written to
+ * surv (any order) and true is returned; otherwise false (copies of tau must
+ * be split by the tie rules). */
+template <int NG>
+__device__ __forceinline__ bool wave_fast_select(const uint64_t* mc, int M, int K, uint64_t* surv)
+{
+    const int lane = threadIdx.x & 63;
+    uint32_t kk[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        const int i = lane + 64 * q;
+        kk[q] = i < M ? cand_key_of(mc[i]) : 0u;
+    }
+    int G, E;
+    const uint32_t tau = wave_select_kth<NG>(kk, K, &G, &E);
+    const bool fast = E == K - G;
+    if (fast) {
+        int off = 0;
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            const bool t = kk[q] >= tau; /* tau >= 1: padding keys are 0 */
+            const uint64_t mask = __ballot(t);
+            if (t) surv[off + __popcll(mask & ((1ull << lane) - 1ull))] = mc[lane + 64 * q];
+            off += __popcll(mask);
+        }
+    }
+    return fast;
 }
 
 /* Rank-by-count k-th largest of key(i), i in [0, n) (n <= kRankMax).  The
@@ -237,22 +269,21 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
      * 64 thread maxima (distinct elements, so the wave holds at least that
      * many keys >= each value) */
     const int kw = (K + NW - 1) / NW;
-    const int m = (K + S - 1) / S;
-    uint32_t wth, wrc;
-    wave_kth_largest2(tmax, kw, m, wth, wrc);
+    const int nwave = S * NW;
+    int r1 = (2 * K + nwave - 1) / nwave;
+    r1 = r1 < 1 ? 1 : (r1 > 64 ? 64 : r1);
+    uint32_t wth, wr1;
+    wave_kth_largest2(tmax, kw, r1, wth, wr1);
     if (lane == 0) {
         sh.wtheta[wid] = wth;
-        sh.red[wid] = wrc;
+        if (nwave <= kWaveBounds)
+            st_dev(&a.wbounds[(int64_t)row * kWaveBounds + chunk * NW + wid], wr1);
     }
     __syncthreads();
-    /* theta: every wave has >= kw keys >= theta, so the chunk has >= K;
-     * rc: some wave has >= m keys >= rc */
-    uint32_t theta = 0xFFFFFFFFu, rc = 0u;
+    /* theta: every wave has >= kw keys >= theta, so the chunk has >= K */
+    uint32_t theta = 0xFFFFFFFFu;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        theta = sh.wtheta[w] < theta ? sh.wtheta[w] : theta;
-        rc = sh.red[w] > rc ? sh.red[w] : rc;
-    }
+    for (int w = 0; w < NW; ++w) theta = sh.wtheta[w] < theta ? sh.wtheta[w] : theta;
     theta = theta < 1u ? 1u : theta;
 
     /* emit every key >= theta straight to the chunk's HBM slots: wave-level
@@ -342,7 +373,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     if (tid == 0) {
         uint64_t* rp64 = reinterpret_cast<uint64_t*>(a.recs + (int64_t)row * kMaxSplits + chunk);
         st_dev(rp64, ((uint64_t)rec_bound << 32) | (uint32_t)emitted);
-        st_dev(rp64 + 1, ((uint64_t)rec_mode_e << 32) | rc);
+        st_dev(rp64 + 1, (uint64_t)rec_mode_e << 32);
     }
 
     /* ----------------------------------------------- last workgroup elects */
@@ -354,8 +385,12 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     uint64_t* gmerge = a.merge + (int64_t)row * kCandRow;
     const int span = S << a.cap_log2;
 
-    /* one round trip: the chunk records and the first batch of slots (the
-     * index is clamped instead of branched on, so every load is issued) */
+    /* one round trip: the chunk records, the wave bounds and the first
+     * batch of slots (the index is clamped instead of branched on, so every
+     * load is issued) */
+    const bool use_wb = nwave <= kWaveBounds;
+    uint32_t wbv = 0u;
+    if (use_wb && tid < nwave) wbv = ld_dev(&a.wbounds[(int64_t)row * kWaveBounds + tid]);
     if (tid < S) {
         const uint64_t* rp64 =
             reinterpret_cast<const uint64_t*>(a.recs + (int64_t)row * kMaxSplits + tid);
@@ -363,7 +398,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         ChunkRec r;
         r.count = (uint32_t)w0;
         r.bound = (uint32_t)(w0 >> 32);
-        r.rc = (uint32_t)w1;
+        r.rsv = 0u;
         r.mode_e = (uint32_t)(w1 >> 32);
         sh.rec[tid] = r;
     }
@@ -373,39 +408,62 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         const int f = tid + i * BLOCK;
         v[i] = ld_dev(&rcand[f < span ? f : span - 1]);
     }
+    if (use_wb && tid < nwave) sh.wb[tid] = wbv;
     __syncthreads();
-    uint32_t lb, lr;
+    uint32_t lb, l1 = 0u;
     bool any_exact;
     {
-        uint32_t mb = 1u, mr = 0xFFFFFFFFu, ex = 0u;
+        uint32_t mb = 1u, ex = 0u;
         if (tid < S) {
             const ChunkRec r = sh.rec[tid];
             mb = r.bound > 1u ? r.bound : 1u;
-            mr = r.rc;
             ex = r.mode_e >> 31;
         }
         mb = wave_max_u32(mb);
-        mr = wave_min_u32(mr);
         ex = wave_max_u32(ex);
         if (lane == 0) {
             sh.red[wid] = mb;
-            sh.red[16 + wid] = mr;
             sh.red[32 + wid] = ex;
+        }
+        /* a lower bound of the ceil(K/r1)-th largest wave bound, by every
+         * wave (no barrier); 10 bits below the common prefix are enough to
+         * cut the candidates to about K */
+        if (use_wb) {
+            const int j = (K + r1 - 1) / r1;
+            if (nwave <= 128) {
+                uint32_t kk[2];
+                int nz = 0;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int i = lane + 64 * q;
+                    kk[q] = i < nwave ? sh.wb[i] : 0u;
+                    nz += __popcll(__ballot(kk[q] != 0u));
+                }
+                if (nz >= j) l1 = wave_kth_bound<2>(kk, j, 10);
+            } else {
+                uint32_t kk[kWaveBounds / 64];
+                int nz = 0;
+#pragma unroll
+                for (int q = 0; q < kWaveBounds / 64; ++q) {
+                    const int i = lane + 64 * q;
+                    kk[q] = i < nwave ? sh.wb[i] : 0u;
+                    nz += __popcll(__ballot(kk[q] != 0u));
+                }
+                if (nz >= j) l1 = wave_kth_bound<kWaveBounds / 64>(kk, j, 10);
+            }
         }
         __syncthreads();
         lb = 1u;
-        lr = 0xFFFFFFFFu;
         ex = 0u;
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
             lb = sh.red[w] > lb ? sh.red[w] : lb;
-            lr = sh.red[16 + w] < lr ? sh.red[16 + w] : lr;
             ex |= sh.red[32 + w];
         }
         any_exact = ex != 0u;
     }
     if (any_exact) flags |= G4S_FLAG_CHUNK_EXACT;
-    const uint32_t L = lb > lr ? lb : lr;
+    const uint32_t L = lb > l1 ? lb : l1;
 
     /* keep the candidates >= L (wave-level compaction); LDS holds the first
      * kMergeLds of them, the rest go to the row's HBM merge area */
@@ -460,29 +518,14 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
             nsurv = M;
         } else if (M <= 512) {
             if (wid == 0) {
-                uint32_t kk[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const int i = lane + 64 * q;
-                    kk[q] = i < M ? cand_key_of(sh.mc[i]) : 0u;
-                }
-                int G, E;
-                const uint32_t tau = wave_select_kth<8>(kk, K, &G, &E);
-                if (lane == 0) {
-                    sh.misc[4] = (int)tau;
-                    sh.misc[5] = (E == K - G) ? 0 : 1;
-                }
+                const bool fast = M <= 128   ? wave_fast_select<2>(sh.mc, M, K, sh.surv)
+                                  : M <= 256 ? wave_fast_select<4>(sh.mc, M, K, sh.surv)
+                                             : wave_fast_select<8>(sh.mc, M, K, sh.surv);
+                if (lane == 0) sh.misc[5] = fast ? 0 : 1;
             }
             __syncthreads();
-            const uint32_t tau = (uint32_t)sh.misc[4];
             general = sh.misc[5] != 0;
-            if (!general) {
-                for (int i = tid; i < M; i += BLOCK) {
-                    const uint64_t c = sh.mc[i];
-                    if (cand_key_of(c) >= tau) sh.surv[atomicAdd(&sh.misc[2], 1)] = c;
-                }
-                nsurv = K;
-            }
+            if (!general) nsurv = K;
         } else {
             general = true;
         }
@@ -617,8 +660,8 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     float lsum = 0.0f;
     for (int base = 0; base < nsurv; base += 64) {
         const float x = (base + lane < nsurv) ? sh.val[base + lane] : 0.0f;
-        const int n = nsurv - base < 64 ? nsurv - base : 64;
-        for (int l = 0; l < n; ++l) lsum = lsum + lane_f(x, l);
+#pragma unroll
+        for (int l = 0; l < 64; ++l) lsum = lsum + lane_f(x, l);
     }
     /* greedy choice: first position of the largest p (p >= 0, so its bits
      * order like the values) */
@@ -646,9 +689,9 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         int hit = -1;
         for (int base = 0; base < nsurv; base += 64) {
             const float x = (base + lane < nsurv) ? sh.prob[base + lane] : 0.0f;
-            const int n = nsurv - base < 64 ? nsurv - base : 64;
             float mine_c = 0.0f;
-            for (int l = 0; l < n; ++l) {
+#pragma unroll
+            for (int l = 0; l < 64; ++l) {
                 cum = cum + lane_f(x, l);
                 mine_c = (lane == l) ? cum : mine_c;
             }
