@@ -54,12 +54,12 @@ struct FullChunk {
     float sapx;       /* approximate sum of exp(y - ymax) over the terms taking part */
     ss::PMap lmap;    /* lsum kernel: the chunk's terms in beta_l */
     ss::PMap cmap;    /* draw kernel: the chunk's p in beta_c */
-    double de;        /* lsum kernel: sum of the chunk's e in binary64 */
+    int32_t spare[2];
     int32_t beta_l;   /* predicted binade of LSum entering the chunk */
     int32_t beta_c;   /* predicted binade of the running sum entering the chunk */
     int32_t nsurv;    /* max kernel: terms of the chunk taking part */
     int32_t fsurv;    /* max kernel: first index taking part, INT_MAX: none */
-    int32_t soff;     /* LSum chain: terms taking part before the chunk */
+    int32_t soff;     /* row kernel: terms taking part before the chunk */
     int32_t pad;
 };
 static_assert(sizeof(FullChunk) == 64, "FullChunk layout");

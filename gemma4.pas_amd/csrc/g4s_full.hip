@@ -206,18 +206,12 @@ __device__ __forceinline__ float y_approx(float x, float cap, float inv_cap, int
 {
     float y = x;
     if (cap > 0.0f) {
+        /* cap * tanh(w) = cap - 2 cap / (e^(2w) + 1): branch-free, absolute
+         * error a few cap * 2^-24 (what the predictions need) */
         const float w = x * inv_cap;
-        float t;
-        if (__builtin_fabsf(w) < 0.5f) {
-            const float w2 = w * w; /* odd Taylor series of tanh to w^9 */
-            t = w * (1.0f + w2 * (-0.33333334f + w2 * (0.13333334f + w2 * (-0.053968254f +
-                                                                        w2 * 0.021869488f))));
-        } else {
-            const float wc = w > 12.0f ? 12.0f : (w < -12.0f ? -12.0f : w);
-            const float e2 = __builtin_amdgcn_exp2f(wc * 2.8853900817779268f); /* e^(2w) */
-            t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e2 + 1.0f);
-        }
-        y = t * cap;
+        const float wc = __builtin_fminf(__builtin_fmaxf(w, -12.0f), 12.0f);
+        const float e2 = __builtin_amdgcn_exp2f(wc * 2.8853900817779268f); /* e^(2w) */
+        y = cap - (2.0f * cap) * __builtin_amdgcn_rcpf(e2 + 1.0f);
     }
     if (scale) y = y * inv_t;
     return y;
@@ -270,16 +264,50 @@ __device__ __forceinline__ float e_of(uint32_t raw, const Ctx& c, const float* t
     return e_direct(x_of<DT>(raw), c);
 }
 
-/* The e of one thread's 16 terms (0 for terms that do not take part). */
+/* The e of one thread's 16 terms (0 for terms that do not take part).  For
+ * bf16 logits every term reads the table (a clamped index, no branch); the
+ * rare codes outside its window are evaluated afterwards, behind one
+ * wave-uniform branch. */
+template <int DT, bool GENERAL>
+__device__ __forceinline__ void terms_e_t(const uint32_t (&raw)[kFullPer], int nvalid,
+                                          int64_t e0, const Ctx& c, const Mask& k,
+                                          const float* tab, float (&t)[kFullPer])
+{
+    if (DT == 1 && c.win_lo >= 0) {
+        uint32_t miss = 0u;
+#pragma unroll
+        for (int j = 0; j < kFullPer; ++j) {
+            const bool part =
+                GENERAL ? (j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j)) : true;
+            const int ti = tab_index(raw[j], c.win_lo);
+            const float v = tab[ti < 0 ? 0 : ti];
+            t[j] = part ? v : 0.0f;
+            miss |= (part && ti < 0) ? (1u << j) : 0u;
+        }
+        if (__ballot(miss != 0u)) {
+#pragma unroll
+            for (int j = 0; j < kFullPer; ++j)
+                if (miss & (1u << j)) t[j] = e_direct(x_of<DT>(raw[j]), c);
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < kFullPer; ++j) {
+        const bool part = GENERAL ? (j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j)) : true;
+        t[j] = part ? e_direct(x_of<DT>(raw[j]), c) : 0.0f;
+    }
+}
+
+/* Whole chunks of full rows (the common case) skip the per-term mask. */
 template <int DT>
 __device__ __forceinline__ void terms_e(const uint32_t (&raw)[kFullPer], int nvalid, int64_t e0,
                                         const Ctx& c, const Mask& k, const float* tab,
                                         float (&t)[kFullPer])
 {
-#pragma unroll
-    for (int j = 0; j < kFullPer; ++j)
-        t[j] = (j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j)) ? e_of<DT>(raw[j], c, tab)
-                                                                        : 0.0f;
+    if (k.cls == kRowWide || nvalid < kFullPer)
+        terms_e_t<DT, true>(raw, nvalid, e0, c, k, tab, t);
+    else
+        terms_e_t<DT, false>(raw, nvalid, e0, c, k, tab, t);
 }
 
 /* p of one term from its e: RN32(e * fl32(1/LSum)) on a full row
@@ -314,6 +342,7 @@ struct ChainShared {
     float tab[DT == 1 ? kFullTab : 1];
     PMap cmap[kFullMaxChunks];
     int32_t cbeta[kFullMaxChunks];
+    float cpost[kFullMaxChunks]; /* LSum chain: exact running sum after each chunk */
 };
 
 __device__ __forceinline__ uint32_t block_max_key(uint32_t v, Scratch& sh, int slot)
@@ -437,27 +466,36 @@ __device__ __forceinline__ PMap wave_shift_map(PMap f)
     return o;
 }
 
-/* The map of one thread's terms in binade e. */
+/* The map of one thread's terms in binade e (terms beyond the row are 0,
+ * and a 0 term is the identity). */
 __device__ __forceinline__ PMap thread_map(const float (&t)[kFullPer], int nvalid, int32_t e)
 {
-    int32_t csum = 0, ties = 0;
-    int32_t ct[kFullPer];
+    (void)nvalid;
+    /* Without a half-unit tie every term adds c = rint(q) units, q = a/u =
+     * ldexp(a, 150-E) exact, whatever the parity: the map is (C, C) with C
+     * the sum of the c (summed in binary32: exact below 2^24, and a sum
+     * that reaches 2^24 means the thread leaves the binade either way).  A
+     * tie (fract(q) == 1/2) anywhere in the wave takes the exact per-term
+     * maps (wave-uniform branch; ties are rare). */
+    float cs = 0.0f;
+    bool tie = false;
+    const int sh = 150 - e;
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j) {
-        ct[j] = (j < nvalid) ? ss::term_ct(t[j], e) : 0;
-        csum += ct[j] >> 1;
-        ties |= ct[j];
+        const float q = __builtin_ldexpf(t[j], sh);
+        cs += __builtin_rintf(q);
+        tie = tie || __builtin_amdgcn_fractf(q) == 0.5f;
     }
     PMap f;
-    if ((ties & 1) == 0) {
-        /* no half-ulp tie: the map does not depend on the parity */
-        f.d0 = csum > (1 << 26) ? (1 << 26) : csum;
+    if (__ballot(tie) == 0) {
+        f.d0 = (int32_t)__builtin_fminf(cs, 67108864.0f); /* 2^26, as map_sat caps */
         f.d1 = f.d0;
         return f;
     }
     f = ss::map_identity();
 #pragma unroll
-    for (int j = 0; j < kFullPer; ++j) f = ss::map_sat(ss::map_then(f, ss::map_of_ct(ct[j])));
+    for (int j = 0; j < kFullPer; ++j)
+        f = ss::map_sat(ss::map_then(f, ss::map_of_ct(ss::term_ct_f(t[j], e))));
     return f;
 }
 
@@ -564,7 +602,7 @@ __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st,
  * after the last accepted chunk goes to sh.misc[9..10] and the first chunk
  * that does not apply (nch: none) to sh.misc[14].  Ends with a barrier. */
 __device__ void chain_maps(const PMap* cmap, const int32_t* cbeta, int cb, int nch, State st,
-                           float thr, Scratch& sh)
+                           float thr, Scratch& sh, float* cpost)
 {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
@@ -574,7 +612,9 @@ __device__ void chain_maps(const PMap* cmap, const int32_t* cbeta, int cb, int n
             const PMap f = c < nch ? cmap[c] : ss::map_identity();
             const int32_t be = c < nch ? cbeta[c] : -1;
             const int n = nch - g < 64 ? nch - g : 64;
-            for (int l = 0; l < n; ++l) {
+            float post = 0.0f;
+            int l = 0;
+            for (; l < n; ++l) {
                 const int32_t bl = __builtin_amdgcn_readlane(be, l);
                 const int32_t d0 = __builtin_amdgcn_readlane(f.d0, l);
                 const int32_t d1 = __builtin_amdgcn_readlane(f.d1, l);
@@ -584,7 +624,9 @@ __device__ void chain_maps(const PMap* cmap, const int32_t* cbeta, int cb, int n
                     break;
                 }
                 st.m = m2;
+                post = lane == l ? ss::value_of(st) : post;
             }
+            if (cpost && lane < l) cpost[c] = post; /* exact running sum after chunk c */
         }
         if (lane == 0) {
             sh.misc[9] = st.e;
@@ -1047,23 +1089,47 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
     uint32_t raw[kFullPer];
     const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
     const int nvalid = load16<DT>(row_ptr<DT>(a, row), e0, V, raw);
-    uint32_t kmax = 0u, amax = 0u, ymk = 0u, fs = 0xFFFFFFFFu;
+    /* maxima as floats (the key of a float maximum is the maximum key: the
+     * order-preserving map identifies -0 and +0, as the comparisons do) */
+    float xm = -__builtin_inff(), am = 0.0f, ym = -__builtin_inff();
+    uint32_t fs = 0xFFFFFFFFu;
     int ns = 0;
     float ya[kFullPer];
     bool part[kFullPer];
+    if (k.cls == kRowWide || nvalid < kFullPer) {
 #pragma unroll
-    for (int j = 0; j < kFullPer; ++j) {
-        const float xj = x_of<DT>(raw[j]);
-        part[j] = j < nvalid && takes_part(k, xj, e0 + j);
-        ya[j] = y_approx(xj, cap, inv_cap, scale, inv_t);
-        if (j < nvalid) kmax = g4s_max_u(kmax, f2key(xj));
-        if (part[j]) {
-            amax = g4s_max_u(amax, __float_as_uint(xj) & 0x7FFFFFFFu);
-            ymk = g4s_max_u(ymk, f2key(ya[j]));
-            ns += 1;
-            fs = g4s_min_u(fs, (uint32_t)(e0 + j));
+        for (int j = 0; j < kFullPer; ++j) {
+            const float xj = x_of<DT>(raw[j]);
+            part[j] = j < nvalid && takes_part(k, xj, e0 + j);
+            ya[j] = y_approx(xj, cap, inv_cap, scale, inv_t);
+            if (j < nvalid) xm = __builtin_fmaxf(xm, xj);
+            am = part[j] ? __builtin_fmaxf(am, __builtin_fabsf(xj)) : am;
+            ym = part[j] ? __builtin_fmaxf(ym, ya[j]) : ym;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kFullPer; ++j) {
+            const float xj = x_of<DT>(raw[j]);
+            part[j] = true;
+            ya[j] = y_approx(xj, cap, inv_cap, scale, inv_t);
+            xm = __builtin_fmaxf(xm, xj);
+            am = __builtin_fmaxf(am, __builtin_fabsf(xj));
+            ym = __builtin_fmaxf(ym, ya[j]);
         }
     }
+    if (k.cls == kRowWide) {
+#pragma unroll
+        for (int j = 0; j < kFullPer; ++j) {
+            ns += part[j] ? 1 : 0;
+            fs = part[j] ? g4s_min_u(fs, (uint32_t)(e0 + j)) : fs;
+        }
+    } else {
+        ns = nvalid;
+        fs = nvalid > 0 ? (uint32_t)e0 : fs;
+    }
+    uint32_t kmax = nvalid > 0 ? f2key(xm) : 0u;
+    uint32_t amax = __float_as_uint(am);
+    uint32_t ymk = f2key(ym);
     /* the maxima in one LDS exchange */
     {
         const int lane = tid & 63, wid = tid >> 6;
@@ -1242,26 +1308,30 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
         const int nvalid = load16<DT>(rowp, e0, V, raw);
         float t[kFullPer];
         terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t);                  /* Tensors.pas:660 */
-        double dsum = 0.0;
-        uint32_t first1 = 0xFFFFFFFFu;
+        /* the terms with e = 1 - jj*2^-24, jj < kNear (the row maximum and
+         * its near ties): looked at only in waves that hold one */
+        constexpr float kNearLo = 1.0f - (float)(kNear - 1) * 0x1p-24f;
+        float tmx = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kFullPer; ++j) {
-            dsum += (double)t[j];
-            if (t[j] >= 1.0f - (float)(kNear - 1) * 0x1p-24f && t[j] <= 1.0f) {
-                /* e = 1 - jj*2^-24 exactly, jj < kNear */
-                const int jj = (int)((1.0f - t[j]) * 0x1p24f);
-                if (jj == 0)
-                    first1 = g4s_min_u(first1, (uint32_t)(e0 + j));
-                else if (k.cls == kRowWide)
-                    atomicMin(&rr->near[jj], (int32_t)(e0 + j));
+        for (int j = 0; j < kFullPer; ++j) tmx = __builtin_fmaxf(tmx, t[j]);
+        uint32_t first1 = 0xFFFFFFFFu;
+        if (__ballot(tmx >= kNearLo)) {
+            uint32_t nearm = 0u;
+#pragma unroll
+            for (int j = 0; j < kFullPer; ++j) {
+                first1 = t[j] == 1.0f ? g4s_min_u(first1, (uint32_t)(e0 + j)) : first1;
+                nearm |= (t[j] >= kNearLo && t[j] < 1.0f) ? (1u << j) : 0u;
+            }
+            if (k.cls == kRowWide && nearm != 0u) {
+                for (int j = 0; j < kFullPer; ++j)
+                    if (nearm & (1u << j))
+                        atomicMin(&rr->near[(int)((1.0f - t[j]) * 0x1p24f)], (int32_t)(e0 + j));
             }
         }
         const PMap cm = block_chunk_map(thread_map(t, nvalid, rc[b].beta_l), sh.s);
-        dsum = block_sum_d(dsum, sh.s);
         first1 = block_min_u(first1, sh.s);
         if (tid == 0) {
             rc[b].lmap = cm;
-            rc[b].de = dsum;
             if (first1 != 0xFFFFFFFFu) atomicMin(&rr->near[0], (int32_t)first1);
         }
     }
@@ -1300,7 +1370,7 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
     int reev = 0;
     for (int cb = 0; cb < nch;) {
         if (cb > 0) {
-            chain_maps(sh.cmap, sh.cbeta, cb, nch, st, __builtin_inff(), sh.s);
+            chain_maps(sh.cmap, sh.cbeta, cb, nch, st, __builtin_inff(), sh.s, sh.cpost);
             st.e = sh.s.misc[9];
             st.m = sh.s.misc[10];
             cb = sh.s.misc[14];
@@ -1322,6 +1392,7 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
         }
         int h;
         st = resolve_chunk(t, nv, st, __builtin_inff(), pos, &h, sh.s);
+        if (tid == 0) sh.cpost[cb] = ss::value_of(st);
         ++cb;
     }
     const float lsum = ss::value_of(st);
@@ -1351,25 +1422,16 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
         }
         return;
     }
-    /* predicted binade of the running sum entering each chunk, and the
-     * chunk where it is predicted to reach thr (with margin) */
-    double d[CPT];
-    double tsum = 0.0;
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-        const int cb = tid * CPT + q;
-        d[q] = cb < nch ? rc[cb].de : 0.0;
-        tsum += d[q];
-    }
-    double pre = block_excl_scan_d(tsum, sh.s);
+    /* predicted binade of the draw's running sum entering each chunk (the
+     * exact LSum prefix before the chunk times 1/LSum), and the chunk where
+     * it is predicted to reach thr (with margin) */
+    __syncthreads(); /* cpost complete */
     uint32_t last = (uint32_t)(nch - 1);
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-        const int cb = tid * CPT + q;
-        if (cb < nch) rc[cb].beta_c = ss::state_of((float)(pre * (double)inv)).e;
-        pre += d[q];
-        if (cb < nch && pre * (double)inv >= (double)thr * (1.0 + 0x1p-10))
-            last = g4s_min_u(last, (uint32_t)cb);
+    for (int cb = tid; cb < nch; cb += kFullBlock) {
+        const double pre = cb > 0 ? (double)sh.cpost[cb - 1] : 0.0;
+        const double post = (double)sh.cpost[cb];
+        rc[cb].beta_c = ss::state_of((float)(pre * (double)inv)).e;
+        if (post * (double)inv >= (double)thr * (1.0 + 0x1p-10)) last = g4s_min_u(last, (uint32_t)cb);
     }
     last = block_min_u(last, sh.s);
     if (tid == 0) {
@@ -1503,7 +1565,7 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
     int reev = 0;
     for (int cb = 0; cb < nch; ++cb) {
         if (cb > 0) {
-            chain_maps(sh.cmap, sh.cbeta, cb, nch, st, thr, sh.s);
+            chain_maps(sh.cmap, sh.cbeta, cb, nch, st, thr, sh.s, nullptr);
             st.e = sh.s.misc[9];
             st.m = sh.s.misc[10];
             cb = sh.s.misc[14];

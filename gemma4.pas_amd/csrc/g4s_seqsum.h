@@ -87,18 +87,34 @@ G4S_SS_HD float value_of(State st)
  * binade (a >= 2^(E-126)).  Packed as c*2 + t. */
 G4S_SS_HD int32_t term_ct(float a, int32_t e)
 {
+    /* branch-free: s = e - E(a) units of shift; s < 0: a alone leaves the
+     * binade; s = 0: a is an integer number of units; s >= 25: a < u/2
+     * rounds away (k = 0, rem < half); +0 gives k = rem = 0 */
     const uint32_t b = fbits(a);
     const int32_t ea = (int32_t)(b >> 23);
-    if (ea == 0 && (b & 0x7FFFFFu) == 0u) return 0; /* +0 */
-    const int32_t ma = (int32_t)(b & 0x7FFFFFu) | (ea ? 0x800000 : 0);
+    const uint32_t ma = (b & 0x7FFFFFu) | (ea ? 0x800000u : 0u);
     const int32_t s = e - (ea ? ea : 1);
-    if (s < 0) return kTop * 2;
-    if (s == 0) return ma * 2;
-    if (s > 25) return 0; /* a < u/4 */
-    const int32_t k = ma >> s;
-    const int32_t rem = ma & ((1 << s) - 1);
-    const int32_t half = 1 << (s - 1);
-    return (k + (rem > half)) * 2 + (rem == half);
+    const int32_t sc = s < 0 ? 0 : (s > 31 ? 31 : s);
+    const uint32_t k = ma >> sc;
+    const uint32_t rem = ma & ((1u << sc) - 1u);
+    const uint32_t half = sc ? (1u << (sc - 1)) : 1u; /* s = 0: rem = 0 is no tie */
+    const int32_t ct = (int32_t)((k + (rem > half ? 1u : 0u)) * 2u + (rem == half ? 1u : 0u));
+    return s < 0 ? kTop * 2 : ct;
+}
+
+/* term_ct in binary32 arithmetic (fewer instructions on the GPU): with
+ * u = 2^(E-150), q = a/u = ldexp(a, 150-E) is exact (or >= 2^24, or far
+ * below 1/2 when it underflows), k = floor(q) and f = q - k are exact, and
+ * c, t follow from f.  Equal to term_ct for every a >= 0 and binade E. */
+G4S_SS_HD int32_t term_ct_f(float a, int32_t e)
+{
+    const float q = __builtin_ldexpf(a, 150 - e);
+    const bool left = q >= 16777216.0f;
+    const float qc = left ? 0.0f : q; /* keeps the conversion in range */
+    const float k = __builtin_floorf(qc);
+    const float f = qc - k;
+    const int32_t ct = ((int32_t)k + (f > 0.5f ? 1 : 0)) * 2 + (f == 0.5f ? 1 : 0);
+    return left ? kTop * 2 : ct;
 }
 
 G4S_SS_HD PMap map_of_ct(int32_t ct)

@@ -143,6 +143,32 @@ int64_t ss_check_steps(uint64_t seed, int64_t n)
     return bad;
 }
 
+/* term_ct_f == term_ct over random terms (all classes, subnormals
+ * included) and binades 1..254. */
+int64_t ss_check_term_ct_f(uint64_t seed, int64_t n)
+{
+    Rng r{seed};
+    int64_t bad = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        float a;
+        if ((r.next() & 3) == 0) {
+            const uint32_t b = (uint32_t)(r.next() & 0x7F7FFFFFu); /* any finite a >= 0 */
+            std::memcpy(&a, &b, 4);
+        } else {
+            a = gen_term(r, (int)(r.next() % 7));
+        }
+        const int32_t e = 1 + (int32_t)(r.next() % 254);
+        if (term_ct_f(a, e) != term_ct(a, e)) ++bad;
+        /* and the binades around a's own */
+        const int32_t ea = (int32_t)(fbits(a) >> 23);
+        for (int32_t d = -2; d <= 26; ++d) {
+            const int32_t e2 = ea + d;
+            if (e2 >= 1 && e2 <= 254 && term_ct_f(a, e2) != term_ct(a, e2)) ++bad;
+        }
+    }
+    return bad;
+}
+
 /* Associativity of map composition over random term maps. */
 int64_t ss_check_assoc(uint64_t seed, int64_t n)
 {

@@ -20,6 +20,8 @@ def ss():
     L = ctypes.CDLL(LIB)
     L.ss_check_steps.restype = ctypes.c_int64
     L.ss_check_steps.argtypes = [ctypes.c_uint64, ctypes.c_int64]
+    L.ss_check_term_ct_f.restype = ctypes.c_int64
+    L.ss_check_term_ct_f.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     L.ss_check_assoc.restype = ctypes.c_int64
     L.ss_check_assoc.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     L.ss_check_sequence.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
@@ -30,6 +32,13 @@ def ss():
 def test_single_steps(ss):
     """RN32(S + a) from the term map, for S and a across every binade."""
     assert ss.ss_check_steps(1, 2_000_000) == 0
+
+
+def test_float_term_classification_matches_integer(ss):
+    """The binary32 form of a term's (c, t) used by the GPU kernels equals
+    the integer form, for random terms including subnormals, in every
+    binade near the term's own and in random binades."""
+    assert ss.ss_check_term_ct_f(7, 300_000) == 0
 
 
 def test_composition_associative(ss):
