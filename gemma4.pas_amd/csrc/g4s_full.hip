@@ -534,8 +534,17 @@ __device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st,
     while (pos < kFullBlock) {
         const int32_t e = st.e;
         const PMap f = (tid >= pos) ? thread_map(t, nvalid, e) : ss::map_identity();
-        const PMap incl = wave_scan_maps(f);
-        const PMap excl = wave_shift_map(incl);
+        PMap incl, excl;
+        if (__ballot(f.d0 != f.d1) == 0) {
+            /* constant maps (no half-unit tie in the wave): a prefix sum */
+            const int32_t x = wave_inclusive_scan(f.d0 > (1 << 26) ? (1 << 26) : f.d0);
+            incl.d0 = incl.d1 = x > (1 << 26) ? (1 << 26) : x;
+            const int32_t y = __builtin_amdgcn_update_dpp(0, incl.d0, 0x138, 0xf, 0xf, false);
+            excl.d0 = excl.d1 = y;
+        } else {
+            incl = wave_scan_maps(f);
+            excl = wave_shift_map(incl);
+        }
         if (lane == 63) sh.wmap[wid] = incl;
         __syncthreads();
         if (tid == 0) {
@@ -1111,10 +1120,27 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
         for (int j = 0; j < kFullPer; ++j) {
             const float xj = x_of<DT>(raw[j]);
             part[j] = true;
-            ya[j] = y_approx(xj, cap, inv_cap, scale, inv_t);
             xm = __builtin_fmaxf(xm, xj);
             am = __builtin_fmaxf(am, __builtin_fabsf(xj));
-            ym = __builtin_fmaxf(ym, ya[j]);
+        }
+        if (cap > 0.0f && __ballot(am * inv_cap >= 0.1f) == 0) {
+            /* every |x/cap| < 0.1 in the wave: cap tanh(x/cap) = x - x^3/(3 cap^2)
+             * + O(x^5/cap^4), relative error < 1e-5 -- enough for predictions */
+            const float c3 = -(inv_cap * inv_cap) * (1.0f / 3.0f);
+#pragma unroll
+            for (int j = 0; j < kFullPer; ++j) {
+                const float xj = x_of<DT>(raw[j]);
+                float y = xj + xj * (xj * xj) * c3;
+                if (scale) y = y * inv_t;
+                ya[j] = y;
+                ym = __builtin_fmaxf(ym, y);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kFullPer; ++j) {
+                ya[j] = y_approx(x_of<DT>(raw[j]), cap, inv_cap, scale, inv_t);
+                ym = __builtin_fmaxf(ym, ya[j]);
+            }
         }
     }
     if (k.cls == kRowWide) {
