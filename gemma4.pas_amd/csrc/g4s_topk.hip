@@ -42,9 +42,20 @@ using namespace g4s::cr;
 
 namespace {
 
-constexpr int kBatchLoads = 16; /* candidate slots one merge thread loads per round */
+/* candidate slots one merge thread loads per round */
+template <int BLOCK, int KCAP>
+constexpr int batch_loads()
+{
+    return (BLOCK == 1024 && KCAP <= 256) ? 8 : 16;
+}
 
+/* LDS of the kernel, sized by the launch's K bound (KCAP >= every K of the
+ * launch) so that the many phase-1 workgroups of a batch stay resident
+ * together: MCAP merge candidates are kept on chip. */
+template <int KCAP, int MCAP>
 struct TopkShared {
+    static constexpr int kKcap = KCAP;
+    static constexpr int kMcap = MCAP;
     uint32_t wtheta[16];
     int scan[16];
     uint32_t red[48];
@@ -53,11 +64,11 @@ struct TopkShared {
     uint32_t hist[256];
     ChunkRec rec[kMaxSplits];
     uint32_t wb[kWaveBounds];
-    uint64_t mc[kMergeLds];     /* phase-1 emission, then merge candidates, then replay tiles */
-    uint64_t surv[kMaxTopK];    /* survivors (unsorted); min-heap storage during a replay */
-    uint64_t sorted[kMaxTopK];  /* survivors ascending by vocab index */
-    float val[kMaxTopK];        /* tail: v, then e */
-    float prob[kMaxTopK];
+    uint64_t mc[MCAP];     /* merge candidates, then replay tiles */
+    uint64_t surv[KCAP];   /* survivors (unsorted); min-heap storage during a replay */
+    uint64_t sorted[KCAP]; /* survivors ascending by vocab index */
+    float val[KCAP];       /* tail: v, then e */
+    float prob[KCAP];
 };
 
 __device__ __forceinline__ float lane_f(float x, int l)
@@ -72,12 +83,12 @@ __device__ __forceinline__ float lane_f(float x, int l)
  * decides.  Elements are screened in tiles against the current root; the
  * screened ones (in index order) are inserted by one lane.  On return
  * hv[0..K) / hi[0..K) hold the heap. */
-template <int BLOCK, int DT>
-__device__ void heap_replay(const char* row, int vocab, int K, TopkShared& sh, float* hv,
-                            int32_t* hi)
+template <int BLOCK, int DT, typename SH>
+__device__ void heap_replay(const char* row, int vocab, int K, SH& sh, float* hv, int32_t* hi)
 {
+    static_assert(SH::kMcap >= BLOCK, "replay tiles fit the merge area");
     float* qv = reinterpret_cast<float*>(sh.mc);
-    int32_t* qi = reinterpret_cast<int32_t*>(sh.mc) + kMergeLds;
+    int32_t* qi = reinterpret_cast<int32_t*>(sh.mc) + SH::kMcap;
     const int tid = threadIdx.x;
     for (int i = tid; i < K; i += BLOCK) {
         hv[i] = -1e30f; /* :2634-2638 */
@@ -187,8 +198,8 @@ __device__ uint32_t rank_kth(int n, int k, KeyF key, int* s_misc, int* gt, int* 
     return r;
 }
 
-template <int BLOCK, typename KeyF>
-__device__ uint32_t select_kth(int n, int k, KeyF key, TopkShared& sh, int* gt, int* eq)
+template <int BLOCK, typename KeyF, typename SH>
+__device__ uint32_t select_kth(int n, int k, KeyF key, SH& sh, int* gt, int* eq)
 {
     if (n <= kRankMax) return rank_kth<BLOCK>(n, k, key, sh.misc, gt, eq);
     return block_radix_kth<BLOCK>(n, k, key, [](int) { return true; }, sh.hist, sh.misc + 4, gt,
@@ -197,15 +208,18 @@ __device__ uint32_t select_kth(int n, int k, KeyF key, TopkShared& sh, int* gt, 
 
 }  // namespace
 
-template <int BLOCK, int ITEMS, int DT>
+template <int BLOCK, int ITEMS, int DT, int KCAP>
 __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 {
     constexpr int VW = Elem<DT>::VW;
     constexpr int NV = ITEMS / VW;
     constexpr int NW = BLOCK / 64;
     constexpr int CHUNK = BLOCK * ITEMS;
+    constexpr int MCAP = KCAP <= 64 ? 512 : kMergeLds;
+    constexpr int kBatchLoads = batch_loads<BLOCK, KCAP>();
     static_assert(BLOCK >= kMaxSplits, "one merge thread per chunk record");
-    __shared__ TopkShared sh;
+    static_assert(KCAP <= BLOCK, "one survivor per thread");
+    __shared__ TopkShared<KCAP, MCAP> sh;
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int row = blockIdx.y;
@@ -466,7 +480,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     const uint32_t L = lb > l1 ? lb : l1;
 
     /* keep the candidates >= L (wave-level compaction); LDS holds the first
-     * kMergeLds of them, the rest go to the row's HBM merge area */
+     * MCAP of them, the rest go to the row's HBM merge area */
     auto keep = [&](int f, uint64_t c) {
         return f < span && (f & (cap - 1)) < (int)sh.rec[f >> a.cap_log2].count &&
                cand_key_of(c) >= L;
@@ -490,7 +504,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 #pragma unroll
         for (int i = 0; i < kBatchLoads; ++i) {
             if (keep(b0 + tid + i * BLOCK, v[i])) {
-                if (pos < kMergeLds)
+                if (pos < MCAP)
                     sh.mc[pos] = v[i];
                 else
                     gmerge[pos] = v[i];
@@ -500,14 +514,14 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     }
     __syncthreads();
     const int M = sh.misc[1];
-    if (M > kMergeLds) flags |= G4S_FLAG_WIDE_MERGE;
-    auto ent = [&](int i) -> uint64_t { return i < kMergeLds ? sh.mc[i] : gmerge[i]; };
+    if (M > MCAP) flags |= G4S_FLAG_WIDE_MERGE;
+    auto ent = [&](int i) -> uint64_t { return i < MCAP ? sh.mc[i] : gmerge[i]; };
     auto ekey = [&](int i) { return cand_key_of(ent(i)); };
     auto eidx = [&](int i) { return cand_idx_of(ent(i)); };
 
     /* exact top K of the M candidates */
     int nsurv = 0;
-    bool general = any_exact || M > kMergeLds;
+    bool general = any_exact || M > MCAP;
     if (!general) {
         /* one wave finds the K-th largest key tau of the M candidates (ballot
          * search over registers); when the candidates hold exactly K keys
@@ -516,7 +530,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         if (M <= K) {
             for (int i = tid; i < M; i += BLOCK) sh.surv[i] = sh.mc[i];
             nsurv = M;
-        } else if (M <= 512) {
+        } else if (M <= 512 && M <= MCAP) {
             if (wid == 0) {
                 const bool fast = M <= 128   ? wave_fast_select<2>(sh.mc, M, K, sh.surv)
                                   : M <= 256 ? wave_fast_select<4>(sh.mc, M, K, sh.surv)
@@ -589,7 +603,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
                 nsurv = sv;
             } else {
                 float* hv = reinterpret_cast<float*>(sh.surv);
-                int32_t* hi = reinterpret_cast<int32_t*>(sh.surv) + kMaxTopK;
+                int32_t* hi = reinterpret_cast<int32_t*>(sh.surv) + KCAP;
                 heap_replay<BLOCK, DT>(rowp, V, K, sh, hv, hi);
                 /* the heap holds K entries, all with index >= 0 here (M > K);
                  * K <= kbound <= BLOCK, so one entry per thread */
@@ -727,10 +741,18 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 /* ---------------------------------------------------------------- launch */
 
 template <int BLOCK, int ITEMS, int DT>
-static hipError_t launch_cfg(const TopkArgs& a, hipStream_t s)
+static hipError_t launch_cfg(const TopkArgs& a, int kcap, hipStream_t s)
 {
     dim3 grid((unsigned)a.splits, (unsigned)a.batch);
-    hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT>), grid, dim3(BLOCK), 0, s, a);
+    if constexpr (BLOCK == 256) {
+        (void)kcap;
+        hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 64>), grid, dim3(BLOCK), 0, s, a);
+    } else {
+        if (kcap <= 256)
+            hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 256>), grid, dim3(BLOCK), 0, s, a);
+        else
+            hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 1024>), grid, dim3(BLOCK), 0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -740,13 +762,13 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound)
     c.block = kbound <= 64 ? 256 : 1024;
     c.cap_log2 = 1;
     while ((1 << c.cap_log2) < 2 * kbound) ++c.cap_log2;
-    c.items = 32;
-    c.chunk = c.block * c.items;
-    c.splits = (vocab + c.chunk - 1) / c.chunk;
-    if ((c.splits << c.cap_log2) > kCandRow || c.splits > kMaxSplits) {
-        c.items = 64;
+    /* 32 items per thread unless the candidate slots do not fit the workspace */
+    const int items_try[2] = {32, 64};
+    for (int i = 0; i < 2; ++i) {
+        c.items = items_try[i];
         c.chunk = c.block * c.items;
         c.splits = (vocab + c.chunk - 1) / c.chunk;
+        if ((c.splits << c.cap_log2) <= kCandRow && c.splits <= kMaxSplits) break;
     }
     c.ok = ((c.splits << c.cap_log2) <= kCandRow) && (c.splits <= kMaxSplits) &&
            (1 << c.cap_log2) <= kMergeLds;
@@ -755,16 +777,17 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound)
 
 hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStream_t s)
 {
+    const int kc = a.kbound;
     if (dtype == G4S_DTYPE_F32) {
-        if (c.block == 256 && c.items == 32) return launch_cfg<256, 32, 0>(a, s);
-        if (c.block == 256 && c.items == 64) return launch_cfg<256, 64, 0>(a, s);
-        if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 0>(a, s);
-        return launch_cfg<1024, 64, 0>(a, s);
+        if (c.block == 256 && c.items == 32) return launch_cfg<256, 32, 0>(a, kc, s);
+        if (c.block == 256 && c.items == 64) return launch_cfg<256, 64, 0>(a, kc, s);
+        if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 0>(a, kc, s);
+        return launch_cfg<1024, 64, 0>(a, kc, s);
     }
-    if (c.block == 256 && c.items == 32) return launch_cfg<256, 32, 1>(a, s);
-    if (c.block == 256 && c.items == 64) return launch_cfg<256, 64, 1>(a, s);
-    if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 1>(a, s);
-    return launch_cfg<1024, 64, 1>(a, s);
+    if (c.block == 256 && c.items == 32) return launch_cfg<256, 32, 1>(a, kc, s);
+    if (c.block == 256 && c.items == 64) return launch_cfg<256, 64, 1>(a, kc, s);
+    if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 1>(a, kc, s);
+    return launch_cfg<1024, 64, 1>(a, kc, s);
 }
 
 }  // namespace g4s
