@@ -11,15 +11,17 @@
 
 namespace g4s {
 
-constexpr int kFullBlock = 256;                     /* threads per chunk workgroup */
-constexpr int kFullPer = 16;                        /* consecutive terms per thread */
-constexpr int kFullChunk = kFullBlock * kFullPer;   /* terms per chunk */
-constexpr int kFullMaxChunks = 1024;                /* chunks per row: vocab <= 2^22 */
+constexpr int kFullBlock = 256;                     /* threads of the streaming workgroups */
+constexpr int kFullPer = 16;                        /* consecutive terms per lane */
+constexpr int kFullChunk = 64 * kFullPer;           /* terms per chunk: one wave's 1024 */
+constexpr int kFullMaxChunks = 4096;                /* chunks per row: vocab <= 2^22 */
+constexpr int kFullCPW = 4;                         /* chunks per wave, streaming passes */
 constexpr int kFullTab = 4096;                      /* bf16 codes with a tabulated e */
-constexpr int kFullCPW = 4;                         /* chunks per workgroup, lsum/cdf passes */
 constexpr int kNear = 8;  /* e = 1 - j*2^-24 (j < kNear): the values whose p can tie the
                              largest p under the top-k tail's division */
 constexpr int kWideBins = 2048;                     /* radix-select histogram bins */
+constexpr int kSelChunk = kFullBlock * kFullPer;    /* terms per wide-select workgroup */
+constexpr int kSelMaxChunks = 1024;                 /* select chunks per row */
 
 /* Row classes (DoSample's dispatch, src/Gemma4.Model.pas:2756). */
 enum : int32_t { kRowTopk = 0, kRowFull = 1, kRowWide = 2 };
@@ -40,29 +42,26 @@ struct FullRow {
     int32_t nodraw;   /* T <= 0: the greedy choice, no draw (probabilities still written) */
     int32_t count;    /* terms that take part: V, or the wide row's survivors */
     int32_t first;    /* index of the first term that takes part */
+    int32_t beta_end; /* predicted binade of LSum after the last chunk */
     int32_t near[kNear]; /* first index with e == 1 - j*2^-24 (atomic min), INT_MAX: none */
     /* diagnostics: chunks re-evaluated and re-evaluation rounds, LSum chain
      * then draw chain */
     int32_t l_reev, l_rounds, c_reev, c_rounds;
 };
 
-/* Per-chunk records. */
+/* Per-chunk record of the max kernel (and the survivor offsets of the row
+ * kernel). */
 struct FullChunk {
-    uint32_t maxkey;  /* max kernel: chunk's largest key */
-    uint32_t amax;    /* max kernel: largest |x| as a key */
+    uint32_t maxkey;  /* chunk's largest key */
+    uint32_t amax;    /* largest |x| as a key */
     float ymax;       /* approximate y at the chunk's largest logit */
     float sapx;       /* approximate sum of exp(y - ymax) over the terms taking part */
-    ss::PMap lmap;    /* lsum kernel: the chunk's terms in beta_l */
-    ss::PMap cmap;    /* draw kernel: the chunk's p in beta_c */
-    int32_t spare[2];
-    int32_t beta_l;   /* predicted binade of LSum entering the chunk */
-    int32_t beta_c;   /* predicted binade of the running sum entering the chunk */
-    int32_t nsurv;    /* max kernel: terms of the chunk taking part */
-    int32_t fsurv;    /* max kernel: first index taking part, INT_MAX: none */
+    int32_t nsurv;    /* terms of the chunk taking part */
+    int32_t fsurv;    /* first index taking part, INT_MAX: none */
     int32_t soff;     /* row kernel: terms taking part before the chunk */
     int32_t pad;
 };
-static_assert(sizeof(FullChunk) == 64, "FullChunk layout");
+static_assert(sizeof(FullChunk) == 32, "FullChunk layout");
 
 /* Radix select of a wide row's K-th largest key and its tie resolution. */
 struct WideSel {
@@ -94,16 +93,21 @@ struct TieRec {
 
 struct FullWorkspace {
     FullRow* rows = nullptr;     /* [max_batch] */
-    FullChunk* chunks = nullptr; /* [max_batch][kFullMaxChunks] */
+    FullChunk* chunks = nullptr; /* [max_batch][cstride] */
+    ss::PMap* lmap = nullptr;    /* [max_batch][cstride] chunk's terms in beta_l */
+    ss::PMap* cmap = nullptr;    /* [max_batch][cstride] chunk's p in beta_c */
+    int32_t* beta_l = nullptr;   /* [max_batch][cstride] predicted binade of LSum entering */
+    int32_t* beta_c = nullptr;   /* [max_batch][cstride] same for the draw's running sum */
     float* etab = nullptr;       /* [max_batch][kFullTab] */
     /* wide rows */
     WideSel* sel = nullptr;      /* [max_batch] */
     uint32_t* hist = nullptr;    /* [max_batch][kWideBins], zero between launches */
-    TieRec* ties = nullptr;      /* [max_batch][kFullMaxChunks] */
+    TieRec* ties = nullptr;      /* [max_batch][kSelMaxChunks] */
     uint32_t* bits = nullptr;    /* [max_batch][ceil(vocab/32)] surviving tied copies */
     float* heap_v = nullptr;     /* [vocab] replay heap (one row at a time) */
     int32_t* heap_i = nullptr;   /* [vocab] */
     int32_t bits_stride = 0;     /* words per row of `bits` */
+    int32_t cstride = 0;         /* chunk records per row (= chunks of the vocabulary) */
 };
 
 struct FullArgs {
@@ -116,7 +120,9 @@ struct FullArgs {
     g4s_params p0;
     double u0;
     float softcap;
-    int32_t nch;
+    int32_t nch;      /* chunks of kFullChunk terms per row */
+    int32_t nsel;     /* chunks of kSelChunk terms per row (wide select) */
+    int32_t nstage;   /* chunks each chain precomputes (set by full_launch) */
     int32_t wide_on;  /* wide rows are handled by this launch */
     FullWorkspace ws;
     int32_t* ids;

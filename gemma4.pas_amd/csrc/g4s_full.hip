@@ -23,9 +23,11 @@
  * the arithmetic (y = RN32(cap * tanh(x / cap)), p_i = RN32(e_i / LSum)),
  * and the first survivor as the draw when fl32(u * TopP) <= 0.
  *
- * Rows are cut into chunks of 4096 terms, 16 consecutive terms per thread
- * of a 256-thread workgroup.  Launches (the wide ones only when wide rows
- * can occur):
+ * Rows are cut into chunks of 1024 terms, one wave's: 16 consecutive terms
+ * per lane.  The streaming passes give every wave kFullCPW chunks and use
+ * no barrier beyond loading the e table; the two chains are one workgroup
+ * per row whose wave 0 walks the row.  Launches (the wide ones only when
+ * wide rows can occur; they cut rows into 4096-term select chunks):
  *   wide hist/find x3: 11+11+10-bit MSD radix select of tau (LDS
  *             histograms added into a per-row histogram, one workgroup per
  *             row fixes each digit);
@@ -40,14 +42,15 @@
  *             the streaming passes look e up; the predicted binade of LSum
  *             entering every chunk (a parallel prefix of the estimates);
  *   3 lsum:   each chunk's terms as one exact map of the running sum in its
- *             predicted binade (g4s_seqsum.h), plus binary64 chunk sums;
- *   4 chain:  one workgroup per row chains the maps left to right,
- *             verifying every step and re-evaluating any chunk whose map
- *             does not apply: LSum, the argmax, and the predicted binades of
- *             the draw's running sum;
+ *             predicted binade (g4s_seqsum.h);
+ *   4 chain:  LSum: the workgroup stages in LDS the chunks where the sum is
+ *             predicted to change binade, then wave 0 composes the chunk
+ *             maps 64 at a time, verifying every step, and re-evaluates the
+ *             chunks whose map does not apply; the argmax; the predicted
+ *             binades of the draw's running sum;
  *   5 cdf:    p for the outputs and the same maps for p, up to the chunk
  *             where the running sum is predicted to reach fl32(u*TopP);
- *   6 draw:   one workgroup per row finds the exact first index and writes
+ *   6 draw:   the same chain over the maps of p: the exact first index, and
  *             the token.
  * Transcendental steps are correctly rounded (g4s_crmath.h); every running
  * sum is the reference's left-to-right binary32 sum, bit for bit.
@@ -65,7 +68,8 @@ using ss::State;
 namespace {
 
 constexpr int NWF = kFullBlock / 64;                 /* waves per workgroup */
-constexpr int CPT = kFullMaxChunks / kFullBlock;     /* chunk records per thread */
+constexpr int kRowCPT = kFullMaxChunks / kFullBlock;  /* most chunk records per thread */
+constexpr int kSelCPT = kSelMaxChunks / kFullBlock;   /* select records per thread */
 
 struct RowIn {
     g4s_params p;
@@ -231,13 +235,18 @@ __device__ __forceinline__ float wave_sum_f32(float v)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-/* Index of a bf16 code in the row's table, or -1 outside the window. */
-__device__ __forceinline__ int tab_index(uint32_t code, int win_lo)
+/* The table holds the codes whose |x| lies in the 16 binades from win_lo
+ * up, entry (sign << 11) | (binade - win_lo) << 7 | mantissa.  With
+ * d = code - (win_lo << 7) that entry is (d & 0x7FF) | ((code >> 4) & 0x800)
+ * (bit 11 of code >> 4 is the sign: the exponent field shifted right by 4
+ * stays below 0x800), and the code is in the window exactly when bits 11-14
+ * of d are 0 (a code below the window borrows into them: win_lo <= 240). */
+__device__ __forceinline__ uint32_t tab_index(uint32_t code, uint32_t base, uint32_t& d)
 {
-    const int eb = (int)((code >> 7) & 0xFFu) - win_lo;
-    if ((unsigned)eb >= 16u) return -1;
-    return (int)(((code >> 15) << 11) | ((uint32_t)eb << 7) | (code & 0x7Fu));
+    d = code - base;
+    return (d & 0x7FFu) | ((code >> 4) & 0x800u);
 }
+constexpr uint32_t kTabMiss = 0x7800u;
 
 struct Ctx {
     float cap, inv_cap, inv_t, m;
@@ -251,19 +260,6 @@ __device__ __noinline__ float e_direct(float x, Ctx c)
     return exp_diff_cr32(y_exact(x, c.cls, c.cap, c.inv_cap, c.scale, c.inv_t), c.m);
 }
 
-/* e of one term: the table when the code is in the window, else evaluated. */
-template <int DT>
-__device__ __forceinline__ float e_of(uint32_t raw, const Ctx& c, const float* tab)
-{
-    if constexpr (DT == 1) {
-        if (c.win_lo >= 0) {
-            const int ti = tab_index(raw, c.win_lo);
-            if (ti >= 0) return tab[ti];
-        }
-    }
-    return e_direct(x_of<DT>(raw), c);
-}
-
 /* The e of one thread's 16 terms (0 for terms that do not take part).  For
  * bf16 logits every term reads the table (a clamped index, no branch); the
  * rare codes outside its window are evaluated afterwards, behind one
@@ -274,20 +270,24 @@ __device__ __forceinline__ void terms_e_t(const uint32_t (&raw)[kFullPer], int n
                                           const float* tab, float (&t)[kFullPer])
 {
     if (DT == 1 && c.win_lo >= 0) {
-        uint32_t miss = 0u;
+        const uint32_t base = (uint32_t)c.win_lo << 7;
+        uint32_t anymiss = 0u;
+        bool part[kFullPer];
 #pragma unroll
         for (int j = 0; j < kFullPer; ++j) {
-            const bool part =
-                GENERAL ? (j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j)) : true;
-            const int ti = tab_index(raw[j], c.win_lo);
-            const float v = tab[ti < 0 ? 0 : ti];
-            t[j] = part ? v : 0.0f;
-            miss |= (part && ti < 0) ? (1u << j) : 0u;
+            part[j] = GENERAL ? (j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j)) : true;
+            uint32_t d;
+            const float v = tab[tab_index(raw[j], base, d)];
+            t[j] = part[j] ? v : 0.0f;
+            anymiss |= part[j] ? (d & kTabMiss) : 0u;
         }
-        if (__ballot(miss != 0u)) {
+        if (__ballot(anymiss != 0u)) {
 #pragma unroll
-            for (int j = 0; j < kFullPer; ++j)
-                if (miss & (1u << j)) t[j] = e_direct(x_of<DT>(raw[j]), c);
+            for (int j = 0; j < kFullPer; ++j) {
+                uint32_t d;
+                (void)tab_index(raw[j], base, d);
+                if (part[j] && (d & kTabMiss) != 0u) t[j] = e_direct(x_of<DT>(raw[j]), c);
+            }
         }
         return;
     }
@@ -330,20 +330,6 @@ struct Scratch {
     int32_t misc[16];
 };
 
-template <int DT>
-struct TabShared {
-    Scratch s;
-    float tab[DT == 1 ? kFullTab : 1];
-};
-
-template <int DT>
-struct ChainShared {
-    Scratch s;
-    float tab[DT == 1 ? kFullTab : 1];
-    PMap cmap[kFullMaxChunks];
-    int32_t cbeta[kFullMaxChunks];
-    float cpost[kFullMaxChunks]; /* LSum chain: exact running sum after each chunk */
-};
 
 __device__ __forceinline__ uint32_t block_max_key(uint32_t v, Scratch& sh, int slot)
 {
@@ -476,7 +462,7 @@ __device__ __forceinline__ PMap thread_map(const float (&t)[kFullPer], int nvali
      * the sum of the c (summed in binary32: exact below 2^24, and a sum
      * that reaches 2^24 means the thread leaves the binade either way).  A
      * tie (fract(q) == 1/2) anywhere in the wave takes the exact per-term
-     * maps (wave-uniform branch; ties are rare). */
+     * lane maps of ss::lane_map (wave-uniform branch). */
     float cs = 0.0f;
     bool tie = false;
     const int sh = 150 - e;
@@ -492,184 +478,467 @@ __device__ __forceinline__ PMap thread_map(const float (&t)[kFullPer], int nvali
         f.d1 = f.d0;
         return f;
     }
-    f = ss::map_identity();
-#pragma unroll
-    for (int j = 0; j < kFullPer; ++j)
-        f = ss::map_sat(ss::map_then(f, ss::map_of_ct(ss::term_ct_f(t[j], e))));
-    return f;
+    return ss::lane_map(t, kFullPer, e);
 }
 
-/* The whole workgroup's map of a chunk (thread maps scanned over the wave,
- * wave totals composed in order); valid in thread 0. */
-__device__ __forceinline__ PMap block_chunk_map(PMap f, Scratch& sh)
+/* ------------------------------------------------------- wave helpers */
+
+/* The map of a wave's 1024 terms (every lane gets it): the sum of constant
+ * thread maps, or the composition of the thread maps in lane order. */
+__device__ __forceinline__ PMap wave_chunk_map(PMap f)
 {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    PMap r;
+    if (__ballot(f.d0 != f.d1) == 0) {
+        /* a thread map >= 2^24 leaves the binade whatever follows: capping it
+         * there keeps the sum of 64 below 2^31 */
+        const int32_t c = f.d0 > ss::kTop ? ss::kTop : f.d0;
+        int32_t s = wave_sum_i32(c);
+        s = s > (1 << 26) ? (1 << 26) : s;
+        r.d0 = r.d1 = s;
+        return r;
+    }
     const PMap incl = wave_scan_maps(f);
-    if (lane == 63) sh.wmap[wid] = incl;
-    __syncthreads();
-    PMap r = ss::map_identity();
-    if (threadIdx.x == 0)
-        for (int w = 0; w < NWF; ++w) r = ss::map_sat(ss::map_then(r, sh.wmap[w]));
-    __syncthreads();
+    r.d0 = __builtin_amdgcn_readlane(incl.d0, 63);
+    r.d1 = __builtin_amdgcn_readlane(incl.d1, 63);
     return r;
 }
 
 /*
- * Exact evaluation of one chunk's running sum from the exact entering state
- * `st`, by the whole workgroup (thread t holds terms t*16 .. t*16+15 of the
- * chunk; threads before `pos` are already accounted for).  Each round maps
- * every remaining thread's terms in the current binade, finds the first
- * thread whose exit leaves the binade (or reaches `thr`), and walks that
- * thread's terms from its exact entering sum: the map step while the sum
- * stays in its binade, one plain binary32 addition where it leaves it.
- * Returns the state after the chunk or, when `thr` is reached, the index
- * (chunk-relative) of the first term whose running sum reaches it in *hit.
- * Rounds are counted in sh.misc[12].
+ * One resolution round over a chunk held by the wave (lane l holds terms
+ * l*16 .. l*16+15, 0 beyond the row): `f` are this round's lane maps in the
+ * binade of `st` (identity for lanes before `pos`, which are accounted for).
+ * The maps are composed over the wave and applied to st; if every lane stays
+ * in the binade (and below thr) st becomes the state after the chunk and the
+ * round returns true.  Otherwise the first lane ls that leaves (or reaches
+ * thr) enters exactly at its composed state, so it adds its terms to that
+ * sum with plain binary32 additions: st becomes the state after lane ls, pos
+ * ls + 1, and *hit the chunk-relative index of the first term whose running
+ * sum reaches thr, if one does.  Wave-uniform control flow.
  */
-__device__ State resolve_chunk(const float (&t)[kFullPer], int nvalid, State st, float thr,
-                               int pos, int* hit, Scratch& sh)
+__device__ __forceinline__ bool round_step(PMap f, const float (&t)[kFullPer], State& st,
+                                           float thr, int& pos, int* hit)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    *hit = -1;
-    while (pos < kFullBlock) {
-        const int32_t e = st.e;
-        const PMap f = (tid >= pos) ? thread_map(t, nvalid, e) : ss::map_identity();
-        PMap incl, excl;
-        if (__ballot(f.d0 != f.d1) == 0) {
-            /* constant maps (no half-unit tie in the wave): a prefix sum */
-            const int32_t x = wave_inclusive_scan(f.d0 > (1 << 26) ? (1 << 26) : f.d0);
-            incl.d0 = incl.d1 = x > (1 << 26) ? (1 << 26) : x;
-            const int32_t y = __builtin_amdgcn_update_dpp(0, incl.d0, 0x138, 0xf, 0xf, false);
-            excl.d0 = excl.d1 = y;
-        } else {
-            incl = wave_scan_maps(f);
-            excl = wave_shift_map(incl);
-        }
-        if (lane == 63) sh.wmap[wid] = incl;
-        __syncthreads();
-        if (tid == 0) {
-            ++sh.misc[12];
-            int32_t m = st.m;
-            for (int w = 0; w < NWF; ++w) {
-                sh.went[w] = m;
-                m = m >= ss::kTop ? m : ss::map_apply(sh.wmap[w], m);
-            }
-            sh.misc[8] = m;
-        }
-        __syncthreads();
-        const int32_t mw = sh.went[wid];
-        const int32_t m_in = mw >= ss::kTop ? ss::kTop : ss::map_apply(excl, mw);
-        const int32_t m_out = m_in >= ss::kTop ? ss::kTop : ss::map_apply(f, m_in);
-        const bool stop = tid >= pos && (m_out >= ss::kTop ||
-                                         ss::value_of(State{e, m_out}) >= thr);
-        const uint64_t bal = __ballot(stop);
-        if (lane == 0) sh.tcand[wid] = bal ? wid * 64 + (int)__builtin_ctzll(bal) : INT_MAX;
-        __syncthreads();
-        int tstar = INT_MAX;
+    const int lane = threadIdx.x & 63;
+    const int32_t e = st.e;
+    int32_t m_in, m_out;
+    if (__ballot(f.d0 != f.d1) == 0) {
+        /* constant maps: a prefix sum (a lane's map >= 2^24 leaves anyway) */
+        const int32_t c = f.d0 > ss::kTop ? ss::kTop : f.d0;
+        const int32_t x = wave_inclusive_scan(c); /* <= 2^30 */
+        m_in = st.m + (x - c);
+        m_out = st.m + x;
+    } else {
+        const PMap incl = wave_scan_maps(f);
+        const PMap excl = wave_shift_map(incl);
+        m_in = ss::map_apply(excl, st.m);
+        m_in = m_in >= ss::kTop ? ss::kTop : m_in;
+        m_out = m_in >= ss::kTop ? ss::kTop : ss::map_apply(f, m_in);
+    }
+    const uint64_t bal =
+        __ballot(lane >= pos && (m_out >= ss::kTop || ss::value_of(State{e, m_out}) >= thr));
+    if (bal == 0) {
+        st.m = __builtin_amdgcn_readlane(m_out, 63);
+        return true;
+    }
+    const int ls = (int)__builtin_ctzll(bal);
+    /* every lane adds its terms from its own entering sum (no divergence;
+     * only lane ls's is used); terms are >= 0, so the running sum is
+     * monotone and the first term reaching thr follows the count of partial
+     * sums below it */
+    float sum = ss::value_of(State{e, m_in < ss::kTop ? m_in : 0});
+    int below = 0;
 #pragma unroll
-        for (int w = 0; w < NWF; ++w) tstar = sh.tcand[w] < tstar ? sh.tcand[w] : tstar;
-        if (tstar == INT_MAX) {
-            st.m = sh.misc[8];
-            __syncthreads();
-            return st;
-        }
-        if (tid == tstar) {
-            /* m_in is exact (every earlier thread stayed in the binade), so
-             * the thread's terms are plain binary32 additions from there */
-            float sum = ss::value_of(State{e, m_in});
-            int h = -1;
-#pragma unroll
-            for (int j = 0; j < kFullPer; ++j) {
-                if (j < nvalid && h < 0) {
-                    sum = sum + t[j];
-                    if (sum >= thr) h = tstar * kFullPer + j;
-                }
-            }
-            const State s2 = ss::state_of(sum);
-            sh.misc[9] = s2.e;
-            sh.misc[10] = s2.m;
-            sh.misc[11] = h;
-        }
-        __syncthreads();
-        st.e = sh.misc[9];
-        st.m = sh.misc[10];
-        const int h = sh.misc[11];
-        __syncthreads();
-        if (h >= 0) {
-            *hit = h;
-            return st;
-        }
-        pos = tstar + 1;
+    for (int j = 0; j < kFullPer; ++j) {
+        sum = sum + t[j];
+        below += sum < thr ? 1 : 0;
+    }
+    sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sum), ls));
+    below = __builtin_amdgcn_readlane(below, ls);
+    st = ss::state_of(sum);
+    if (sum >= thr) *hit = ls * kFullPer + below;
+    pos = ls + 1;
+    return false;
+}
+
+/* Exact evaluation of one chunk held by the wave from the exact entering
+ * state st, lanes from `pos` on: rounds with the lane maps in the current
+ * binade.  Returns the state after the chunk, or at the term reaching thr
+ * (*hit, chunk-relative; -1: none). */
+__device__ State resolve_wave(const float (&t)[kFullPer], int nvalid, State st, float thr,
+                              int pos, int* hit, int* rounds)
+{
+    const int lane = threadIdx.x & 63;
+    while (pos < 64) {
+        ++*rounds;
+        PMap f = thread_map(t, nvalid, st.e); /* every lane: thread_map votes over the wave */
+        if (lane < pos) f = ss::map_identity();
+        if (round_step(f, t, st, thr, pos, hit) || *hit >= 0) break;
     }
     return st;
 }
 
-/* Chain the chunk maps from chunk cb on, while they apply: a chunk's map
- * applies when the sum enters it in the predicted binade and the result
- * stays in that binade (and, for the draw, below thr).  Wave 0 walks the
- * chunks with the maps held one per lane (readlane per chunk); the state
- * after the last accepted chunk goes to sh.misc[9..10] and the first chunk
- * that does not apply (nch: none) to sh.misc[14].  Ends with a barrier. */
-__device__ void chain_maps(const PMap* cmap, const int32_t* cbeta, int cb, int nch, State st,
-                           float thr, Scratch& sh, float* cpost)
+/* The first kHeadLanes lanes of a row's first chunk, one lane after the
+ * other with plain binary32 additions (the running sum changes binade every
+ * few terms there). */
+constexpr int kHeadLanes = 8;
+__device__ State head_walk(const float (&t)[kFullPer], float thr, int* hit)
 {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        int stop = nch;
-        for (int g = cb; g < nch && stop == nch; g += 64) {
-            const int c = g + lane;
-            const PMap f = c < nch ? cmap[c] : ss::map_identity();
-            const int32_t be = c < nch ? cbeta[c] : -1;
-            const int n = nch - g < 64 ? nch - g : 64;
-            float post = 0.0f;
-            int l = 0;
-            for (; l < n; ++l) {
-                const int32_t bl = __builtin_amdgcn_readlane(be, l);
-                const int32_t d0 = __builtin_amdgcn_readlane(f.d0, l);
-                const int32_t d1 = __builtin_amdgcn_readlane(f.d1, l);
-                const int32_t m2 = st.m + ((st.m & 1) ? d1 : d0);
-                if (st.e != bl || m2 >= ss::kTop || ss::value_of(State{st.e, m2}) >= thr) {
-                    stop = g + l;
-                    break;
-                }
-                st.m = m2;
-                post = lane == l ? ss::value_of(st) : post;
+    float s = 0.0f;
+    for (int l = 0; l < kHeadLanes; ++l) {
+        float x = s;
+        int below = 0;
+#pragma unroll
+        for (int j = 0; j < kFullPer; ++j) {
+            x = x + t[j];
+            below += x < thr ? 1 : 0;
+        }
+        s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+        below = __builtin_amdgcn_readlane(below, l);
+        if (s >= thr) {
+            *hit = l * kFullPer + below;
+            break;
+        }
+    }
+    return ss::state_of(s);
+}
+
+/*
+ * Chain the chunk maps from chunk c on, 64 chunks per step: the maps are
+ * composed over the wave and applied to the entering state, and accepted up
+ * to the first chunk whose map does not apply -- a chunk applies when the
+ * sum enters it in the predicted binade and stays in that binade (and, for
+ * the draw, below thr).  Returns that chunk (nch: none) with `st` the exact
+ * state entering it; cpost (when given) gets the exact running sum after
+ * every accepted chunk.  One wave; wave-uniform control flow.
+ */
+template <bool THR>
+__device__ int walk_maps(const PMap* cm, const int32_t* cb, int c, int nch, State& st, float thr,
+                         float* cpost)
+{
+    const int lane = threadIdx.x & 63;
+    for (int g = c; g < nch; g += 64) {
+        const int cc = g + lane;
+        const bool valid = cc < nch;
+        const PMap f = valid ? cm[cc] : ss::map_identity();
+        const int32_t be = valid ? cb[cc] : -1;
+        int32_t m_after;
+        if (__ballot(f.d0 != f.d1) == 0) {
+            const int32_t x = wave_inclusive_scan(f.d0 > ss::kTop ? ss::kTop : f.d0);
+            m_after = st.m + x;
+        } else {
+            m_after = ss::map_apply(wave_scan_maps(f), st.m);
+        }
+        bool bad = !valid || be != st.e || m_after >= ss::kTop;
+        if (THR) bad = bad || ss::value_of(State{st.e, m_after}) >= thr;
+        const uint64_t bal = __ballot(bad);
+        const int l = bal ? (int)__builtin_ctzll(bal) : 64;
+        if (cpost && lane < l) cpost[cc] = ss::value_of(State{st.e, m_after});
+        if (l > 0) st.m = __builtin_amdgcn_readlane(m_after, l - 1);
+        if (l < 64) return g + l < nch ? g + l : nch;
+    }
+    return nch;
+}
+
+/* 16 terms of a lane from a staged (full) chunk in LDS. */
+template <int DT>
+__device__ __forceinline__ void stage16(const char* src, uint32_t (&raw)[kFullPer])
+{
+    if constexpr (DT == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 w = reinterpret_cast<const uint4*>(src)[q];
+            raw[4 * q] = w.x;
+            raw[4 * q + 1] = w.y;
+            raw[4 * q + 2] = w.z;
+            raw[4 * q + 3] = w.w;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint4 w = reinterpret_cast<const uint4*>(src)[q];
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                raw[8 * q + 2 * i] = ww[i] & 0xFFFFu;
+                raw[8 * q + 2 * i + 1] = ww[i] >> 16;
             }
-            if (cpost && lane < l) cpost[c] = post; /* exact running sum after chunk c */
         }
-        if (lane == 0) {
-            sh.misc[9] = st.e;
-            sh.misc[10] = st.m;
-            sh.misc[14] = stop;
+    }
+}
+
+/* Most chunks a chain precomputes: the ones it is predicted to re-evaluate
+ * (where the running sum changes binade, chunk 0, the draw's last chunk). */
+constexpr int kStageMax = 16;
+
+/* A staged chunk's lane maps in its predicted binade b and in b + 1. */
+struct StageMaps {
+    PMap lo[64];
+    PMap hi[64];
+    int32_t b;
+    int32_t pad[3];
+};
+
+/* LDS of a chain workgroup (dynamic shared memory): the e table, the chunk
+ * maps and predicted binades, the exact running sum after every chunk, the
+ * staged chunk numbers, and per staged chunk its maps and its terms (lane l's
+ * 16 terms at l*16). */
+struct ChainLds {
+    float* tab;
+    PMap* cm;
+    int32_t* cb;
+    float* cpost;
+    int32_t* sid;
+    StageMaps* sm;
+    float* tv;
+};
+
+__host__ __device__ __forceinline__ size_t chain_lds_layout(int dt, int nch, int nstage, size_t* off)
+{
+    size_t o = 0;
+    off[0] = o;
+    o += dt == 1 ? (size_t)kFullTab * 4 : 0;
+    off[1] = o;
+    o += (size_t)nch * sizeof(PMap);
+    off[2] = o;
+    o += (size_t)nch * 4;
+    off[3] = o;
+    o += (size_t)nch * 4;
+    off[4] = o;
+    o += (size_t)kStageMax * 4;
+    o = (o + 15) & ~(size_t)15;
+    off[5] = o;
+    o += (size_t)nstage * sizeof(StageMaps);
+    o = (o + 15) & ~(size_t)15;
+    off[6] = o;
+    o += (size_t)nstage * kFullChunk * 4;
+    return o;
+}
+
+template <int DT>
+__device__ __forceinline__ ChainLds chain_lds(char* base, int nch, int nstage)
+{
+    size_t off[7];
+    (void)chain_lds_layout(DT, nch, nstage, off);
+    ChainLds L;
+    L.tab = reinterpret_cast<float*>(base + off[0]);
+    L.cm = reinterpret_cast<PMap*>(base + off[1]);
+    L.cb = reinterpret_cast<int32_t*>(base + off[2]);
+    L.cpost = reinterpret_cast<float*>(base + off[3]);
+    L.sid = reinterpret_cast<int32_t*>(base + off[4]);
+    L.sm = reinterpret_cast<StageMaps*>(base + off[5]);
+    L.tv = reinterpret_cast<float*>(base + off[6]);
+    return L;
+}
+
+/* The 16 terms (e, or p when P) of lane `lane` in chunk c. */
+template <int DT, bool P>
+__device__ __forceinline__ int chain_load_terms(const FullArgs& a, const char* rowp, int c,
+                                                const Ctx& ctx, const Mask& k, const FullRow& r,
+                                                const float* tab, float (&t)[kFullPer])
+{
+    const int lane = threadIdx.x & 63;
+    uint32_t raw[kFullPer];
+    const int64_t e0 = (int64_t)c * kFullChunk + (int64_t)lane * kFullPer;
+    const int nv = load16<DT>(rowp, e0, a.vocab, raw);
+    terms_e<DT>(raw, nv, e0, ctx, k, tab, t);
+    if (P) {
+#pragma unroll
+        for (int j = 0; j < kFullPer; ++j) t[j] = p_of(t[j], k.cls, r.inv, r.lsum);
+    }
+    return nv;
+}
+
+/*
+ * Prologue of a chain workgroup (all threads): the row's table, the chunk
+ * maps and binades of chunks 0..clast (identity and -1 beyond), the first
+ * `nstage` full chunks that `pred` selects, and for each of those (one wave
+ * per chunk) its terms and its lanes' constant maps in its predicted binade
+ * and the next.  Ends with a barrier.
+ */
+/* Chain workgroups: 16 waves for the prologue (one staged chunk each), then
+ * wave 0 alone. */
+constexpr int kChainBlock = 1024;
+constexpr int kChainWaves = kChainBlock / 64;
+constexpr int kChainCPT = kFullMaxChunks / kChainBlock;
+static_assert(kFullTab / 4 == kChainBlock, "one float4 of the table per thread");
+static_assert(kStageMax % kChainWaves == 0, "staged chunks per wave");
+
+struct ChainScratch {
+    int32_t iscan[kChainWaves];
+};
+
+/* Exclusive prefix over the chain workgroup in thread order (ints). */
+__device__ __forceinline__ int chain_excl_scan(int v, ChainScratch& sh, int& total)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int x = wave_inclusive_scan(v);
+    if (lane == 63) sh.iscan[wid] = x;
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kChainWaves; ++w) {
+        off += (w < wid) ? sh.iscan[w] : 0;
+        tot += sh.iscan[w];
+    }
+    total = tot;
+    __syncthreads();
+    return off + x - v;
+}
+
+template <int DT, bool P, typename Pred>
+__device__ void chain_prologue(const FullArgs& a, int row, const FullRow& r, const Ctx& ctx,
+                               const Mask& k, const PMap* gmap, const int32_t* gbeta, int clast,
+                               Pred pred, const ChainLds& L, ChainScratch& sh)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int nch = a.nch;
+    const int V = a.vocab;
+    const int nstage = a.nstage;
+    if (DT == 1 && r.win_lo >= 0) {
+        const float4* src = reinterpret_cast<const float4*>(a.ws.etab + (int64_t)row * kFullTab);
+        reinterpret_cast<float4*>(L.tab)[tid] = src[tid]; /* kFullTab / 4 == kChainBlock */
+    }
+    for (int c = tid; c < nch; c += kChainBlock) {
+        L.cm[c] = c <= clast ? gmap[c] : ss::map_identity();
+        L.cb[c] = c <= clast ? gbeta[c] : -1;
+    }
+    /* the staged chunks: the first nstage full chunks in index order that
+     * pred selects (thread t looks at chunks t*cpt .. t*cpt+cpt-1) */
+    const int cpt = (nch + kChainBlock - 1) / kChainBlock;
+    uint32_t selm = 0u;
+    int cnt = 0;
+#pragma unroll
+    for (int q = 0; q < kChainCPT; ++q) {
+        const int c = tid * cpt + q;
+        if (q < cpt && c < nch && c <= clast && (int64_t)(c + 1) * kFullChunk <= V && pred(c)) {
+            selm |= 1u << q;
+            ++cnt;
         }
+    }
+    int total;
+    int pos = chain_excl_scan(cnt, sh, total);
+#pragma unroll
+    for (int q = 0; q < kChainCPT; ++q) {
+        if (selm & (1u << q)) {
+            if (pos < nstage) L.sid[pos] = tid * cpt + q;
+            ++pos;
+        }
+    }
+    if (tid < kStageMax && tid >= (total < nstage ? total : nstage)) L.sid[tid] = -1;
+    __syncthreads();
+    /* wave w precomputes slot w */
+    constexpr int kSlots = kStageMax / kChainWaves;
+    constexpr int kVec = kFullPer * Elem<DT>::SIZE / 16; /* 16-byte loads per lane per chunk */
+    const char* rowp = row_ptr<DT>(a, row);
+    uint4 pk[kSlots][kVec];
+    int cs[kSlots];
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+        const int sl = wid + i * kChainWaves;
+        cs[i] = sl < nstage ? L.sid[sl] : -1;
+        if (cs[i] >= 0) {
+            const uint4* src = reinterpret_cast<const uint4*>(
+                rowp + ((int64_t)cs[i] * kFullChunk + (int64_t)lane * kFullPer) * Elem<DT>::SIZE);
+#pragma unroll
+            for (int q = 0; q < kVec; ++q) pk[i][q] = src[q];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+        const int c = cs[i];
+        if (c < 0) continue;
+        const int sl = wid + i * kChainWaves;
+        uint32_t raw[kFullPer];
+#pragma unroll
+        for (int q = 0; q < kVec; ++q) {
+            const uint32_t w4[4] = {pk[i][q].x, pk[i][q].y, pk[i][q].z, pk[i][q].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                if (DT == 0) {
+                    raw[4 * q + m] = w4[m];
+                } else {
+                    raw[8 * q + 2 * m] = w4[m] & 0xFFFFu;
+                    raw[8 * q + 2 * m + 1] = w4[m] >> 16;
+                }
+            }
+        }
+        float t[kFullPer];
+        const int64_t e0 = (int64_t)c * kFullChunk + (int64_t)lane * kFullPer;
+        terms_e<DT>(raw, kFullPer, e0, ctx, k, L.tab, t);
+        if (P) {
+#pragma unroll
+            for (int j = 0; j < kFullPer; ++j) t[j] = p_of(t[j], k.cls, r.inv, r.lsum);
+        }
+        float4* dst = reinterpret_cast<float4*>(L.tv + (size_t)sl * kFullChunk + lane * kFullPer);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dst[q] = make_float4(t[4 * q], t[4 * q + 1], t[4 * q + 2], t[4 * q + 3]);
+        const int32_t b = gbeta[c] < 1 ? 1 : (gbeta[c] > 253 ? 253 : gbeta[c]);
+        L.sm[sl].lo[lane] = thread_map(t, kFullPer, b);
+        L.sm[sl].hi[lane] = thread_map(t, kFullPer, b + 1);
+        if (lane == 0) L.sm[sl].b = b;
     }
     __syncthreads();
 }
 
-/* The row's first kHead terms (threads 0 .. kHead/16 - 1 of chunk 0), where
- * the running sum changes binade every few terms, summed left to right in
- * binary32 by wave 0 (one readlane per term); the result and the first index
- * reaching `thr` go to sh.misc[9..11] for the whole workgroup. */
-constexpr int kHead = 256;
-__device__ void head_walk(const float (&t)[kFullPer], float thr, Scratch& sh)
+/*
+ * The exact running sum through chunk c from the exact entering state st,
+ * by the chain wave: chunk 0 starts with the sequential head; a staged chunk
+ * takes its precomputed lane maps for the predicted binade and the next (a
+ * crossing into the next binade then costs two map compositions and one
+ * lane's plain additions); anything else takes the general rounds.  *hit gets
+ * the chunk-relative index of the first term whose running sum reaches thr
+ * (-1: none).
+ */
+template <int DT, bool P>
+__device__ State chain_chunk(const FullArgs& a, const char* rowp, int c, State st, float thr,
+                             const ChainLds& L, const Ctx& ctx, const Mask& k, const FullRow& r,
+                             int* hit, int* rounds)
 {
-    if (threadIdx.x >= 64) return;
-    float s = 0.0f;
-    int h = -1;
-    for (int l = 0; l < kHead / kFullPer; ++l) {
+    const int lane = threadIdx.x & 63;
+    const int sl = lane < a.nstage ? L.sid[lane] : -1;
+    const uint64_t hb = __ballot(sl == c);
+    float t[kFullPer];
+    int nv = kFullPer;
+    int pos = 0;
+    *hit = -1;
+    if (hb) {
+        const int s = (int)__builtin_ctzll(hb);
+        const float4* src =
+            reinterpret_cast<const float4*>(L.tv + (size_t)s * kFullChunk + lane * kFullPer);
 #pragma unroll
-        for (int j = 0; j < kFullPer; ++j) {
-            s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[j]), l));
-            if (h < 0 && s >= thr) h = l * kFullPer + j;
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = src[q];
+            t[4 * q] = v.x;
+            t[4 * q + 1] = v.y;
+            t[4 * q + 2] = v.z;
+            t[4 * q + 3] = v.w;
         }
-        if (h >= 0) break;
+        const StageMaps* sm = L.sm + s;
+        const int32_t b = sm->b;
+        if (c == 0) {
+            st = head_walk(t, thr, hit);
+            if (*hit >= 0) return st;
+            pos = kHeadLanes;
+        } else if (st.e == b) {
+            ++*rounds;
+            if (round_step(sm->lo[lane], t, st, thr, pos, hit) || *hit >= 0) return st;
+            if (pos < 64 && st.e == b + 1) {
+                ++*rounds;
+                const PMap f = lane >= pos ? sm->hi[lane] : ss::map_identity();
+                if (round_step(f, t, st, thr, pos, hit) || *hit >= 0) return st;
+            }
+        }
+    } else {
+        nv = chain_load_terms<DT, P>(a, rowp, c, ctx, k, r, L.tab, t);
+        if (c == 0) {
+            st = head_walk(t, thr, hit);
+            if (*hit >= 0) return st;
+            pos = kHeadLanes;
+        }
     }
-    if (threadIdx.x == 0) {
-        const State st = ss::state_of(s);
-        sh.misc[9] = st.e;
-        sh.misc[10] = st.m;
-        sh.misc[11] = h;
-    }
+    if (pos < 64) st = resolve_wave(t, nv, st, thr, pos, hit, rounds);
+    return st;
 }
 
 /* Final outputs of a row (called by wave 0 of the row's workgroup). */
@@ -740,7 +1009,7 @@ __device__ int kth_in_chunk(const FullArgs& a, const char* rowp, int cb, int r, 
                             Scratch& sh)
 {
     uint32_t raw[kFullPer];
-    const int64_t e0 = (int64_t)cb * kFullChunk + (int64_t)threadIdx.x * kFullPer;
+    const int64_t e0 = (int64_t)cb * kSelChunk + (int64_t)threadIdx.x * kFullPer;
     const int nv = load16<DT>(rowp, e0, a.vocab, raw);
     int cnt = 0;
 #pragma unroll
@@ -784,7 +1053,7 @@ __global__ __launch_bounds__(kFullBlock) void wide_hist_kernel(FullArgs a, int p
     for (int i = tid; i < kWideBins; i += kFullBlock) hist[i] = 0u;
     __syncthreads();
     uint32_t raw[kFullPer];
-    const int nv = load16<DT>(row_ptr<DT>(a, row), (int64_t)b * kFullChunk + (int64_t)tid * kFullPer,
+    const int nv = load16<DT>(row_ptr<DT>(a, row), (int64_t)b * kSelChunk + (int64_t)tid * kFullPer,
                               a.vocab, raw);
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j) {
@@ -899,7 +1168,7 @@ __global__ __launch_bounds__(kFullBlock) void wide_ties_kernel(FullArgs a)
     const WideSel s = a.ws.sel[row];
     if (s.state != kSelTies) return;
     uint32_t raw[kFullPer];
-    const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
+    const int64_t e0 = (int64_t)b * kSelChunk + (int64_t)tid * kFullPer;
     const int nv = load16<DT>(row_ptr<DT>(a, row), e0, a.vocab, raw);
     int ge = 0, eq = 0;
     uint32_t gt = 0u; /* last index above tau, plus one */
@@ -920,7 +1189,7 @@ __global__ __launch_bounds__(kFullBlock) void wide_ties_kernel(FullArgs a)
         t.ceq = eq;
         t.maxgt = (int32_t)gt - 1;
         t.pad = 0;
-        a.ws.ties[(int64_t)row * kFullMaxChunks + b] = t;
+        a.ws.ties[(int64_t)row * kSelMaxChunks + b] = t;
     }
 }
 
@@ -940,14 +1209,14 @@ __global__ __launch_bounds__(kFullBlock) void wide_ties_find_kernel(FullArgs a)
     WideSel* sp = a.ws.sel + row;
     const WideSel s = *sp;
     if (s.state != kSelTies) return;
-    const int nch = a.nch;
+    const int nch = a.nsel;
     const int K = ri.p.top_k;
-    const TieRec* tr = a.ws.ties + (int64_t)row * kFullMaxChunks;
-    int ge[CPT], eq[CPT];
+    const TieRec* tr = a.ws.ties + (int64_t)row * kSelMaxChunks;
+    int ge[kSelCPT], eq[kSelCPT];
     int sge = 0, seqn = 0, mgt = -1;
 #pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-        const int cb = tid * CPT + q;
+    for (int q = 0; q < kSelCPT; ++q) {
+        const int cb = tid * kSelCPT + q;
         ge[q] = eq[q] = 0;
         if (cb < nch) {
             const TieRec t = tr[cb];
@@ -969,8 +1238,8 @@ __global__ __launch_bounds__(kFullBlock) void wide_ties_find_kernel(FullArgs a)
     }
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-        const int cb = tid * CPT + q;
+    for (int q = 0; q < kSelCPT; ++q) {
+        const int cb = tid * kSelCPT + q;
         if (run_ge < K && K <= run_ge + ge[q]) {
             sh.misc[0] = cb;
             sh.misc[1] = K - run_ge;
@@ -1079,13 +1348,16 @@ __global__ __launch_bounds__(64) void wide_replay_kernel(FullArgs a)
 
 /* ------------------------------------------------------------ 1: max */
 
+/* Wave w of workgroup g handles chunks (g*4 + w)*kFullCPW .. +kFullCPW-1 of
+ * its row; every chunk gets its record. */
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
 {
-    __shared__ Scratch sh;
-    const int tid = threadIdx.x;
-    const int row = blockIdx.y, b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.y;
+    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * kFullCPW;
     const int V = a.vocab;
+    if (cw >= a.nch) return;
     const RowIn ri = row_in(a, row);
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
@@ -1094,108 +1366,95 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
     const float T = ri.p.temperature;
     const int scale = (T > 0.0f) && (T != 1.0f);                       /* Model.pas:2703 */
     const float inv_t = scale ? div_cr32(1.0f, T) : 1.0f;              /* Model.pas:2705 */
+    const char* rowp = row_ptr<DT>(a, row);
+    FullChunk* rc = a.ws.chunks + (int64_t)row * a.ws.cstride;
 
-    uint32_t raw[kFullPer];
-    const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
-    const int nvalid = load16<DT>(row_ptr<DT>(a, row), e0, V, raw);
-    /* maxima as floats (the key of a float maximum is the maximum key: the
-     * order-preserving map identifies -0 and +0, as the comparisons do) */
-    float xm = -__builtin_inff(), am = 0.0f, ym = -__builtin_inff();
-    uint32_t fs = 0xFFFFFFFFu;
-    int ns = 0;
-    float ya[kFullPer];
-    bool part[kFullPer];
-    if (k.cls == kRowWide || nvalid < kFullPer) {
-#pragma unroll
-        for (int j = 0; j < kFullPer; ++j) {
-            const float xj = x_of<DT>(raw[j]);
-            part[j] = j < nvalid && takes_part(k, xj, e0 + j);
-            ya[j] = y_approx(xj, cap, inv_cap, scale, inv_t);
-            if (j < nvalid) xm = __builtin_fmaxf(xm, xj);
-            am = part[j] ? __builtin_fmaxf(am, __builtin_fabsf(xj)) : am;
-            ym = part[j] ? __builtin_fmaxf(ym, ya[j]) : ym;
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < kFullPer; ++j) {
-            const float xj = x_of<DT>(raw[j]);
-            part[j] = true;
-            xm = __builtin_fmaxf(xm, xj);
-            am = __builtin_fmaxf(am, __builtin_fabsf(xj));
-        }
-        if (cap > 0.0f && __ballot(am * inv_cap >= 0.1f) == 0) {
-            /* every |x/cap| < 0.1 in the wave: cap tanh(x/cap) = x - x^3/(3 cap^2)
-             * + O(x^5/cap^4), relative error < 1e-5 -- enough for predictions */
-            const float c3 = -(inv_cap * inv_cap) * (1.0f / 3.0f);
+    for (int q = 0; q < kFullCPW; ++q) {
+        const int b = cw + q;
+        if (b >= a.nch) break;
+        uint32_t raw[kFullPer];
+        const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
+        const int nvalid = load16<DT>(rowp, e0, V, raw);
+        /* maxima as floats (the key of a float maximum is the maximum key:
+         * the order-preserving map identifies -0 and +0, as the comparisons
+         * do) */
+        float xm = -__builtin_inff(), am = 0.0f, ym = -__builtin_inff();
+        uint32_t fs = 0xFFFFFFFFu;
+        int ns = 0;
+        float ya[kFullPer];
+        bool part[kFullPer];
+        if (k.cls == kRowWide || nvalid < kFullPer) {
 #pragma unroll
             for (int j = 0; j < kFullPer; ++j) {
                 const float xj = x_of<DT>(raw[j]);
-                float y = xj + xj * (xj * xj) * c3;
-                if (scale) y = y * inv_t;
-                ya[j] = y;
-                ym = __builtin_fmaxf(ym, y);
+                part[j] = j < nvalid && takes_part(k, xj, e0 + j);
+                ya[j] = y_approx(xj, cap, inv_cap, scale, inv_t);
+                if (j < nvalid) xm = __builtin_fmaxf(xm, xj);
+                am = part[j] ? __builtin_fmaxf(am, __builtin_fabsf(xj)) : am;
+                ym = part[j] ? __builtin_fmaxf(ym, ya[j]) : ym;
             }
         } else {
 #pragma unroll
             for (int j = 0; j < kFullPer; ++j) {
-                ya[j] = y_approx(x_of<DT>(raw[j]), cap, inv_cap, scale, inv_t);
-                ym = __builtin_fmaxf(ym, ya[j]);
+                const float xj = x_of<DT>(raw[j]);
+                part[j] = true;
+                xm = __builtin_fmaxf(xm, xj);
+                am = __builtin_fmaxf(am, __builtin_fabsf(xj));
+            }
+            if (cap > 0.0f && __ballot(am * inv_cap >= 0.1f) == 0) {
+                /* every |x/cap| < 0.1 in the wave: cap tanh(x/cap) = x -
+                 * x^3/(3 cap^2) + O(x^5/cap^4), relative error < 1e-5 --
+                 * enough for predictions */
+                const float c3 = -(inv_cap * inv_cap) * (1.0f / 3.0f);
+#pragma unroll
+                for (int j = 0; j < kFullPer; ++j) {
+                    const float xj = x_of<DT>(raw[j]);
+                    float y = __builtin_fmaf(xj * (xj * xj), c3, xj);
+                    if (scale) y = y * inv_t;
+                    ya[j] = y;
+                    ym = __builtin_fmaxf(ym, y);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < kFullPer; ++j) {
+                    ya[j] = y_approx(x_of<DT>(raw[j]), cap, inv_cap, scale, inv_t);
+                    ym = __builtin_fmaxf(ym, ya[j]);
+                }
             }
         }
-    }
-    if (k.cls == kRowWide) {
+        if (k.cls == kRowWide) {
 #pragma unroll
-        for (int j = 0; j < kFullPer; ++j) {
-            ns += part[j] ? 1 : 0;
-            fs = part[j] ? g4s_min_u(fs, (uint32_t)(e0 + j)) : fs;
+            for (int j = 0; j < kFullPer; ++j) {
+                ns += part[j] ? 1 : 0;
+                fs = part[j] ? g4s_min_u(fs, (uint32_t)(e0 + j)) : fs;
+            }
+        } else {
+            ns = nvalid;
+            fs = nvalid > 0 ? (uint32_t)e0 : fs;
         }
-    } else {
-        ns = nvalid;
-        fs = nvalid > 0 ? (uint32_t)e0 : fs;
-    }
-    uint32_t kmax = nvalid > 0 ? f2key(xm) : 0u;
-    uint32_t amax = __float_as_uint(am);
-    uint32_t ymk = f2key(ym);
-    /* the maxima in one LDS exchange */
-    {
-        const int lane = tid & 63, wid = tid >> 6;
-        kmax = wave_max_u32(kmax);
-        amax = wave_max_u32(amax);
-        ymk = wave_max_u32(ymk);
+        const uint32_t kmax = wave_max_u32(nvalid > 0 ? f2key(xm) : 0u);
+        const uint32_t amax = wave_max_u32(__float_as_uint(am));
+        const float ymax = key2f(wave_max_u32(f2key(ym)));
+        const float lg2e_ymax = ymax * 1.4426950408889634f;
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kFullPer; ++j)
+            if (part[j]) s += __builtin_amdgcn_exp2f(__builtin_fmaf(ya[j], 1.4426950408889634f, -lg2e_ymax));
+        s = wave_sum_f32(s);
+        ns = wave_sum_i32(ns);
+        fs = wave_min_u32(fs);
         if (lane == 0) {
-            sh.ured[wid] = kmax;
-            sh.ured[NWF + wid] = amax;
-            sh.ured[2 * NWF + wid] = ymk;
+            FullChunk r;
+            r.maxkey = kmax;
+            r.amax = amax;
+            r.ymax = ymax;
+            r.sapx = s;
+            r.nsurv = ns;
+            r.fsurv = fs == 0xFFFFFFFFu ? INT_MAX : (int32_t)fs;
+            r.soff = 0;
+            r.pad = 0;
+            rc[b] = r;
         }
-        __syncthreads();
-#pragma unroll
-        for (int w = 0; w < NWF; ++w) {
-            kmax = g4s_max_u(kmax, sh.ured[w]);
-            amax = g4s_max_u(amax, sh.ured[NWF + w]);
-            ymk = g4s_max_u(ymk, sh.ured[2 * NWF + w]);
-        }
-    }
-    const float ymax = key2f(ymk);
-    const float lg2e_ymax = ymax * 1.4426950408889634f;
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kFullPer; ++j)
-        if (part[j]) s += __builtin_amdgcn_exp2f(ya[j] * 1.4426950408889634f - lg2e_ymax);
-    s = wave_sum_f32(s);
-    if ((tid & 63) == 0) sh.fred[tid >> 6] = s;
-    ns = block_sum_int(ns, sh); /* its barriers also cover fred */
-    fs = block_min_u(fs, sh);
-    s = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NWF; ++w) s += sh.fred[w];
-    if (tid == 0) {
-        FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks + b;
-        rc->maxkey = kmax;
-        rc->amax = amax;
-        rc->ymax = ymax;
-        rc->sapx = s;
-        rc->nsurv = ns;
-        rc->fsurv = fs == 0xFFFFFFFFu ? INT_MAX : (int32_t)fs;
     }
 }
 
@@ -1204,7 +1463,7 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
 /* Every workgroup of a row reduces the chunk records to the row's m; for
  * bf16 logits workgroup g fills entries g*256 .. g*256+255 of the e table;
  * workgroup 0 also writes the row record, the predicted binades and the
- * survivor offsets. */
+ * survivor offsets (thread t handles chunks t*cpt .. t*cpt+cpt-1). */
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
 {
@@ -1215,15 +1474,12 @@ __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
     const int nch = a.nch;
-    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
+    const int cpt = (nch + kFullBlock - 1) / kFullBlock;
+    FullChunk* rc = a.ws.chunks + (int64_t)row * a.ws.cstride;
     uint32_t km = 0u, am = 0u;
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-        const int cb = tid * CPT + q;
-        if (cb < nch) {
-            km = g4s_max_u(km, rc[cb].maxkey);
-            am = g4s_max_u(am, rc[cb].amax);
-        }
+    for (int cb = tid; cb < nch; cb += kFullBlock) {
+        km = g4s_max_u(km, rc[cb].maxkey);
+        am = g4s_max_u(am, rc[cb].amax);
     }
     km = block_max_key(km, sh, 0);
     am = block_max_key(am, sh, 1);
@@ -1250,40 +1506,39 @@ __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
     /* predicted binade of LSum entering every chunk: exclusive prefix of the
      * chunk estimates (a prediction only: non-finite estimates add 0); the
      * survivor offsets and the first survivor */
-    double d[CPT];
-    int ns[CPT];
+    const auto est = [&](const FullChunk& c) {
+        double z = (double)c.ymax - (double)m;
+        z = z > 50.0 ? 50.0 : (z < -700.0 ? -700.0 : z);
+        const double v = (double)c.sapx * exp_fast_d(z);
+        return (v >= 0.0 && v < 1e300) ? v : 0.0;
+    };
     double tsum = 0.0;
     int tns = 0;
     uint32_t fs = 0xFFFFFFFFu;
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-        const int cb = tid * CPT + q;
-        d[q] = 0.0;
-        ns[q] = 0;
+    for (int q = 0; q < cpt; ++q) {
+        const int cb = tid * cpt + q;
         if (cb < nch) {
-            double z = (double)rc[cb].ymax - (double)m;
-            z = z > 50.0 ? 50.0 : (z < -700.0 ? -700.0 : z);
-            const double v = (double)rc[cb].sapx * exp_fast_d(z);
-            d[q] = (v >= 0.0 && v < 1e300) ? v : 0.0;
-            ns[q] = rc[cb].nsurv;
-            fs = g4s_min_u(fs, (uint32_t)rc[cb].fsurv);
+            const FullChunk c = rc[cb];
+            tsum += est(c);
+            tns += c.nsurv;
+            fs = g4s_min_u(fs, (uint32_t)c.fsurv);
         }
-        tsum += d[q];
-        tns += ns[q];
     }
+    const double total = block_sum_d(tsum, sh);
     double pre = block_excl_scan_d(tsum, sh);
     int count;
     int soff = block_excl_scan_i(tns, sh, count);
     fs = block_min_u(fs, sh);
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-        const int cb = tid * CPT + q;
+    int32_t* bl = a.ws.beta_l + (int64_t)row * a.ws.cstride;
+    for (int q = 0; q < cpt; ++q) {
+        const int cb = tid * cpt + q;
         if (cb < nch) {
-            rc[cb].beta_l = ss::state_of((float)pre).e;
+            const FullChunk c = rc[cb];
+            bl[cb] = ss::state_of((float)pre).e;
             rc[cb].soff = soff;
+            pre += est(c);
+            soff += c.nsurv;
         }
-        pre += d[q];
-        soff += ns[q];
     }
     if (tid == 0) {
         FullRow r;
@@ -1301,6 +1556,7 @@ __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
         r.nodraw = 0;
         r.count = count;
         r.first = (int32_t)fs;
+        r.beta_end = ss::state_of((float)total).e;
         for (int j = 0; j < kNear; ++j) r.near[j] = INT_MAX;
         r.l_reev = r.l_rounds = r.c_reev = r.c_rounds = 0;
         a.ws.rows[row] = r;
@@ -1310,27 +1566,38 @@ __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
 /* ------------------------------------------------- 3: lsum chunk maps */
 
 template <int DT>
+struct TabLds {
+    float tab[DT == 1 ? kFullTab : 1];
+};
+
+/* Each chunk's terms as one map of LSum in the chunk's predicted binade,
+ * one chunk per wave at a time; the first index of e == 1 and, on wide rows,
+ * of its near ties. */
+template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
 {
-    __shared__ TabShared<DT> sh;
-    const int tid = threadIdx.x;
+    __shared__ TabLds<DT> sh;
+    const int lane = threadIdx.x & 63;
     const int row = blockIdx.y;
     const int V = a.vocab;
+    const int nch = a.nch;
+    if ((int)blockIdx.x * NWF * kFullCPW >= nch) return;
     const RowIn ri = row_in(a, row);
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
     const char* rowp = row_ptr<DT>(a, row);
-    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
     FullRow* rr = a.ws.rows + row;
     const FullRow r = *rr;
     const Ctx c = make_ctx(a, r, k.cls);
     load_tab<DT>(a, row, r, sh.tab);
+    const int64_t rbase = (int64_t)row * a.ws.cstride;
+    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * kFullCPW;
 
     for (int q = 0; q < kFullCPW; ++q) {
-        const int b = blockIdx.x * kFullCPW + q;
-        if (b >= a.nch) break;
+        const int b = cw + q;
+        if (b >= nch) break;
         uint32_t raw[kFullPer];
-        const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
+        const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
         const int nvalid = load16<DT>(rowp, e0, V, raw);
         float t[kFullPer];
         terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t);                  /* Tensors.pas:660 */
@@ -1340,8 +1607,8 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
         float tmx = 0.0f;
 #pragma unroll
         for (int j = 0; j < kFullPer; ++j) tmx = __builtin_fmaxf(tmx, t[j]);
-        uint32_t first1 = 0xFFFFFFFFu;
         if (__ballot(tmx >= kNearLo)) {
+            uint32_t first1 = 0xFFFFFFFFu;
             uint32_t nearm = 0u;
 #pragma unroll
             for (int j = 0; j < kFullPer; ++j) {
@@ -1353,13 +1620,12 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
                     if (nearm & (1u << j))
                         atomicMin(&rr->near[(int)((1.0f - t[j]) * 0x1p24f)], (int32_t)(e0 + j));
             }
+            first1 = wave_min_u32(first1);
+            if (lane == 0 && first1 != 0xFFFFFFFFu) atomicMin(&rr->near[0], (int32_t)first1);
         }
-        const PMap cm = block_chunk_map(thread_map(t, nvalid, rc[b].beta_l), sh.s);
-        first1 = block_min_u(first1, sh.s);
-        if (tid == 0) {
-            rc[b].lmap = cm;
-            if (first1 != 0xFFFFFFFFu) atomicMin(&rr->near[0], (int32_t)first1);
-        }
+        const int32_t beta = a.ws.beta_l[rbase + b];
+        const PMap cm = wave_chunk_map(thread_map(t, nvalid, beta));
+        if (lane == 0) a.ws.lmap[rbase + b] = cm;
     }
 }
 
@@ -1367,58 +1633,43 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
 
 /* One workgroup per row: LSum by chaining the chunk maps left to right
  * (Tensors.pas:657-663; Model.pas:2794-2799), re-evaluating the chunks whose
- * map does not apply; then the argmax and the predictions for the draw. */
+ * map does not apply (the predicted binade crossings, staged in LDS by the
+ * whole workgroup; then wave 0 alone); then the argmax and the predictions
+ * for the draw. */
 template <int DT>
-__global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
+__global__ __launch_bounds__(kChainBlock) void full_lsum_chain_kernel(FullArgs a)
 {
-    __shared__ ChainShared<DT> sh;
-    const int tid = threadIdx.x;
+    extern __shared__ __align__(16) char dsm[];
+    __shared__ ChainScratch sh;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int row = blockIdx.y;
-    const int V = a.vocab;
     const RowIn ri = row_in(a, row);
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
     const char* rowp = row_ptr<DT>(a, row);
-    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
-    const FullRow r = a.ws.rows[row];
     const int nch = a.nch;
-    for (int cb = tid; cb < nch; cb += kFullBlock) {
-        sh.cmap[cb] = rc[cb].lmap;
-        sh.cbeta[cb] = rc[cb].beta_l;
-    }
-    if (tid == 0) sh.s.misc[12] = 0;
+    const int64_t rbase = (int64_t)row * a.ws.cstride;
+    const FullRow r = a.ws.rows[row];
+    const ChainLds L = chain_lds<DT>(dsm, nch, a.nstage);
+    const int32_t* gb = a.ws.beta_l + rbase;
+    const int32_t bend = r.beta_end;
     const Ctx c = make_ctx(a, r, k.cls);
-    load_tab<DT>(a, row, r, sh.tab); /* ends with a barrier */
+    chain_prologue<DT, false>(
+        a, row, r, c, k, a.ws.lmap + rbase, gb, nch - 1,
+        [&](int q) { return q == 0 || gb[q] != (q + 1 < nch ? gb[q + 1] : bend); }, L, sh);
+    if (tid >= 64) return;
 
-    uint32_t raw[kFullPer];
-    float t[kFullPer];
     State st = ss::state_of(0.0f);
-    int reev = 0;
+    int reev = 0, rounds = 0;
     for (int cb = 0; cb < nch;) {
         if (cb > 0) {
-            chain_maps(sh.cmap, sh.cbeta, cb, nch, st, __builtin_inff(), sh.s, sh.cpost);
-            st.e = sh.s.misc[9];
-            st.m = sh.s.misc[10];
-            cb = sh.s.misc[14];
-            __syncthreads();
+            cb = walk_maps<false>(L.cm, L.cb, cb, nch, st, 0.0f, L.cpost);
             if (cb >= nch) break;
         }
         ++reev;
-        const int64_t f0 = (int64_t)cb * kFullChunk + (int64_t)tid * kFullPer;
-        const int nv = load16<DT>(rowp, f0, V, raw);
-        terms_e<DT>(raw, nv, f0, c, k, sh.tab, t);
-        int pos = 0;
-        if (cb == 0) {
-            head_walk(t, __builtin_inff(), sh.s);
-            __syncthreads();
-            st.e = sh.s.misc[9];
-            st.m = sh.s.misc[10];
-            __syncthreads();
-            pos = kHead / kFullPer;
-        }
         int h;
-        st = resolve_chunk(t, nv, st, __builtin_inff(), pos, &h, sh.s);
-        if (tid == 0) sh.cpost[cb] = ss::value_of(st);
+        st = chain_chunk<DT, false>(a, rowp, cb, st, __builtin_inff(), L, c, k, r, &h, &rounds);
+        if (lane == 0) L.cpost[cb] = ss::value_of(st);
         ++cb;
     }
     const float lsum = ss::value_of(st);
@@ -1441,26 +1692,24 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
     /* fl32(u*TopP) <= 0: the first term's running sum already reaches it */
     const bool direct = !nodraw && !(thr > 0.0f);
     if ((nodraw || direct) && !all) {
-        if (tid < 64) {
-            uint32_t f = row_flags(k);
-            if (direct) f |= G4S_FLAG_DREW | G4S_FLAG_REACHED;
-            write_row_outputs(a, row, direct ? r.first : argmax, argmax, lsum, r.count, f);
-        }
+        uint32_t f = row_flags(k);
+        if (direct) f |= G4S_FLAG_DREW | G4S_FLAG_REACHED;
+        write_row_outputs(a, row, direct ? r.first : argmax, argmax, lsum, r.count, f);
         return;
     }
     /* predicted binade of the draw's running sum entering each chunk (the
      * exact LSum prefix before the chunk times 1/LSum), and the chunk where
      * it is predicted to reach thr (with margin) */
-    __syncthreads(); /* cpost complete */
     uint32_t last = (uint32_t)(nch - 1);
-    for (int cb = tid; cb < nch; cb += kFullBlock) {
-        const double pre = cb > 0 ? (double)sh.cpost[cb - 1] : 0.0;
-        const double post = (double)sh.cpost[cb];
-        rc[cb].beta_c = ss::state_of((float)(pre * (double)inv)).e;
+    int32_t* gbc = a.ws.beta_c + rbase;
+    for (int cb = lane; cb < nch; cb += 64) {
+        const double pre = cb > 0 ? (double)L.cpost[cb - 1] : 0.0;
+        const double post = (double)L.cpost[cb];
+        gbc[cb] = ss::state_of((float)(pre * (double)inv)).e;
         if (post * (double)inv >= (double)thr * (1.0 + 0x1p-10)) last = g4s_min_u(last, (uint32_t)cb);
     }
-    last = block_min_u(last, sh.s);
-    if (tid == 0) {
+    last = wave_min_u32(last);
+    if (lane == 0) {
         FullRow w = r;
         w.lsum = lsum;
         w.inv = inv;
@@ -1469,7 +1718,7 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
         w.c_last = (all || direct) ? nch - 1 : (int32_t)last;
         w.nodraw = nodraw ? 1 : (direct ? 2 : 0);
         w.l_reev = reev;
-        w.l_rounds = sh.s.misc[12];
+        w.l_rounds = rounds;
         w.c_reev = 0;
         w.c_rounds = 0;
         a.ws.rows[row] = w;
@@ -1481,26 +1730,28 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_chain_kernel(FullArgs a)
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
 {
-    __shared__ TabShared<DT> sh;
-    const int tid = threadIdx.x;
+    __shared__ TabLds<DT> sh;
+    const int lane = threadIdx.x & 63;
     const int row = blockIdx.y;
     const int V = a.vocab;
     const RowIn ri = row_in(a, row);
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
     const FullRow r = a.ws.rows[row];
-    if (r.c_last < 0 || (int)blockIdx.x * kFullCPW > r.c_last) return;
+    if (r.c_last < 0 || (int)blockIdx.x * NWF * kFullCPW > r.c_last) return;
     const char* rowp = row_ptr<DT>(a, row);
-    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
+    const int64_t rbase = (int64_t)row * a.ws.cstride;
+    const FullChunk* rc = a.ws.chunks + rbase;
     const Ctx c = make_ctx(a, r, k.cls);
     load_tab<DT>(a, row, r, sh.tab);
     const bool all = term_outputs(a, k.cls);
+    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * kFullCPW;
 
     for (int q = 0; q < kFullCPW; ++q) {
-        const int b = blockIdx.x * kFullCPW + q;
+        const int b = cw + q;
         if (b > r.c_last) break;
         uint32_t raw[kFullPer];
-        const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)tid * kFullPer;
+        const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
         const int nvalid = load16<DT>(rowp, e0, V, raw);
         float t[kFullPer];
         terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t);
@@ -1525,8 +1776,7 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
                     part[j] = j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j);
                     cnt += part[j] ? 1 : 0;
                 }
-                int tot;
-                int pos = rc[b].soff + block_excl_scan_i(cnt, sh.s, tot);
+                int pos = rc[b].soff + wave_inclusive_scan(cnt) - cnt;
 #pragma unroll
                 for (int j = 0; j < kFullPer; ++j)
                     if (part[j]) {
@@ -1539,8 +1789,8 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
             }
         }
         if (r.nodraw) continue;
-        const PMap cm = block_chunk_map(thread_map(t, nvalid, rc[b].beta_c), sh.s);
-        if (tid == 0) rc[b].cmap = cm;
+        const PMap cm = wave_chunk_map(thread_map(t, nvalid, a.ws.beta_c[rbase + b]));
+        if (lane == 0) a.ws.cmap[rbase + b] = cm;
     }
 }
 
@@ -1550,12 +1800,12 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
  * running sum of p reaches thr (Model.pas:2727-2735, 2811-2824), else the
  * argmax. */
 template <int DT>
-__global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
+__global__ __launch_bounds__(kChainBlock) void full_cdf_chain_kernel(FullArgs a)
 {
-    __shared__ ChainShared<DT> sh;
-    const int tid = threadIdx.x;
+    extern __shared__ __align__(16) char dsm[];
+    __shared__ ChainScratch sh;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int row = blockIdx.y;
-    const int V = a.vocab;
     const RowIn ri = row_in(a, row);
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
@@ -1573,61 +1823,36 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
         return;
     }
     const char* rowp = row_ptr<DT>(a, row);
-    FullChunk* rc = a.ws.chunks + (int64_t)row * kFullMaxChunks;
     const int nch = a.nch;
-    for (int cb = tid; cb < nch; cb += kFullBlock) {
-        sh.cmap[cb] = cb <= r.c_last ? rc[cb].cmap : ss::map_identity();
-        sh.cbeta[cb] = cb <= r.c_last ? rc[cb].beta_c : -1;
-    }
-    if (tid == 0) sh.s.misc[12] = 0;
+    const int64_t rbase = (int64_t)row * a.ws.cstride;
+    const ChainLds L = chain_lds<DT>(dsm, nch, a.nstage);
+    const int32_t* gb = a.ws.beta_c + rbase;
+    const int cl = r.c_last;
     const Ctx c = make_ctx(a, r, k.cls);
-    load_tab<DT>(a, row, r, sh.tab); /* ends with a barrier */
-    const float thr = r.thr;
+    chain_prologue<DT, true>(a, row, r, c, k, a.ws.cmap + rbase, gb, cl,
+                             [&](int q) { return q == 0 || q == cl || gb[q] != gb[q + 1]; }, L, sh);
+    if (tid >= 64) return;
 
-    uint32_t raw[kFullPer];
-    float t[kFullPer];
+    const float thr = r.thr;
     State st = ss::state_of(0.0f);
     int64_t hit = -1;
-    int reev = 0;
+    int reev = 0, rounds = 0;
     for (int cb = 0; cb < nch; ++cb) {
         if (cb > 0) {
-            chain_maps(sh.cmap, sh.cbeta, cb, nch, st, thr, sh.s, nullptr);
-            st.e = sh.s.misc[9];
-            st.m = sh.s.misc[10];
-            cb = sh.s.misc[14];
-            __syncthreads();
+            cb = walk_maps<true>(L.cm, L.cb, cb, nch, st, thr, nullptr);
             if (cb >= nch) break;
         }
         ++reev;
-        const int64_t f0 = (int64_t)cb * kFullChunk + (int64_t)tid * kFullPer;
-        const int nv = load16<DT>(rowp, f0, V, raw);
-        terms_e<DT>(raw, nv, f0, c, k, sh.tab, t);
-#pragma unroll
-        for (int j = 0; j < kFullPer; ++j) t[j] = p_of(t[j], k.cls, r.inv, r.lsum);
-        int pos = 0;
-        if (cb == 0) {
-            head_walk(t, thr, sh.s);
-            __syncthreads();
-            st.e = sh.s.misc[9];
-            st.m = sh.s.misc[10];
-            const int hh = sh.s.misc[11];
-            __syncthreads();
-            if (hh >= 0) {
-                hit = hh;
-                break;
-            }
-            pos = kHead / kFullPer;
-        }
         int h;
-        st = resolve_chunk(t, nv, st, thr, pos, &h, sh.s);
+        st = chain_chunk<DT, true>(a, rowp, cb, st, thr, L, c, k, r, &h, &rounds);
         if (h >= 0) {
             hit = (int64_t)cb * kFullChunk + h;
             break;
         }
     }
-    if (tid == 0) {
+    if (lane == 0) {
         a.ws.rows[row].c_reev = reev;
-        a.ws.rows[row].c_rounds = sh.s.misc[12];
+        a.ws.rows[row].c_rounds = rounds;
     }
     uint32_t flags = fl | G4S_FLAG_DREW;
     int32_t id = r.argmax;
@@ -1635,26 +1860,33 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_chain_kernel(FullArgs a)
         id = (int32_t)hit;
         flags |= G4S_FLAG_REACHED;
     }
-    if (tid < 64) write_row_outputs(a, row, id, r.argmax, r.lsum, r.count, flags);
+    write_row_outputs(a, row, id, r.argmax, r.lsum, r.count, flags);
 }
 
 /* ---------------------------------------------------------------- host */
 
 bool full_supported(int32_t vocab)
 {
-    return (vocab + kFullChunk - 1) / kFullChunk <= kFullMaxChunks;
+    return (vocab + kFullChunk - 1) / kFullChunk <= kFullMaxChunks &&
+           (vocab + kSelChunk - 1) / kSelChunk <= kSelMaxChunks;
 }
 
 hipError_t full_alloc(FullWorkspace& ws, int32_t vocab, int32_t max_batch)
 {
     const size_t mb = (size_t)max_batch;
     ws.bits_stride = (vocab + 31) / 32;
+    ws.cstride = (vocab + kFullChunk - 1) / kFullChunk;
+    const size_t nc = mb * (size_t)ws.cstride;
     hipError_t e = hipMalloc((void**)&ws.rows, mb * sizeof(FullRow));
-    if (e == hipSuccess) e = hipMalloc((void**)&ws.chunks, mb * kFullMaxChunks * sizeof(FullChunk));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.chunks, nc * sizeof(FullChunk));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.lmap, nc * sizeof(PMap));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.cmap, nc * sizeof(PMap));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.beta_l, nc * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.beta_c, nc * sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.etab, mb * kFullTab * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.sel, mb * sizeof(WideSel));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.hist, mb * kWideBins * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMalloc((void**)&ws.ties, mb * kFullMaxChunks * sizeof(TieRec));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.ties, mb * kSelMaxChunks * sizeof(TieRec));
     if (e == hipSuccess)
         e = hipMalloc((void**)&ws.bits, mb * (size_t)ws.bits_stride * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.heap_v, (size_t)vocab * sizeof(float));
@@ -1664,8 +1896,8 @@ hipError_t full_alloc(FullWorkspace& ws, int32_t vocab, int32_t max_batch)
 
 void full_free(FullWorkspace& ws)
 {
-    void* ptrs[] = {ws.rows, ws.chunks, ws.etab, ws.sel, ws.hist,
-                    ws.ties, ws.bits, ws.heap_v, ws.heap_i};
+    void* ptrs[] = {ws.rows, ws.chunks, ws.lmap, ws.cmap, ws.beta_l, ws.beta_c, ws.etab,
+                    ws.sel, ws.hist, ws.ties, ws.bits, ws.heap_v, ws.heap_i};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     ws = FullWorkspace{};
@@ -1676,29 +1908,77 @@ hipError_t full_init(FullWorkspace& ws, int32_t max_batch, hipStream_t s)
     return hipMemsetAsync(ws.hist, 0, (size_t)max_batch * kWideBins * sizeof(uint32_t), s);
 }
 
+/* Chunks the chains precompute: kStageMax when the LDS allows, fewer on a
+ * device with less LDS per workgroup (then the chains re-evaluate more from
+ * the logits).  Raises the launch limit for dynamic LDS beyond 64 KiB once
+ * per kernel. */
 template <int DT>
-static hipError_t launch_dt(const FullArgs& a, hipStream_t s)
+static int chain_nstage(int nch, size_t* lds)
 {
-    const dim3 grid((unsigned)a.nch, (unsigned)a.batch);
+    static int limit = -1;
+    static bool raised = false;
+    if (limit < 0) {
+        int dev = 0, v = 65536;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            v = 65536;
+        (void)hipGetLastError();
+        limit = v;
+    }
+    size_t off[7];
+    int ns = kStageMax;
+    for (; ns > 0; --ns) {
+        *lds = chain_lds_layout(DT, nch, ns, off);
+        if (*lds + sizeof(ChainScratch) <= (size_t)limit) break;
+    }
+    *lds = chain_lds_layout(DT, nch, ns, off);
+    if (*lds > 65536 && !raised) {
+        const int want = limit - (int)sizeof(ChainScratch);
+        hipError_t e = hipFuncSetAttribute((const void*)full_lsum_chain_kernel<DT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, want);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)full_cdf_chain_kernel<DT>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, want);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            limit = 65536; /* stay within the default */
+            for (ns = kStageMax; ns > 0; --ns) {
+                *lds = chain_lds_layout(DT, nch, ns, off);
+                if (*lds + sizeof(ChainScratch) <= (size_t)limit) break;
+            }
+            *lds = chain_lds_layout(DT, nch, ns, off);
+        }
+        raised = true;
+    }
+    return ns;
+}
+
+template <int DT>
+static hipError_t launch_dt(const FullArgs& a0, hipStream_t s)
+{
+    FullArgs a = a0;
+    size_t lds = 0;
+    a.nstage = chain_nstage<DT>(a.nch, &lds);
+    const dim3 sel((unsigned)a.nsel, (unsigned)a.batch);
     const dim3 rows(1u, (unsigned)a.batch);
-    const dim3 grid4((unsigned)((a.nch + kFullCPW - 1) / kFullCPW), (unsigned)a.batch);
+    const dim3 waves((unsigned)((a.nch + NWF * kFullCPW - 1) / (NWF * kFullCPW)), (unsigned)a.batch);
     if (a.wide_on) {
         for (int pass = 0; pass < 3; ++pass) {
-            hipLaunchKernelGGL((wide_hist_kernel<DT>), grid, dim3(kFullBlock), 0, s, a, pass);
+            hipLaunchKernelGGL((wide_hist_kernel<DT>), sel, dim3(kFullBlock), 0, s, a, pass);
             hipLaunchKernelGGL(wide_find_kernel, rows, dim3(kFullBlock), 0, s, a, pass);
         }
-        hipLaunchKernelGGL((wide_ties_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
+        hipLaunchKernelGGL((wide_ties_kernel<DT>), sel, dim3(kFullBlock), 0, s, a);
         hipLaunchKernelGGL((wide_ties_find_kernel<DT>), rows, dim3(kFullBlock), 0, s, a);
         hipLaunchKernelGGL((wide_replay_kernel<DT>), dim3(1), dim3(64), 0, s, a);
     }
-    hipLaunchKernelGGL((full_max_kernel<DT>), grid, dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_max_kernel<DT>), waves, dim3(kFullBlock), 0, s, a);
     hipLaunchKernelGGL((full_row_kernel<DT>),
                        dim3(DT == 1 ? (unsigned)(kFullTab / kFullBlock) : 1u, (unsigned)a.batch),
                        dim3(kFullBlock), 0, s, a);
-    hipLaunchKernelGGL((full_lsum_kernel<DT>), grid4, dim3(kFullBlock), 0, s, a);
-    hipLaunchKernelGGL((full_lsum_chain_kernel<DT>), rows, dim3(kFullBlock), 0, s, a);
-    hipLaunchKernelGGL((full_cdf_kernel<DT>), grid4, dim3(kFullBlock), 0, s, a);
-    hipLaunchKernelGGL((full_cdf_chain_kernel<DT>), rows, dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_lsum_kernel<DT>), waves, dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_lsum_chain_kernel<DT>), rows, dim3(kChainBlock), lds, s, a);
+    hipLaunchKernelGGL((full_cdf_kernel<DT>), waves, dim3(kFullBlock), 0, s, a);
+    hipLaunchKernelGGL((full_cdf_chain_kernel<DT>), rows, dim3(kChainBlock), lds, s, a);
     return hipGetLastError();
 }
 

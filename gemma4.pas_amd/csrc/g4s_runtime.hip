@@ -178,6 +178,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         f.u0 = u0;
         f.softcap = s->softcap;
         f.nch = (s->vocab + g4s::kFullChunk - 1) / g4s::kFullChunk;
+        f.nsel = (s->vocab + g4s::kSelChunk - 1) / g4s::kSelChunk;
         f.wide_on = wide ? 1 : 0;
         f.ws = s->full;
         f.ids = d_ids;

@@ -157,6 +157,41 @@ G4S_SS_HD PMap map_sat(PMap f)
     return r;
 }
 
+/* The map of a run of n terms in binade e in one pass over the terms.
+ * A term q = a/u = k + f adds k + (f > 1/2) units unless f == 1/2 (a
+ * half-unit tie), where it adds k or k + 1, whichever makes the sum even.
+ * The running parity chain that starts even gives d0.  The chain that starts
+ * odd adds the same units up to the first tie (only ties depend on parity),
+ * rounds that tie the other way, and from there on both sums are even and
+ * identical: d1 = d0 + 1 when the even chain rounds its first tie down,
+ * d0 - 1 when it rounds it up, d0 without a tie.  Each d_p is exact when the
+ * true value is below kTop and at least kTop otherwise (q is clamped at
+ * 2^25, where a term alone leaves the binade, and d0 at 2^26). */
+G4S_SS_HD PMap lane_map(const float* t, int n, int32_t e)
+{
+    int32_t D = 0, P = 0, delta = 0;
+    bool seen = false;
+    for (int j = 0; j < n; ++j) {
+        float q = __builtin_ldexpf(t[j], 150 - e);
+        q = q < 33554432.0f ? q : 33554432.0f;
+        const float fl = __builtin_floorf(q);
+        const float fr = q - fl;
+        const int32_t fi = (int32_t)fl;
+        const bool tie = fr == 0.5f;
+        const int32_t x = (P ^ fi) & 1;
+        const int32_t a = fi + (tie ? x : (fr > 0.5f ? 1 : 0));
+        delta = (tie && !seen) ? 1 - 2 * x : delta;
+        seen = seen || tie;
+        D += a;
+        D = D > (1 << 26) ? (1 << 26) : D;
+        P = (P ^ a) & 1;
+    }
+    PMap r;
+    r.d0 = D;
+    r.d1 = D + delta;
+    return r;
+}
+
 /* One reference step, S <- RN32(S + a), on a state (exact by definition). */
 G4S_SS_HD State step_add(State st, float a)
 {

@@ -169,6 +169,59 @@ int64_t ss_check_term_ct_f(uint64_t seed, int64_t n)
     return bad;
 }
 
+/* lane_map against the literal loop: runs of 16 terms in binade e (unit
+ * fractions with few bits, forced half-unit ties, zeros, terms that alone
+ * leave the binade), each applied literally from an even and an odd entering
+ * significand.  Where the literal sum stays in the binade the map must give
+ * its significand exactly; where it leaves, the map's result must be >= 2^24.
+ * Also against the composition of per-term maps. */
+int64_t ss_check_lane_map(uint64_t seed, int64_t n)
+{
+    Rng r{seed};
+    int64_t bad = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t e = 30 + (int32_t)(r.next() % 170);
+        const int len = 1 + (int)(r.next() % 16);
+        float t[16];
+        const int mode = (int)(r.next() % 4);
+        for (int j = 0; j < len; ++j) {
+            double q;
+            const uint64_t z = r.next();
+            if ((z & 7) == 0) {
+                q = 0.0;
+            } else if ((z & 7) == 1) {
+                q = (double)(r.next() % 4096) + 0.5;                 /* a tie */
+            } else if (mode == 3 && (z & 15) == 2) {
+                q = 16777216.0 + (double)(r.next() % 1000);          /* leaves alone */
+            } else {
+                const int bits = 1 + (int)(r.next() % 12);           /* fraction bits */
+                const double scale = mode == 0 ? 4096.0 : (mode == 1 ? 64.0 : 1048576.0);
+                q = std::floor(r.unif() * scale * (double)(1 << bits)) / (double)(1 << bits);
+            }
+            t[j] = (float)std::ldexp(q, e - 150);
+        }
+        const PMap f = lane_map(t, len, e);
+        PMap g = map_identity();
+        for (int j = 0; j < len; ++j) g = map_sat(map_then(g, map_of_ct(term_ct(t[j], e))));
+        for (int p = 0; p < 2; ++p) {
+            const int32_t gd = p ? g.d1 : g.d0, fd = p ? f.d1 : f.d0;
+            if ((gd < kTop || fd < kTop) && gd != fd) ++bad;
+            /* literal from M = 2^23 + something of parity p */
+            const int32_t m0 = (int32_t)((0x800000u + (uint32_t)(r.next() % 0x7FFFFEu)) & ~1u) | p;
+            float sum = value_of(State{e, m0});
+            for (int j = 0; j < len; ++j) sum = sum + t[j];
+            const State s2 = state_of(sum);
+            const int32_t got = m0 + fd;
+            if (s2.e == e) {
+                if (got != s2.m) ++bad;
+            } else if (got < kTop) {
+                ++bad;
+            }
+        }
+    }
+    return bad;
+}
+
 /* Associativity of map composition over random term maps. */
 int64_t ss_check_assoc(uint64_t seed, int64_t n)
 {

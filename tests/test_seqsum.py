@@ -22,6 +22,8 @@ def ss():
     L.ss_check_steps.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     L.ss_check_term_ct_f.restype = ctypes.c_int64
     L.ss_check_term_ct_f.argtypes = [ctypes.c_uint64, ctypes.c_int64]
+    L.ss_check_lane_map.restype = ctypes.c_int64
+    L.ss_check_lane_map.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     L.ss_check_assoc.restype = ctypes.c_int64
     L.ss_check_assoc.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     L.ss_check_sequence.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
@@ -39,6 +41,13 @@ def test_float_term_classification_matches_integer(ss):
     the integer form, for random terms including subnormals, in every
     binade near the term's own and in random binades."""
     assert ss.ss_check_term_ct_f(7, 300_000) == 0
+
+
+def test_lane_map_matches_literal_loop(ss):
+    """The single-pass lane map (parity chain with the first-tie offset)
+    against the literal binary32 loop from even and odd entering sums, and
+    against the composition of per-term maps."""
+    assert ss.ss_check_lane_map(11, 400_000) == 0
 
 
 def test_composition_associative(ss):
