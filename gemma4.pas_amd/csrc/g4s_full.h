@@ -98,7 +98,10 @@ struct FullWorkspace {
     ss::PMap* cmap = nullptr;    /* [max_batch][cstride] chunk's p in beta_c */
     int32_t* beta_l = nullptr;   /* [max_batch][cstride] predicted binade of LSum entering */
     int32_t* beta_c = nullptr;   /* [max_batch][cstride] same for the draw's running sum */
-    float* etab = nullptr;       /* [max_batch][kFullTab] */
+    float* etab = nullptr;       /* [max_batch][kFullTab] e of the tabulated bf16 codes */
+    float* ptab = nullptr;       /* [max_batch][kFullTab] p of the same codes */
+    uint64_t* tmask = nullptr;   /* [max_batch][2] binades where a table e ([0]) or p
+                                    ([1]) is a half-unit tie (64-binade windows) */
     /* wide rows */
     WideSel* sel = nullptr;      /* [max_batch] */
     uint32_t* hist = nullptr;    /* [max_batch][kWideBins], zero between launches */

@@ -251,6 +251,7 @@ constexpr uint32_t kTabMiss = 0x7800u;
 struct Ctx {
     float cap, inv_cap, inv_t, m;
     int scale, win_lo, cls;
+    float inv, lsum; /* for p (after the LSum chain) */
 };
 
 /* e of one term evaluated from x (kept out of line: it is the rare case for
@@ -260,12 +261,26 @@ __device__ __noinline__ float e_direct(float x, Ctx c)
     return exp_diff_cr32(y_exact(x, c.cls, c.cap, c.inv_cap, c.scale, c.inv_t), c.m);
 }
 
-/* The e of one thread's 16 terms (0 for terms that do not take part).  For
- * bf16 logits every term reads the table (a clamped index, no branch); the
- * rare codes outside its window are evaluated afterwards, behind one
- * wave-uniform branch. */
-template <int DT, bool GENERAL>
-__device__ __forceinline__ void terms_e_t(const uint32_t (&raw)[kFullPer], int nvalid,
+/* p of one term from its e: RN32(e * fl32(1/LSum)) on a full row
+ * (Tensors.pas:666-672), RN32(e / LSum) on a wide row (Model.pas:2800-2801). */
+__device__ __forceinline__ float p_of(float e, int cls, float inv, float lsum)
+{
+    return cls == kRowWide ? div_cr32(e, lsum) : e * inv;
+}
+
+/* p of one term evaluated from x (out of line, as e_direct). */
+__device__ __noinline__ float p_direct(float x, Ctx c)
+{
+    return p_of(e_direct(x, c), c.cls, c.inv, c.lsum);
+}
+
+/* The e of one lane's 16 terms (0 for terms that do not take part), or,
+ * with P, their p (the table then holds p).  For bf16 logits every term
+ * reads the table (no branch); the rare codes outside its window are
+ * evaluated afterwards, behind one wave-uniform branch.  Returns true when
+ * every term of the wave came from the table. */
+template <int DT, bool GENERAL, bool P>
+__device__ __forceinline__ bool terms_e_t(const uint32_t (&raw)[kFullPer], int nvalid,
                                           int64_t e0, const Ctx& c, const Mask& k,
                                           const float* tab, float (&t)[kFullPer])
 {
@@ -281,40 +296,33 @@ __device__ __forceinline__ void terms_e_t(const uint32_t (&raw)[kFullPer], int n
             t[j] = part[j] ? v : 0.0f;
             anymiss |= part[j] ? (d & kTabMiss) : 0u;
         }
-        if (__ballot(anymiss != 0u)) {
+        if (__ballot(anymiss != 0u) == 0) return true;
 #pragma unroll
-            for (int j = 0; j < kFullPer; ++j) {
-                uint32_t d;
-                (void)tab_index(raw[j], base, d);
-                if (part[j] && (d & kTabMiss) != 0u) t[j] = e_direct(x_of<DT>(raw[j]), c);
-            }
+        for (int j = 0; j < kFullPer; ++j) {
+            uint32_t d;
+            (void)tab_index(raw[j], base, d);
+            if (part[j] && (d & kTabMiss) != 0u)
+                t[j] = P ? p_direct(x_of<DT>(raw[j]), c) : e_direct(x_of<DT>(raw[j]), c);
         }
-        return;
+        return false;
     }
 #pragma unroll
     for (int j = 0; j < kFullPer; ++j) {
         const bool part = GENERAL ? (j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j)) : true;
-        t[j] = part ? e_direct(x_of<DT>(raw[j]), c) : 0.0f;
+        t[j] = part ? (P ? p_direct(x_of<DT>(raw[j]), c) : e_direct(x_of<DT>(raw[j]), c)) : 0.0f;
     }
+    return false;
 }
 
 /* Whole chunks of full rows (the common case) skip the per-term mask. */
-template <int DT>
-__device__ __forceinline__ void terms_e(const uint32_t (&raw)[kFullPer], int nvalid, int64_t e0,
+template <int DT, bool P = false>
+__device__ __forceinline__ bool terms_e(const uint32_t (&raw)[kFullPer], int nvalid, int64_t e0,
                                         const Ctx& c, const Mask& k, const float* tab,
                                         float (&t)[kFullPer])
 {
     if (k.cls == kRowWide || nvalid < kFullPer)
-        terms_e_t<DT, true>(raw, nvalid, e0, c, k, tab, t);
-    else
-        terms_e_t<DT, false>(raw, nvalid, e0, c, k, tab, t);
-}
-
-/* p of one term from its e: RN32(e * fl32(1/LSum)) on a full row
- * (Tensors.pas:666-672), RN32(e / LSum) on a wide row (Model.pas:2800-2801). */
-__device__ __forceinline__ float p_of(float e, int cls, float inv, float lsum)
-{
-    return cls == kRowWide ? div_cr32(e, lsum) : e * inv;
+        return terms_e_t<DT, true, P>(raw, nvalid, e0, c, k, tab, t);
+    return terms_e_t<DT, false, P>(raw, nvalid, e0, c, k, tab, t);
 }
 
 /* ------------------------------------------------------ block helpers */
@@ -479,6 +487,56 @@ __device__ __forceinline__ PMap thread_map(const float (&t)[kFullPer], int nvali
         return f;
     }
     return ss::lane_map(t, kFullPer, e);
+}
+
+/* The lane map without the tie vote, for waves whose terms are known to
+ * hold no half-unit tie in binade e (every term tabulated, and the row's
+ * tie mask clear for e). */
+__device__ __forceinline__ PMap thread_map_nt(const float (&t)[kFullPer], int32_t e)
+{
+    float cs = 0.0f;
+    const int sh = 150 - e;
+#pragma unroll
+    for (int j = 0; j < kFullPer; ++j) cs += __builtin_rintf(__builtin_ldexpf(t[j], sh));
+    PMap f;
+    f.d0 = f.d1 = (int32_t)__builtin_fminf(cs, 67108864.0f);
+    return f;
+}
+
+/* A value v > 0 is a half-unit tie in binade E (fract(v / 2^(E-150)) ==
+ * 1/2) exactly when its lowest set bit is 2^(E-151), E = (lowest set bit's
+ * exponent) + 151.  A row's tie mask records, for the 64 binades from `base`
+ * on, whether a value of its table is a tie there; binades outside the
+ * window count as possible ties. */
+constexpr int kTieBaseE = 120; /* LSum >= 1: binades 127 and up */
+constexpr int kTieBaseP = 72;  /* running sums of p <= 1: binades up to 127 */
+
+/* The 64-bit window mask of one value (0: no tie inside the window). */
+__device__ __forceinline__ uint64_t tie_bits(float v, int base)
+{
+    const uint32_t b = __float_as_uint(v);
+    const int ef = (int)(b >> 23);
+    const uint32_t sig = (b & 0x7FFFFFu) | (ef ? 0x800000u : 0u);
+    const int E = (ef ? ef : 1) + (int)__builtin_ctz(sig | 0x1000000u) + 1 - base;
+    return (b != 0u && (unsigned)E < 64u) ? (1ull << E) : 0ull;
+}
+
+__device__ __forceinline__ bool tie_possible(uint64_t mask, int base, int32_t e)
+{
+    const int i = e - base;
+    return (unsigned)i >= 64u || ((mask >> i) & 1ull) != 0ull;
+}
+
+/* OR over the wave of a 64-bit value (every lane gets it). */
+__device__ __forceinline__ uint64_t wave_or64(uint64_t v)
+{
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        lo |= (uint32_t)__shfl_xor((int)lo, o, 64);
+        hi |= (uint32_t)__shfl_xor((int)hi, o, 64);
+    }
+    return ((uint64_t)hi << 32) | lo;
 }
 
 /* ------------------------------------------------------- wave helpers */
@@ -740,11 +798,8 @@ __device__ __forceinline__ int chain_load_terms(const FullArgs& a, const char* r
     uint32_t raw[kFullPer];
     const int64_t e0 = (int64_t)c * kFullChunk + (int64_t)lane * kFullPer;
     const int nv = load16<DT>(rowp, e0, a.vocab, raw);
-    terms_e<DT>(raw, nv, e0, ctx, k, tab, t);
-    if (P) {
-#pragma unroll
-        for (int j = 0; j < kFullPer; ++j) t[j] = p_of(t[j], k.cls, r.inv, r.lsum);
-    }
+    (void)r;
+    terms_e<DT, P>(raw, nv, e0, ctx, k, tab, t);
     return nv;
 }
 
@@ -765,6 +820,10 @@ static_assert(kStageMax % kChainWaves == 0, "staged chunks per wave");
 
 struct ChainScratch {
     int32_t iscan[kChainWaves];
+    uint32_t lastw[kChainWaves];
+    uint32_t pm[2];
+    float lsum, inv;
+    int32_t argmax, reev, rounds;
 };
 
 /* Exclusive prefix over the chain workgroup in thread order (ints). */
@@ -795,7 +854,8 @@ __device__ void chain_prologue(const FullArgs& a, int row, const FullRow& r, con
     const int V = a.vocab;
     const int nstage = a.nstage;
     if (DT == 1 && r.win_lo >= 0) {
-        const float4* src = reinterpret_cast<const float4*>(a.ws.etab + (int64_t)row * kFullTab);
+        const float4* src =
+            reinterpret_cast<const float4*>((P ? a.ws.ptab : a.ws.etab) + (int64_t)row * kFullTab);
         reinterpret_cast<float4*>(L.tab)[tid] = src[tid]; /* kFullTab / 4 == kChainBlock */
     }
     for (int c = tid; c < nch; c += kChainBlock) {
@@ -864,11 +924,7 @@ __device__ void chain_prologue(const FullArgs& a, int row, const FullRow& r, con
         }
         float t[kFullPer];
         const int64_t e0 = (int64_t)c * kFullChunk + (int64_t)lane * kFullPer;
-        terms_e<DT>(raw, kFullPer, e0, ctx, k, L.tab, t);
-        if (P) {
-#pragma unroll
-            for (int j = 0; j < kFullPer; ++j) t[j] = p_of(t[j], k.cls, r.inv, r.lsum);
-        }
+        terms_e<DT, P>(raw, kFullPer, e0, ctx, k, L.tab, t);
         float4* dst = reinterpret_cast<float4*>(L.tv + (size_t)sl * kFullChunk + lane * kFullPer);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -983,15 +1039,17 @@ __device__ __forceinline__ Ctx make_ctx(const FullArgs& a, const FullRow& r, int
     c.scale = r.scale;
     c.win_lo = r.win_lo;
     c.cls = cls;
+    c.inv = r.inv;
+    c.lsum = r.lsum;
     return c;
 }
 
 /* Copy the row's e table into LDS (ends with a barrier). */
 template <int DT>
-__device__ __forceinline__ void load_tab(const FullArgs& a, int row, const FullRow& r, float* tab)
+__device__ __forceinline__ void load_tab(const float* gtab, int row, const FullRow& r, float* tab)
 {
     if (DT == 1 && r.win_lo >= 0) {
-        const float4* src = reinterpret_cast<const float4*>(a.ws.etab + (int64_t)row * kFullTab);
+        const float4* src = reinterpret_cast<const float4*>(gtab + (int64_t)row * kFullTab);
         float4 v[kFullTab / 4 / kFullBlock];
 #pragma unroll
         for (int q = 0; q < kFullTab / 4 / kFullBlock; ++q) v[q] = src[threadIdx.x + q * kFullBlock];
@@ -1368,6 +1426,7 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
     const float inv_t = scale ? div_cr32(1.0f, T) : 1.0f;              /* Model.pas:2705 */
     const char* rowp = row_ptr<DT>(a, row);
     FullChunk* rc = a.ws.chunks + (int64_t)row * a.ws.cstride;
+    if (cw == 0 && lane < 2) a.ws.tmask[(int64_t)row * 2 + lane] = 0ull; /* for the row kernel */
 
     for (int q = 0; q < kFullCPW; ++q) {
         const int b = cw + q;
@@ -1378,12 +1437,18 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
         /* maxima as floats (the key of a float maximum is the maximum key:
          * the order-preserving map identifies -0 and +0, as the comparisons
          * do) */
-        float xm = -__builtin_inff(), am = 0.0f, ym = -__builtin_inff();
-        uint32_t fs = 0xFFFFFFFFu;
-        int ns = 0;
-        float ya[kFullPer];
-        bool part[kFullPer];
-        if (k.cls == kRowWide || nvalid < kFullPer) {
+        uint32_t kmax, amax;
+        float ymax, s = 0.0f;
+        uint32_t fs;
+        int ns;
+        /* wave-uniform: the branches hold wave reductions */
+        const bool whole = k.cls != kRowWide && (int64_t)(b + 1) * kFullChunk <= V;
+        if (!whole) {
+            float xm = -__builtin_inff(), am = 0.0f, ym = -__builtin_inff();
+            float ya[kFullPer];
+            bool part[kFullPer];
+            fs = 0xFFFFFFFFu;
+            ns = 0;
 #pragma unroll
             for (int j = 0; j < kFullPer; ++j) {
                 const float xj = x_of<DT>(raw[j]);
@@ -1392,57 +1457,55 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
                 if (j < nvalid) xm = __builtin_fmaxf(xm, xj);
                 am = part[j] ? __builtin_fmaxf(am, __builtin_fabsf(xj)) : am;
                 ym = part[j] ? __builtin_fmaxf(ym, ya[j]) : ym;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < kFullPer; ++j) {
-                const float xj = x_of<DT>(raw[j]);
-                part[j] = true;
-                xm = __builtin_fmaxf(xm, xj);
-                am = __builtin_fmaxf(am, __builtin_fabsf(xj));
-            }
-            if (cap > 0.0f && __ballot(am * inv_cap >= 0.1f) == 0) {
-                /* every |x/cap| < 0.1 in the wave: cap tanh(x/cap) = x -
-                 * x^3/(3 cap^2) + O(x^5/cap^4), relative error < 1e-5 --
-                 * enough for predictions */
-                const float c3 = -(inv_cap * inv_cap) * (1.0f / 3.0f);
-#pragma unroll
-                for (int j = 0; j < kFullPer; ++j) {
-                    const float xj = x_of<DT>(raw[j]);
-                    float y = __builtin_fmaf(xj * (xj * xj), c3, xj);
-                    if (scale) y = y * inv_t;
-                    ya[j] = y;
-                    ym = __builtin_fmaxf(ym, y);
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < kFullPer; ++j) {
-                    ya[j] = y_approx(x_of<DT>(raw[j]), cap, inv_cap, scale, inv_t);
-                    ym = __builtin_fmaxf(ym, ya[j]);
-                }
-            }
-        }
-        if (k.cls == kRowWide) {
-#pragma unroll
-            for (int j = 0; j < kFullPer; ++j) {
                 ns += part[j] ? 1 : 0;
                 fs = part[j] ? g4s_min_u(fs, (uint32_t)(e0 + j)) : fs;
             }
-        } else {
-            ns = nvalid;
-            fs = nvalid > 0 ? (uint32_t)e0 : fs;
-        }
-        const uint32_t kmax = wave_max_u32(nvalid > 0 ? f2key(xm) : 0u);
-        const uint32_t amax = wave_max_u32(__float_as_uint(am));
-        const float ymax = key2f(wave_max_u32(f2key(ym)));
-        const float lg2e_ymax = ymax * 1.4426950408889634f;
-        float s = 0.0f;
+            kmax = wave_max_u32(nvalid > 0 ? f2key(xm) : 0u);
+            amax = wave_max_u32(__float_as_uint(am));
+            ymax = key2f(wave_max_u32(f2key(ym)));
+            const float lg2e_ymax = ymax * 1.4426950408889634f;
 #pragma unroll
-        for (int j = 0; j < kFullPer; ++j)
-            if (part[j]) s += __builtin_amdgcn_exp2f(__builtin_fmaf(ya[j], 1.4426950408889634f, -lg2e_ymax));
+            for (int j = 0; j < kFullPer; ++j)
+                if (part[j])
+                    s += __builtin_amdgcn_exp2f(__builtin_fmaf(ya[j], 1.4426950408889634f, -lg2e_ymax));
+            ns = wave_sum_i32(ns);
+            fs = wave_min_u32(fs);
+        } else {
+            /* a whole chunk of a full row: every term takes part, and the
+             * approximate y is monotone in x, so its maximum is y(max x) */
+            float xa[kFullPer];
+            float xm = -__builtin_inff(), xn = __builtin_inff();
+#pragma unroll
+            for (int j = 0; j < kFullPer; ++j) xa[j] = x_of<DT>(raw[j]);
+#pragma unroll
+            for (int j = 0; j < kFullPer; j += 2) {
+                xm = __builtin_fmaxf(xm, __builtin_fmaxf(xa[j], xa[j + 1]));
+                xn = __builtin_fminf(xn, __builtin_fminf(xa[j], xa[j + 1]));
+            }
+            kmax = wave_max_u32(f2key(xm));
+            amax = wave_max_u32(__float_as_uint(__builtin_fmaxf(__builtin_fabsf(xm),
+                                                                __builtin_fabsf(xn))));
+            const float xmax = key2f(kmax);
+            /* every |x/cap| < 0.1: cap tanh(x/cap) = x - x^3/(3 cap^2) +
+             * O(x^5/cap^4), relative error < 1e-5 -- enough for predictions */
+            const bool cubic = cap > 0.0f && __uint_as_float(amax) * inv_cap < 0.1f;
+            const float c3 = -(inv_cap * inv_cap) * (1.0f / 3.0f);
+            const auto yap = [&](float x) {
+                if (cubic) {
+                    const float y = __builtin_fmaf(x * (x * x), c3, x);
+                    return scale ? y * inv_t : y;
+                }
+                return y_approx(x, cap, inv_cap, scale, inv_t);
+            };
+            ymax = yap(xmax);
+            const float lg2e_ymax = ymax * 1.4426950408889634f;
+#pragma unroll
+            for (int j = 0; j < kFullPer; ++j)
+                s += __builtin_amdgcn_exp2f(__builtin_fmaf(yap(xa[j]), 1.4426950408889634f, -lg2e_ymax));
+            ns = kFullChunk;
+            fs = (uint32_t)((int64_t)b * kFullChunk);
+        }
         s = wave_sum_f32(s);
-        ns = wave_sum_i32(ns);
-        fs = wave_min_u32(fs);
         if (lane == 0) {
             FullChunk r;
             r.maxkey = kmax;
@@ -1498,8 +1561,12 @@ __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
         const uint32_t ebi = (uint32_t)win + (((uint32_t)i >> 7) & 15u);
         const uint32_t code = (((uint32_t)i >> 11) << 15) | (ebi << 7) | ((uint32_t)i & 0x7Fu);
         const float x = __uint_as_float(code << 16);
-        a.ws.etab[(int64_t)row * kFullTab + i] =
-            exp_diff_cr32(y_exact(x, k.cls, cap, inv_cap, scale, inv_t), m);
+        const float ev = exp_diff_cr32(y_exact(x, k.cls, cap, inv_cap, scale, inv_t), m);
+        a.ws.etab[(int64_t)row * kFullTab + i] = ev;
+        /* the binades in which a table value is a half-unit tie */
+        const uint64_t tb = wave_or64(tie_bits(ev, kTieBaseE));
+        if ((tid & 63) == 0 && tb != 0ull)
+            atomicOr((unsigned long long*)&a.ws.tmask[(int64_t)row * 2], (unsigned long long)tb);
     }
     if (g != 0) return;
 
@@ -1589,9 +1656,10 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
     FullRow* rr = a.ws.rows + row;
     const FullRow r = *rr;
     const Ctx c = make_ctx(a, r, k.cls);
-    load_tab<DT>(a, row, r, sh.tab);
+    load_tab<DT>(a.ws.etab, row, r, sh.tab);
     const int64_t rbase = (int64_t)row * a.ws.cstride;
     const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * kFullCPW;
+    const uint64_t tm = a.ws.tmask[(int64_t)row * 2];
 
     for (int q = 0; q < kFullCPW; ++q) {
         const int b = cw + q;
@@ -1600,7 +1668,7 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
         const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
         const int nvalid = load16<DT>(rowp, e0, V, raw);
         float t[kFullPer];
-        terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t);                  /* Tensors.pas:660 */
+        const bool tabbed = terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t); /* Tensors.pas:660 */
         /* the terms with e = 1 - jj*2^-24, jj < kNear (the row maximum and
          * its near ties): looked at only in waves that hold one */
         constexpr float kNearLo = 1.0f - (float)(kNear - 1) * 0x1p-24f;
@@ -1624,7 +1692,9 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
             if (lane == 0 && first1 != 0xFFFFFFFFu) atomicMin(&rr->near[0], (int32_t)first1);
         }
         const int32_t beta = a.ws.beta_l[rbase + b];
-        const PMap cm = wave_chunk_map(thread_map(t, nvalid, beta));
+        const PMap cm = wave_chunk_map(tabbed && !tie_possible(tm, kTieBaseE, beta)
+                                           ? thread_map_nt(t, beta)
+                                           : thread_map(t, nvalid, beta));
         if (lane == 0) a.ws.lmap[rbase + b] = cm;
     }
 }
@@ -1654,71 +1724,108 @@ __global__ __launch_bounds__(kChainBlock) void full_lsum_chain_kernel(FullArgs a
     const int32_t* gb = a.ws.beta_l + rbase;
     const int32_t bend = r.beta_end;
     const Ctx c = make_ctx(a, r, k.cls);
+    if (tid < 2) sh.pm[tid] = 0u;
     chain_prologue<DT, false>(
         a, row, r, c, k, a.ws.lmap + rbase, gb, nch - 1,
         [&](int q) { return q == 0 || gb[q] != (q + 1 < nch ? gb[q + 1] : bend); }, L, sh);
-    if (tid >= 64) return;
-
-    State st = ss::state_of(0.0f);
-    int reev = 0, rounds = 0;
-    for (int cb = 0; cb < nch;) {
-        if (cb > 0) {
-            cb = walk_maps<false>(L.cm, L.cb, cb, nch, st, 0.0f, L.cpost);
-            if (cb >= nch) break;
-        }
-        ++reev;
-        int h;
-        st = chain_chunk<DT, false>(a, rowp, cb, st, __builtin_inff(), L, c, k, r, &h, &rounds);
-        if (lane == 0) L.cpost[cb] = ss::value_of(st);
-        ++cb;
-    }
-    const float lsum = ss::value_of(st);
-    const float inv = div_cr32(1.0f, lsum);                            /* Tensors.pas:668 */
-    /* argmax of p.  Full row: p = fl32(e * inv) <= inv with equality exactly
-     * at e == 1 (the next float below 1 gives a p below inv), so the first
-     * e == 1.  Wide row: p = fl32(e / LSum) can also equal fl32(1 / LSum) for
-     * e = 1 - j*2^-24 with small j (never for j >= kNear): the first index
-     * among the values whose quotient ties (Model.pas:2804-2807). */
-    int32_t argmax = r.near[0];
-    if (k.cls == kRowWide) {
-        for (int j = 1; j < kNear; ++j)
-            if (r.near[j] < argmax && div_cr32(1.0f - (float)j * 0x1p-24f, lsum) == inv)
-                argmax = r.near[j];
-    }
+    /* the draw's settings (every wave: they decide whether the others wait
+     * for the chain) */
     const float T = ri.p.temperature;
     const bool all = term_outputs(a, k.cls);
     const bool nodraw = !(T > 0.0f);
     const float thr = nodraw ? __builtin_inff() : mul_u_p_cr32(ri.u, ri.p.top_p); /* :2726 */
     /* fl32(u*TopP) <= 0: the first term's running sum already reaches it */
     const bool direct = !nodraw && !(thr > 0.0f);
-    if ((nodraw || direct) && !all) {
-        uint32_t f = row_flags(k);
-        if (direct) f |= G4S_FLAG_DREW | G4S_FLAG_REACHED;
-        write_row_outputs(a, row, direct ? r.first : argmax, argmax, lsum, r.count, f);
-        return;
+    const bool early = (nodraw || direct) && !all;
+    if (tid >= 64 && early) return;
+
+    if (tid < 64) {
+        State st = ss::state_of(0.0f);
+        int reev = 0, rounds = 0;
+        for (int cb = 0; cb < nch;) {
+            if (cb > 0) {
+                cb = walk_maps<false>(L.cm, L.cb, cb, nch, st, 0.0f, L.cpost);
+                if (cb >= nch) break;
+            }
+            ++reev;
+            int h;
+            st = chain_chunk<DT, false>(a, rowp, cb, st, __builtin_inff(), L, c, k, r, &h, &rounds);
+            if (lane == 0) L.cpost[cb] = ss::value_of(st);
+            ++cb;
+        }
+        const float lsum = ss::value_of(st);
+        const float inv = div_cr32(1.0f, lsum);                        /* Tensors.pas:668 */
+        /* argmax of p.  Full row: p = fl32(e * inv) <= inv with equality
+         * exactly at e == 1 (the next float below 1 gives a p below inv), so
+         * the first e == 1.  Wide row: p = fl32(e / LSum) can also equal
+         * fl32(1 / LSum) for e = 1 - j*2^-24 with small j (never for j >=
+         * kNear): the first index among the values whose quotient ties
+         * (Model.pas:2804-2807). */
+        int32_t argmax = r.near[0];
+        if (k.cls == kRowWide) {
+            for (int j = 1; j < kNear; ++j)
+                if (r.near[j] < argmax && div_cr32(1.0f - (float)j * 0x1p-24f, lsum) == inv)
+                    argmax = r.near[j];
+        }
+        if (early) {
+            uint32_t f = row_flags(k);
+            if (direct) f |= G4S_FLAG_DREW | G4S_FLAG_REACHED;
+            write_row_outputs(a, row, direct ? r.first : argmax, argmax, lsum, r.count, f);
+            return;
+        }
+        if (lane == 0) {
+            sh.lsum = lsum;
+            sh.inv = inv;
+            sh.argmax = argmax;
+            sh.reev = reev;
+            sh.rounds = rounds;
+        }
+    }
+    __syncthreads();
+    const float lsum = sh.lsum, inv = sh.inv;
+    /* the p table (Tensors.pas:666-672; Model.pas:2800-2801 on wide rows)
+     * and the binades where one of its values is a half-unit tie */
+    if (DT == 1 && r.win_lo >= 0) {
+        const float4 e4 = reinterpret_cast<const float4*>(L.tab)[tid];
+        float4 p4;
+        p4.x = p_of(e4.x, k.cls, inv, lsum);
+        p4.y = p_of(e4.y, k.cls, inv, lsum);
+        p4.z = p_of(e4.z, k.cls, inv, lsum);
+        p4.w = p_of(e4.w, k.cls, inv, lsum);
+        reinterpret_cast<float4*>(a.ws.ptab + (int64_t)row * kFullTab)[tid] = p4;
+        const uint64_t tb = wave_or64(tie_bits(p4.x, kTieBaseP) | tie_bits(p4.y, kTieBaseP) |
+                                      tie_bits(p4.z, kTieBaseP) | tie_bits(p4.w, kTieBaseP));
+        if (lane == 0 && tb != 0ull) {
+            atomicOr(&sh.pm[0], (uint32_t)tb);
+            atomicOr(&sh.pm[1], (uint32_t)(tb >> 32));
+        }
     }
     /* predicted binade of the draw's running sum entering each chunk (the
      * exact LSum prefix before the chunk times 1/LSum), and the chunk where
      * it is predicted to reach thr (with margin) */
     uint32_t last = (uint32_t)(nch - 1);
     int32_t* gbc = a.ws.beta_c + rbase;
-    for (int cb = lane; cb < nch; cb += 64) {
+    for (int cb = tid; cb < nch; cb += kChainBlock) {
         const double pre = cb > 0 ? (double)L.cpost[cb - 1] : 0.0;
         const double post = (double)L.cpost[cb];
         gbc[cb] = ss::state_of((float)(pre * (double)inv)).e;
         if (post * (double)inv >= (double)thr * (1.0 + 0x1p-10)) last = g4s_min_u(last, (uint32_t)cb);
     }
     last = wave_min_u32(last);
-    if (lane == 0) {
+    if (lane == 0) sh.lastw[tid >> 6] = last;
+    __syncthreads();
+    if (tid == 0) a.ws.tmask[(int64_t)row * 2 + 1] = ((uint64_t)sh.pm[1] << 32) | sh.pm[0];
+    if (tid == 0) {
+        for (int w = 0; w < kChainWaves; ++w) last = g4s_min_u(last, sh.lastw[w]);
         FullRow w = r;
         w.lsum = lsum;
         w.inv = inv;
         w.thr = thr;
-        w.argmax = argmax;
+        w.argmax = sh.argmax;
         w.c_last = (all || direct) ? nch - 1 : (int32_t)last;
         w.nodraw = nodraw ? 1 : (direct ? 2 : 0);
-        w.l_reev = reev;
-        w.l_rounds = rounds;
+        w.l_reev = sh.reev;
+        w.l_rounds = sh.rounds;
         w.c_reev = 0;
         w.c_rounds = 0;
         a.ws.rows[row] = w;
@@ -1743,9 +1850,10 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
     const int64_t rbase = (int64_t)row * a.ws.cstride;
     const FullChunk* rc = a.ws.chunks + rbase;
     const Ctx c = make_ctx(a, r, k.cls);
-    load_tab<DT>(a, row, r, sh.tab);
+    load_tab<DT>(a.ws.ptab, row, r, sh.tab);
     const bool all = term_outputs(a, k.cls);
     const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * kFullCPW;
+    const uint64_t tm = a.ws.tmask[(int64_t)row * 2 + 1];
 
     for (int q = 0; q < kFullCPW; ++q) {
         const int b = cw + q;
@@ -1754,9 +1862,7 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
         const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
         const int nvalid = load16<DT>(rowp, e0, V, raw);
         float t[kFullPer];
-        terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t);
-#pragma unroll
-        for (int j = 0; j < kFullPer; ++j) t[j] = p_of(t[j], k.cls, r.inv, r.lsum);
+        const bool tabbed = terms_e<DT, true>(raw, nvalid, e0, c, k, sh.tab, t);
         if (all) {
             float* po = a.out.probs ? a.out.probs + (int64_t)row * a.out.capacity : nullptr;
             int32_t* io = a.out.indices ? a.out.indices + (int64_t)row * a.out.capacity : nullptr;
@@ -1789,7 +1895,10 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
             }
         }
         if (r.nodraw) continue;
-        const PMap cm = wave_chunk_map(thread_map(t, nvalid, a.ws.beta_c[rbase + b]));
+        const int32_t beta = a.ws.beta_c[rbase + b];
+        const PMap cm = wave_chunk_map(tabbed && !tie_possible(tm, kTieBaseP, beta)
+                                           ? thread_map_nt(t, beta)
+                                           : thread_map(t, nvalid, beta));
         if (lane == 0) a.ws.cmap[rbase + b] = cm;
     }
 }
@@ -1884,6 +1993,8 @@ hipError_t full_alloc(FullWorkspace& ws, int32_t vocab, int32_t max_batch)
     if (e == hipSuccess) e = hipMalloc((void**)&ws.beta_l, nc * sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.beta_c, nc * sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.etab, mb * kFullTab * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.ptab, mb * kFullTab * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void**)&ws.tmask, mb * 2 * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.sel, mb * sizeof(WideSel));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.hist, mb * kWideBins * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc((void**)&ws.ties, mb * kSelMaxChunks * sizeof(TieRec));
@@ -1896,7 +2007,7 @@ hipError_t full_alloc(FullWorkspace& ws, int32_t vocab, int32_t max_batch)
 
 void full_free(FullWorkspace& ws)
 {
-    void* ptrs[] = {ws.rows, ws.chunks, ws.lmap, ws.cmap, ws.beta_l, ws.beta_c, ws.etab,
+    void* ptrs[] = {ws.rows, ws.chunks, ws.lmap, ws.cmap, ws.beta_l, ws.beta_c, ws.etab, ws.ptab, ws.tmask,
                     ws.sel, ws.hist, ws.ties, ws.bits, ws.heap_v, ws.heap_i};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -1905,7 +2016,8 @@ void full_free(FullWorkspace& ws)
 
 hipError_t full_init(FullWorkspace& ws, int32_t max_batch, hipStream_t s)
 {
-    return hipMemsetAsync(ws.hist, 0, (size_t)max_batch * kWideBins * sizeof(uint32_t), s);
+    hipError_t e = hipMemsetAsync(ws.hist, 0, (size_t)max_batch * kWideBins * sizeof(uint32_t), s);
+    return e;
 }
 
 /* Chunks the chains precompute: kStageMax when the LDS allows, fewer on a
@@ -1915,38 +2027,43 @@ hipError_t full_init(FullWorkspace& ws, int32_t max_batch, hipStream_t s)
 template <int DT>
 static int chain_nstage(int nch, size_t* lds)
 {
-    static int limit = -1;
+    static int limit = -1;    /* dynamic LDS the chain kernels may use */
     static bool raised = false;
     if (limit < 0) {
         int dev = 0, v = 65536;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
             v = 65536;
+        /* less the chain kernels' static LDS (as allocated, padding included) */
+        size_t st = 0;
+        hipFuncAttributes fa;
+        if (hipFuncGetAttributes(&fa, (const void*)full_lsum_chain_kernel<DT>) == hipSuccess)
+            st = fa.sharedSizeBytes;
+        if (hipFuncGetAttributes(&fa, (const void*)full_cdf_chain_kernel<DT>) == hipSuccess &&
+            fa.sharedSizeBytes > st)
+            st = fa.sharedSizeBytes;
         (void)hipGetLastError();
-        limit = v;
+        limit = v - (int)((st + 255) & ~(size_t)255);
     }
-    size_t off[7];
-    int ns = kStageMax;
-    for (; ns > 0; --ns) {
+    const auto fit = [&](int lim) {
+        size_t off[7];
+        int ns = kStageMax;
+        for (; ns > 0; --ns)
+            if (chain_lds_layout(DT, nch, ns, off) <= (size_t)lim) break;
         *lds = chain_lds_layout(DT, nch, ns, off);
-        if (*lds + sizeof(ChainScratch) <= (size_t)limit) break;
-    }
-    *lds = chain_lds_layout(DT, nch, ns, off);
+        return ns;
+    };
+    int ns = fit(limit);
     if (*lds > 65536 && !raised) {
-        const int want = limit - (int)sizeof(ChainScratch);
         hipError_t e = hipFuncSetAttribute((const void*)full_lsum_chain_kernel<DT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, want);
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, limit);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)full_cdf_chain_kernel<DT>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, want);
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, limit);
         if (e != hipSuccess) {
             (void)hipGetLastError();
-            limit = 65536; /* stay within the default */
-            for (ns = kStageMax; ns > 0; --ns) {
-                *lds = chain_lds_layout(DT, nch, ns, off);
-                if (*lds + sizeof(ChainScratch) <= (size_t)limit) break;
-            }
-            *lds = chain_lds_layout(DT, nch, ns, off);
+            limit = 65536 - 1024; /* stay within the default */
+            ns = fit(limit);
         }
         raised = true;
     }
