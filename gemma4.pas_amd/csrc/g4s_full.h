@@ -15,7 +15,6 @@ constexpr int kFullBlock = 256;                     /* threads of the streaming 
 constexpr int kFullPer = 16;                        /* consecutive terms per lane */
 constexpr int kFullChunk = 64 * kFullPer;           /* terms per chunk: one wave's 1024 */
 constexpr int kFullMaxChunks = 4096;                /* chunks per row: vocab <= 2^22 */
-constexpr int kFullCPW = 4;                         /* chunks per wave, streaming passes */
 constexpr int kFullTab = 4096;                      /* bf16 codes with a tabulated e */
 constexpr int kNear = 8;  /* e = 1 - j*2^-24 (j < kNear): the values whose p can tie the
                              largest p under the top-k tail's division */
@@ -126,6 +125,7 @@ struct FullArgs {
     int32_t nch;      /* chunks of kFullChunk terms per row */
     int32_t nsel;     /* chunks of kSelChunk terms per row (wide select) */
     int32_t nstage;   /* chunks each chain precomputes (set by full_launch) */
+    int32_t cpw;      /* chunks per wave of the streaming passes (set by full_launch) */
     int32_t wide_on;  /* wide rows are handled by this launch */
     FullWorkspace ws;
     int32_t* ids;

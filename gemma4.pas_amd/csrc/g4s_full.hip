@@ -24,10 +24,11 @@
  * and the first survivor as the draw when fl32(u * TopP) <= 0.
  *
  * Rows are cut into chunks of 1024 terms, one wave's: 16 consecutive terms
- * per lane.  The streaming passes give every wave kFullCPW chunks and use
- * no barrier beyond loading the e table; the two chains are one workgroup
- * per row whose wave 0 walks the row.  Launches (the wide ones only when
- * wide rows can occur; they cut rows into 4096-term select chunks):
+ * per lane.  The streaming passes give every wave a run of consecutive
+ * chunks and use no barrier beyond loading the e table; the two chains are
+ * one workgroup per row whose wave 0 walks the row.  Launches (the wide
+ * ones only when wide rows can occur; they cut rows into 4096-term select
+ * chunks):
  *   wide hist/find x3: 11+11+10-bit MSD radix select of tau (LDS
  *             histograms added into a per-row histogram, one workgroup per
  *             row fixes each digit);
@@ -1406,16 +1407,17 @@ __global__ __launch_bounds__(64) void wide_replay_kernel(FullArgs a)
 
 /* ------------------------------------------------------------ 1: max */
 
-/* Wave w of workgroup g handles chunks (g*4 + w)*kFullCPW .. +kFullCPW-1 of
- * its row; every chunk gets its record. */
+/* Wave w of workgroup g handles chunks (g*4 + w)*cpw .. +cpw-1 of its row;
+ * every chunk gets its record. */
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
 {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.y;
-    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * kFullCPW;
+    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * a.cpw;
     const int V = a.vocab;
     if (cw >= a.nch) return;
+    const int bend = cw + a.cpw < a.nch ? cw + a.cpw : a.nch;
     const RowIn ri = row_in(a, row);
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
@@ -1428,9 +1430,7 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
     FullChunk* rc = a.ws.chunks + (int64_t)row * a.ws.cstride;
     if (cw == 0 && lane < 2) a.ws.tmask[(int64_t)row * 2 + lane] = 0ull; /* for the row kernel */
 
-    for (int q = 0; q < kFullCPW; ++q) {
-        const int b = cw + q;
-        if (b >= a.nch) break;
+    for (int b = cw; b < bend; ++b) {
         uint32_t raw[kFullPer];
         const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
         const int nvalid = load16<DT>(rowp, e0, V, raw);
@@ -1524,9 +1524,13 @@ __global__ __launch_bounds__(kFullBlock) void full_max_kernel(FullArgs a)
 /* ------------------------------------------------------------ 2: row */
 
 /* Every workgroup of a row reduces the chunk records to the row's m; for
- * bf16 logits workgroup g fills entries g*256 .. g*256+255 of the e table;
- * workgroup 0 also writes the row record, the predicted binades and the
- * survivor offsets (thread t handles chunks t*cpt .. t*cpt+cpt-1). */
+ * bf16 logits workgroup g fills entries g*1024 .. g*1024+1023 of the e
+ * table (kRowPer per thread: four workgroups per row launch far faster than
+ * sixteen); workgroup 0 also writes the row record, the predicted binades
+ * and the survivor offsets (thread t handles chunks t*cpt .. t*cpt+cpt-1). */
+constexpr int kRowPer = 4; /* e-table entries per thread of the row kernel */
+static_assert(kFullTab % (kFullBlock * kRowPer) == 0, "whole workgroups of table entries");
+
 template <int DT>
 __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
 {
@@ -1557,14 +1561,18 @@ __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
     if (DT == 1) {
         const int eb = (int)((am >> 23) & 0xFFu);
         win = eb - 15 < 0 ? 0 : eb - 15;
-        const int i = g * kFullBlock + tid;
-        const uint32_t ebi = (uint32_t)win + (((uint32_t)i >> 7) & 15u);
-        const uint32_t code = (((uint32_t)i >> 11) << 15) | (ebi << 7) | ((uint32_t)i & 0x7Fu);
-        const float x = __uint_as_float(code << 16);
-        const float ev = exp_diff_cr32(y_exact(x, k.cls, cap, inv_cap, scale, inv_t), m);
-        a.ws.etab[(int64_t)row * kFullTab + i] = ev;
+        uint64_t tb = 0ull;
+        for (int s = 0; s < kRowPer; ++s) {
+            const int i = (g * kRowPer + s) * kFullBlock + tid;
+            const uint32_t ebi = (uint32_t)win + (((uint32_t)i >> 7) & 15u);
+            const uint32_t code = (((uint32_t)i >> 11) << 15) | (ebi << 7) | ((uint32_t)i & 0x7Fu);
+            const float x = __uint_as_float(code << 16);
+            const float ev = exp_diff_cr32(y_exact(x, k.cls, cap, inv_cap, scale, inv_t), m);
+            a.ws.etab[(int64_t)row * kFullTab + i] = ev;
+            tb |= tie_bits(ev, kTieBaseE);
+        }
         /* the binades in which a table value is a half-unit tie */
-        const uint64_t tb = wave_or64(tie_bits(ev, kTieBaseE));
+        tb = wave_or64(tb);
         if ((tid & 63) == 0 && tb != 0ull)
             atomicOr((unsigned long long*)&a.ws.tmask[(int64_t)row * 2], (unsigned long long)tb);
     }
@@ -1648,7 +1656,7 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
     const int row = blockIdx.y;
     const int V = a.vocab;
     const int nch = a.nch;
-    if ((int)blockIdx.x * NWF * kFullCPW >= nch) return;
+    if ((int)blockIdx.x * NWF * a.cpw >= nch) return;
     const RowIn ri = row_in(a, row);
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
@@ -1658,12 +1666,14 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
     const Ctx c = make_ctx(a, r, k.cls);
     load_tab<DT>(a.ws.etab, row, r, sh.tab);
     const int64_t rbase = (int64_t)row * a.ws.cstride;
-    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * kFullCPW;
+    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * a.cpw;
+    const int bend = cw + a.cpw < nch ? cw + a.cpw : nch;
     const uint64_t tm = a.ws.tmask[(int64_t)row * 2];
+    /* the predicted binades of the wave's chunks in one load (lane q: chunk
+     * cw + q) */
+    const int32_t betas = cw + lane < bend ? a.ws.beta_l[rbase + cw + lane] : 0;
 
-    for (int q = 0; q < kFullCPW; ++q) {
-        const int b = cw + q;
-        if (b >= nch) break;
+    for (int b = cw; b < bend; ++b) {
         uint32_t raw[kFullPer];
         const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
         const int nvalid = load16<DT>(rowp, e0, V, raw);
@@ -1691,7 +1701,7 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
             first1 = wave_min_u32(first1);
             if (lane == 0 && first1 != 0xFFFFFFFFu) atomicMin(&rr->near[0], (int32_t)first1);
         }
-        const int32_t beta = a.ws.beta_l[rbase + b];
+        const int32_t beta = __builtin_amdgcn_readlane(betas, b - cw);
         const PMap cm = wave_chunk_map(tabbed && !tie_possible(tm, kTieBaseE, beta)
                                            ? thread_map_nt(t, beta)
                                            : thread_map(t, nvalid, beta));
@@ -1845,19 +1855,22 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
     const FullRow r = a.ws.rows[row];
-    if (r.c_last < 0 || (int)blockIdx.x * NWF * kFullCPW > r.c_last) return;
+    if (r.c_last < 0 || (int)blockIdx.x * NWF * a.cpw > r.c_last) return;
     const char* rowp = row_ptr<DT>(a, row);
     const int64_t rbase = (int64_t)row * a.ws.cstride;
     const FullChunk* rc = a.ws.chunks + rbase;
     const Ctx c = make_ctx(a, r, k.cls);
     load_tab<DT>(a.ws.ptab, row, r, sh.tab);
     const bool all = term_outputs(a, k.cls);
-    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * kFullCPW;
+    const int cw = (blockIdx.x * NWF + (threadIdx.x >> 6)) * a.cpw;
+    const int bend = cw + a.cpw <= r.c_last ? cw + a.cpw : r.c_last + 1;
     const uint64_t tm = a.ws.tmask[(int64_t)row * 2 + 1];
+    /* per-chunk inputs up front (lane q: chunk cw + q) */
+    const bool mine = cw + lane < bend;
+    const int32_t betas = mine ? a.ws.beta_c[rbase + cw + lane] : 0;
+    const int32_t soffs = (mine && all && k.cls != kRowFull) ? rc[cw + lane].soff : 0;
 
-    for (int q = 0; q < kFullCPW; ++q) {
-        const int b = cw + q;
-        if (b > r.c_last) break;
+    for (int b = cw; b < bend; ++b) {
         uint32_t raw[kFullPer];
         const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
         const int nvalid = load16<DT>(rowp, e0, V, raw);
@@ -1882,7 +1895,7 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
                     part[j] = j < nvalid && takes_part(k, x_of<DT>(raw[j]), e0 + j);
                     cnt += part[j] ? 1 : 0;
                 }
-                int pos = rc[b].soff + wave_inclusive_scan(cnt) - cnt;
+                int pos = __builtin_amdgcn_readlane(soffs, b - cw) + wave_inclusive_scan(cnt) - cnt;
 #pragma unroll
                 for (int j = 0; j < kFullPer; ++j)
                     if (part[j]) {
@@ -1895,7 +1908,7 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
             }
         }
         if (r.nodraw) continue;
-        const int32_t beta = a.ws.beta_c[rbase + b];
+        const int32_t beta = __builtin_amdgcn_readlane(betas, b - cw);
         const PMap cm = wave_chunk_map(tabbed && !tie_possible(tm, kTieBaseP, beta)
                                            ? thread_map_nt(t, beta)
                                            : thread_map(t, nvalid, beta));
@@ -2070,15 +2083,28 @@ static int chain_nstage(int nch, size_t* lds)
     return ns;
 }
 
+/* Chunks per wave of the streaming passes: 4 (the fastest run length on the
+ * B=256 batch) unless that leaves fewer than 16384 waves, then fewer, down
+ * to 1, so that small batches spread over the chip.  At most 64: a wave's
+ * per-chunk inputs are read with one lane per chunk. */
+static int stream_cpw(int nch, int batch)
+{
+    const int64_t chunks = (int64_t)nch * batch;
+    int cpw = 4;
+    while (cpw > 1 && chunks / cpw < 16384) cpw >>= 1;
+    return cpw;
+}
+
 template <int DT>
 static hipError_t launch_dt(const FullArgs& a0, hipStream_t s)
 {
     FullArgs a = a0;
     size_t lds = 0;
     a.nstage = chain_nstage<DT>(a.nch, &lds);
+    a.cpw = stream_cpw(a.nch, a.batch);
     const dim3 sel((unsigned)a.nsel, (unsigned)a.batch);
     const dim3 rows(1u, (unsigned)a.batch);
-    const dim3 waves((unsigned)((a.nch + NWF * kFullCPW - 1) / (NWF * kFullCPW)), (unsigned)a.batch);
+    const dim3 waves((unsigned)((a.nch + NWF * a.cpw - 1) / (NWF * a.cpw)), (unsigned)a.batch);
     if (a.wide_on) {
         for (int pass = 0; pass < 3; ++pass) {
             hipLaunchKernelGGL((wide_hist_kernel<DT>), sel, dim3(kFullBlock), 0, s, a, pass);
@@ -2090,7 +2116,8 @@ static hipError_t launch_dt(const FullArgs& a0, hipStream_t s)
     }
     hipLaunchKernelGGL((full_max_kernel<DT>), waves, dim3(kFullBlock), 0, s, a);
     hipLaunchKernelGGL((full_row_kernel<DT>),
-                       dim3(DT == 1 ? (unsigned)(kFullTab / kFullBlock) : 1u, (unsigned)a.batch),
+                       dim3(DT == 1 ? (unsigned)(kFullTab / (kFullBlock * kRowPer)) : 1u,
+                            (unsigned)a.batch),
                        dim3(kFullBlock), 0, s, a);
     hipLaunchKernelGGL((full_lsum_kernel<DT>), waves, dim3(kFullBlock), 0, s, a);
     hipLaunchKernelGGL((full_lsum_chain_kernel<DT>), rows, dim3(kChainBlock), lds, s, a);

@@ -493,9 +493,11 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
                 v[i] = ld_dev(&rcand[f < span ? f : span - 1]);
             }
         }
-        int cnt = 0;
+        uint32_t km = 0u; /* bit i: slot i is kept (one evaluation per slot) */
 #pragma unroll
-        for (int i = 0; i < kBatchLoads; ++i) cnt += keep(b0 + tid + i * BLOCK, v[i]);
+        for (int i = 0; i < kBatchLoads; ++i)
+            km |= (uint32_t)keep(b0 + tid + i * BLOCK, v[i]) << i;
+        const int cnt = __popc(km);
         const int incl = wave_inclusive_scan(cnt);
         int base = 0;
         if (lane == 63) base = atomicAdd(&sh.misc[1], incl);
@@ -503,7 +505,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         int pos = base + incl - cnt;
 #pragma unroll
         for (int i = 0; i < kBatchLoads; ++i) {
-            if (keep(b0 + tid + i * BLOCK, v[i])) {
+            if ((km >> i) & 1u) {
                 if (pos < MCAP)
                     sh.mc[pos] = v[i];
                 else
