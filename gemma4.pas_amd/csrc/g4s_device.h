@@ -213,12 +213,15 @@ __device__ __forceinline__ int wave_sum_i32(int v)
     return __builtin_amdgcn_readlane(v, 63);
 }
 
-/* The k1-th and k2-th largest (1 <= k <= 64; 0 for k outside that range) of
- * one uint32 per lane (all 64 lanes active), in one MSB-first ballot
- * search.  Each result P is the largest value with #{lanes: v >= P} >= k
- * (0 when no positive value qualifies); uniform. */
-__device__ __forceinline__ void wave_kth_largest2(uint32_t v, int k1, int k2, uint32_t& r1,
-                                                  uint32_t& r2)
+/* Lower bounds of the k1-th and k2-th largest (1 <= k <= 64; 0 for k
+ * outside that range) of one uint32 per lane (all 64 lanes active), in one
+ * MSB-first ballot search over the `bits` bits below the common prefix of
+ * the wave's values.  Each result P is the largest value whose bits below
+ * those are zero with #{lanes: v >= P} >= k, so at least k lanes hold a
+ * value >= P (0 when no positive value qualifies); with bits >= 32 P is the
+ * k-th largest itself.  Uniform. */
+__device__ __forceinline__ void wave_kth_largest2(uint32_t v, int k1, int k2, int bits,
+                                                  uint32_t& r1, uint32_t& r2)
 {
     /* both results lie in [min v, max v]: their bits above the highest bit
      * in which min and max differ are the common prefix */
@@ -227,8 +230,9 @@ __device__ __forceinline__ void wave_kth_largest2(uint32_t v, int k1, int k2, ui
     const uint32_t pre = top < 0 ? hi : (top >= 31 ? 0u : (hi & ~((2u << top) - 1u)));
     uint32_t p1 = pre, p2 = pre;
     const bool on1 = k1 >= 1 && k1 <= 64, on2 = k2 >= 1 && k2 <= 64;
-#pragma unroll 4
-    for (int bit = top; bit >= 0; --bit) {
+    const int stop = top - bits < -1 ? -1 : top - bits;
+#pragma unroll 2
+    for (int bit = top; bit > stop; --bit) {
         const uint32_t c1 = p1 | (1u << bit), c2 = p2 | (1u << bit);
         const int n1 = __popcll(__ballot(v >= c1));
         const int n2 = __popcll(__ballot(v >= c2));

@@ -8,7 +8,7 @@
 
 namespace g4s {
 
-constexpr int kWaveBounds = 256; /* per-wave bounds kept per row (splits * waves) */
+constexpr int kWaveBounds = 512; /* per-wave bounds kept per row (splits * waves) */
 
 /* Per-chunk record written by phase 1 (16 bytes). */
 struct ChunkRec {

@@ -8,9 +8,10 @@
  *  phase 1 (every workgroup)
  *    - 16-byte loads of the chunk into registers as order-preserving keys;
  *    - a provable lower bound theta of the chunk's K-th largest key: each
- *      wave takes the ceil(K/waves)-th largest of its 64 thread maxima
- *      (ballot binary search; distinct threads, so the wave holds at least
- *      that many keys >= its value) and the block keeps the minimum;
+ *      wave bounds the ceil(K/waves)-th largest of its 64 thread maxima
+ *      from below (ballot binary search over 14 bits below their common
+ *      prefix; distinct threads, so the wave holds at least that many keys
+ *      >= its value) and the block keeps the minimum;
  *    - every key >= theta is a candidate (a superset of the chunk's top-K),
  *      written straight to the chunk's HBM slots by wave-level compaction;
  *      if more than the chunk's slot count qualify (heavy ties), an exact
@@ -67,8 +68,8 @@ struct TopkShared {
     uint64_t mc[MCAP];     /* merge candidates, then replay tiles */
     uint64_t surv[KCAP];   /* survivors (unsorted); min-heap storage during a replay */
     uint64_t sorted[KCAP]; /* survivors ascending by vocab index */
-    float val[KCAP];       /* tail: v, then e */
-    float prob[KCAP];
+    alignas(16) float val[KCAP];  /* tail: v, then e; +0 up to a multiple of 64 */
+    alignas(16) float prob[KCAP]; /* tail: p; +0 up to a multiple of 64 */
 };
 
 __device__ __forceinline__ float lane_f(float x, int l)
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     constexpr int NV = ITEMS / VW;
     constexpr int NW = BLOCK / 64;
     constexpr int CHUNK = BLOCK * ITEMS;
-    constexpr int MCAP = KCAP <= 64 ? 512 : kMergeLds;
+    constexpr int MCAP = KCAP <= 64 ? (BLOCK > 512 ? BLOCK : 512) : kMergeLds; /* >= BLOCK */
     constexpr int kBatchLoads = batch_loads<BLOCK, KCAP>();
     static_assert(BLOCK >= kMaxSplits, "one merge thread per chunk record");
     static_assert(KCAP <= BLOCK, "one survivor per thread");
@@ -279,18 +280,21 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     uint32_t tmax = 0;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) tmax = keys[i] > tmax ? keys[i] : tmax;
-    /* per wave: the ceil(K/waves)-th and the ceil(K/splits)-th largest of the
-     * 64 thread maxima (distinct elements, so the wave holds at least that
-     * many keys >= each value) */
+    /* per wave: lower bounds of the ceil(K/waves)-th and the r1-th largest of
+     * the 64 thread maxima (distinct elements, so the wave holds at least
+     * that many keys >= each value) */
     const int kw = (K + NW - 1) / NW;
     const int nwave = S * NW;
     int r1 = (2 * K + nwave - 1) / nwave;
     r1 = r1 < 1 ? 1 : (r1 > 64 ? 64 : r1);
     uint32_t wth, wr1;
-    wave_kth_largest2(tmax, kw, r1, wth, wr1);
+    /* 14 bits below the common prefix of the thread maxima: a bound a hair
+     * under the exact value costs a candidate or two and saves half of the
+     * search */
+    wave_kth_largest2(tmax, kw, r1, 14, wth, wr1);
     if (lane == 0) {
         sh.wtheta[wid] = wth;
-        if (nwave <= kWaveBounds)
+        if (nwave <= kWaveBounds && nwave <= BLOCK)
             st_dev(&a.wbounds[(int64_t)row * kWaveBounds + chunk * NW + wid], wr1);
     }
     __syncthreads();
@@ -402,7 +406,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     /* one round trip: the chunk records, the wave bounds and the first
      * batch of slots (the index is clamped instead of branched on, so every
      * load is issued) */
-    const bool use_wb = nwave <= kWaveBounds;
+    const bool use_wb = nwave <= kWaveBounds && nwave <= BLOCK; /* one per merge thread */
     uint32_t wbv = 0u;
     if (use_wb && tid < nwave) wbv = ld_dev(&a.wbounds[(int64_t)row * kWaveBounds + tid]);
     if (tid < S) {
@@ -667,17 +671,29 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     for (int w = 0; w < NW; ++w) kmax = g4s_max_u(kmax, sh.red[w]);
     const float vmax = key2f(kmax);                                     /* :2789-2792 */
     if (tid < nsurv) sh.val[pos] = exp_diff_cr32(vv, vmax);             /* :2797 */
+    const int npad = (nsurv + 63) & ~63; /* <= KCAP, a multiple of 64 */
+    if (tid >= nsurv && tid < npad) {
+        sh.val[tid] = 0.0f;
+        sh.prob[tid] = 0.0f;
+    }
     __syncthreads();
 
     /* ------------------------------------------------ tail (wave 0 only) */
     if (wid != 0) return;
-    /* LSum := LSum + LVals[LI], left to right in binary32 (:2798); padding
-     * lanes add +0, which leaves a non-negative sum unchanged */
+    /* LSum := LSum + LVals[LI], left to right in binary32 (:2798), every
+     * lane on the same broadcast LDS reads; the padding adds +0, which
+     * leaves a non-negative sum unchanged */
     float lsum = 0.0f;
-    for (int base = 0; base < nsurv; base += 64) {
-        const float x = (base + lane < nsurv) ? sh.val[base + lane] : 0.0f;
+    for (int base = 0; base < npad; base += 64) {
+        const float4* src = reinterpret_cast<const float4*>(sh.val + base);
 #pragma unroll
-        for (int l = 0; l < 64; ++l) lsum = lsum + lane_f(x, l);
+        for (int l4 = 0; l4 < 16; ++l4) {
+            const float4 x = src[l4];
+            lsum = lsum + x.x;
+            lsum = lsum + x.y;
+            lsum = lsum + x.z;
+            lsum = lsum + x.w;
+        }
     }
     /* greedy choice: first position of the largest p (p >= 0, so its bits
      * order like the values) */
@@ -699,22 +715,27 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     if (T > 0.0f) {                                                     /* :2811-2824 */
         flags |= G4S_FLAG_DREW;
         const float thr = mul_u_p_cr32(u, rp.top_p);
-        /* LCum := LCum + LVals[LI] left to right; lane l keeps the running
-         * sum after term base + l, then one ballot finds the first >= thr */
+        /* LCum := LCum + LVals[LI] left to right (broadcast LDS reads as
+         * for LSum); hit = the first position whose running sum reaches
+         * thr.  A +0 padding term leaves the sum unchanged, so it never
+         * reaches thr first. */
         float cum = 0.0f;
         int hit = -1;
-        for (int base = 0; base < nsurv; base += 64) {
-            const float x = (base + lane < nsurv) ? sh.prob[base + lane] : 0.0f;
-            float mine_c = 0.0f;
+        __builtin_amdgcn_wave_barrier();
+        for (int base = 0; base < npad && hit < 0; base += 64) {
+            const float4* src = reinterpret_cast<const float4*>(sh.prob + base);
 #pragma unroll
-            for (int l = 0; l < 64; ++l) {
-                cum = cum + lane_f(x, l);
-                mine_c = (lane == l) ? cum : mine_c;
-            }
-            const uint64_t reach = __ballot(base + lane < nsurv && mine_c >= thr);
-            if (reach) {
-                hit = base + (int)__builtin_ctzll(reach);
-                break;
+            for (int l4 = 0; l4 < 16; ++l4) {
+                const float4 x = src[l4];
+                const int j = base + 4 * l4;
+                cum = cum + x.x;
+                hit = (hit < 0 && cum >= thr) ? j : hit;
+                cum = cum + x.y;
+                hit = (hit < 0 && cum >= thr) ? j + 1 : hit;
+                cum = cum + x.z;
+                hit = (hit < 0 && cum >= thr) ? j + 2 : hit;
+                cum = cum + x.w;
+                hit = (hit < 0 && cum >= thr) ? j + 3 : hit;
             }
         }
         if (hit >= 0) {
@@ -746,11 +767,13 @@ template <int BLOCK, int ITEMS, int DT>
 static hipError_t launch_cfg(const TopkArgs& a, int kcap, hipStream_t s)
 {
     dim3 grid((unsigned)a.splits, (unsigned)a.batch);
-    if constexpr (BLOCK == 256) {
+    if constexpr (BLOCK < 1024) {
         (void)kcap;
         hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 64>), grid, dim3(BLOCK), 0, s, a);
     } else {
-        if (kcap <= 256)
+        if (kcap <= 64)
+            hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 64>), grid, dim3(BLOCK), 0, s, a);
+        else if (kcap <= 256)
             hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 256>), grid, dim3(BLOCK), 0, s, a);
         else
             hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 1024>), grid, dim3(BLOCK), 0, s, a);
@@ -758,22 +781,35 @@ static hipError_t launch_cfg(const TopkArgs& a, int kcap, hipStream_t s)
     return hipGetLastError();
 }
 
+/* Launch shape: 512 x 16 for K bounds up to 64 (eight waves per 8192-term
+ * chunk), 1024 x 32 above; twice the items per thread when the vocabulary
+ * needs more than kMaxSplits chunks.  Slots per chunk: 4 x kbound when the
+ * workspace holds them, else 2 x kbound (>= 2 x kbound keeps a chunk's
+ * candidates >= theta within its slots except under heavy ties; 4 x also
+ * covers the spread of theta when K is near kbound). */
 TopkConfig topk_plan(int32_t vocab, int32_t kbound)
 {
+    struct Shape {
+        int block, items;
+    };
+    static constexpr Shape kSmallK[3] = {{512, 16}, {1024, 32}, {1024, 64}};
+    static constexpr Shape kLargeK[2] = {{1024, 32}, {1024, 64}};
+    const Shape* shapes = kbound <= 64 ? kSmallK : kLargeK;
+    const int nshape = kbound <= 64 ? 3 : 2;
     TopkConfig c{};
-    c.block = kbound <= 64 ? 256 : 1024;
-    c.cap_log2 = 1;
-    while ((1 << c.cap_log2) < 2 * kbound) ++c.cap_log2;
-    /* 32 items per thread unless the candidate slots do not fit the workspace */
-    const int items_try[2] = {32, 64};
-    for (int i = 0; i < 2; ++i) {
-        c.items = items_try[i];
-        c.chunk = c.block * c.items;
-        c.splits = (vocab + c.chunk - 1) / c.chunk;
-        if ((c.splits << c.cap_log2) <= kCandRow && c.splits <= kMaxSplits) break;
+    c.ok = false;
+    for (int mult = 4; mult >= 2 && !c.ok; mult -= 2) {
+        c.cap_log2 = 1;
+        while ((1 << c.cap_log2) < mult * kbound) ++c.cap_log2;
+        for (int i = 0; i < nshape && !c.ok; ++i) {
+            c.block = shapes[i].block;
+            c.items = shapes[i].items;
+            c.chunk = c.block * c.items;
+            c.splits = (vocab + c.chunk - 1) / c.chunk;
+            c.ok = ((c.splits << c.cap_log2) <= kCandRow) && (c.splits <= kMaxSplits) &&
+                   (1 << c.cap_log2) <= kMergeLds;
+        }
     }
-    c.ok = ((c.splits << c.cap_log2) <= kCandRow) && (c.splits <= kMaxSplits) &&
-           (1 << c.cap_log2) <= kMergeLds;
     return c;
 }
 
@@ -781,13 +817,11 @@ hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStr
 {
     const int kc = a.kbound;
     if (dtype == G4S_DTYPE_F32) {
-        if (c.block == 256 && c.items == 32) return launch_cfg<256, 32, 0>(a, kc, s);
-        if (c.block == 256 && c.items == 64) return launch_cfg<256, 64, 0>(a, kc, s);
+        if (c.block == 512 && c.items == 16) return launch_cfg<512, 16, 0>(a, kc, s);
         if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 0>(a, kc, s);
         return launch_cfg<1024, 64, 0>(a, kc, s);
     }
-    if (c.block == 256 && c.items == 32) return launch_cfg<256, 32, 1>(a, kc, s);
-    if (c.block == 256 && c.items == 64) return launch_cfg<256, 64, 1>(a, kc, s);
+    if (c.block == 512 && c.items == 16) return launch_cfg<512, 16, 1>(a, kc, s);
     if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 1>(a, kc, s);
     return launch_cfg<1024, 64, 1>(a, kc, s);
 }
