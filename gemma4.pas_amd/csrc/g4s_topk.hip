@@ -37,6 +37,8 @@
  */
 #include "g4s_topk.h"
 
+#include <type_traits>
+
 namespace g4s {
 
 using namespace g4s::cr;
@@ -60,12 +62,14 @@ struct TopkShared {
     uint32_t wtheta[16];
     int scan[16];
     uint32_t red[48];
-    int misc[8]; /* [0..3] counters and flags (see the kernel), [4..6] select results */
+    int misc[8]; /* [0..3] counters and flags (see the kernel), [4..6] select results,
+                    [7] the wave-bound lower bound of the merge */
     int flag_last;
     uint32_t hist[256];
     ChunkRec rec[kMaxSplits];
     uint32_t wb[kWaveBounds];
-    uint64_t mc[MCAP];     /* merge candidates, then replay tiles */
+    uint64_t mc[MCAP + 64]; /* phase-1 candidate staging, then merge candidates, then
+                               replay tiles; the last 64 absorb dropped lane writes */
     uint64_t surv[KCAP];   /* survivors (unsorted); min-heap storage during a replay */
     uint64_t sorted[KCAP]; /* survivors ascending by vocab index */
     alignas(16) float val[KCAP];  /* tail: v, then e; +0 up to a multiple of 64 */
@@ -304,8 +308,12 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     for (int w = 0; w < NW; ++w) theta = sh.wtheta[w] < theta ? sh.wtheta[w] : theta;
     theta = theta < 1u ? 1u : theta;
 
-    /* emit every key >= theta straight to the chunk's HBM slots: wave-level
-     * compaction, one LDS atomic per wave for the wave's base */
+    /* every key >= theta is a candidate: wave-level compaction (one LDS
+     * atomic per wave for the wave's base) into the LDS staging area with a
+     * store per item and no branch (an item that is not a candidate, or
+     * beyond the slots, goes to its lane's spare entry), then coalesced
+     * stores to the chunk's HBM slots when they all fit */
+    static_assert(MCAP >= 4 * KCAP || MCAP >= kMergeLds, "staging holds a chunk's slots");
     int mine = 0;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) mine += keys[i] >= theta;
@@ -320,26 +328,23 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 #pragma unroll
             for (int q = 0; q < VW; ++q) {
                 const uint32_t k = keys[j * VW + q];
-                if (k >= theta) {
-                    if (pos < cap)
-                        st_dev(&gcand[pos],
-                               cand_pack(k, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q)));
-                    ++pos;
-                }
+                const bool c = k >= theta;
+                sh.mc[(c && pos < cap) ? pos : MCAP + lane] =
+                    cand_pack(k, (uint32_t)(cbase + ((int64_t)j * BLOCK + tid) * VW + q));
+                pos += c ? 1 : 0;
             }
     }
     __syncthreads();
     const int total = sh.misc[0];
+    if (total <= cap)
+        for (int i = tid; i < total; i += BLOCK) st_dev(&gcand[i], sh.mc[i]);
 
     uint32_t rec_bound = theta, rec_mode_e = 0;
     int emitted = total;
     if (total > cap) {
         /* heavy ties or a weak theta: exact K-th largest of the chunk (the
-         * chunk holds more than cap >= 2K keys >= theta >= 1, so at least K).
-         * The slots are rewritten below: every wave's first-attempt stores
-         * complete before any rewrite is issued. */
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+         * chunk holds more than cap >= 2K keys >= theta >= 1, so at least K);
+         * nothing was written to the slots */
         int gt_c, eq_c;
         const uint32_t tau_c =
             regs_radix_kth<BLOCK, ITEMS>(keys, K, sh.hist, sh.misc + 4, &gt_c, &eq_c);
@@ -446,31 +451,27 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         /* a lower bound of the ceil(K/r1)-th largest wave bound, by every
          * wave (no barrier); 10 bits below the common prefix are enough to
          * cut the candidates to about K */
-        if (use_wb) {
+        if (use_wb && wid == 0) {
             const int j = (K + r1 - 1) / r1;
-            if (nwave <= 128) {
-                uint32_t kk[2];
+            const auto bound = [&](auto ng) {
+                constexpr int NG = decltype(ng)::value;
+                uint32_t kk[NG];
                 int nz = 0;
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
+                for (int q = 0; q < NG; ++q) {
                     const int i = lane + 64 * q;
                     kk[q] = i < nwave ? sh.wb[i] : 0u;
                     nz += __popcll(__ballot(kk[q] != 0u));
                 }
-                if (nz >= j) l1 = wave_kth_bound<2>(kk, j, 10);
-            } else {
-                uint32_t kk[kWaveBounds / 64];
-                int nz = 0;
-#pragma unroll
-                for (int q = 0; q < kWaveBounds / 64; ++q) {
-                    const int i = lane + 64 * q;
-                    kk[q] = i < nwave ? sh.wb[i] : 0u;
-                    nz += __popcll(__ballot(kk[q] != 0u));
-                }
-                if (nz >= j) l1 = wave_kth_bound<kWaveBounds / 64>(kk, j, 10);
-            }
+                return nz >= j ? wave_kth_bound<NG>(kk, j, 10) : 0u;
+            };
+            const uint32_t b = nwave <= 128   ? bound(std::integral_constant<int, 2>{})
+                               : nwave <= 256 ? bound(std::integral_constant<int, 4>{})
+                                              : bound(std::integral_constant<int, kWaveBounds / 64>{});
+            if (lane == 0) sh.misc[7] = (int)b;
         }
         __syncthreads();
+        if (use_wb) l1 = (uint32_t)sh.misc[7];
         lb = 1u;
         ex = 0u;
 #pragma unroll
@@ -485,10 +486,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 
     /* keep the candidates >= L (wave-level compaction); LDS holds the first
      * MCAP of them, the rest go to the row's HBM merge area */
-    auto keep = [&](int f, uint64_t c) {
-        return f < span && (f & (cap - 1)) < (int)sh.rec[f >> a.cap_log2].count &&
-               cand_key_of(c) >= L;
-    };
+
     for (int b0 = 0; b0 < span; b0 += kBatchLoads * BLOCK) {
         if (b0 > 0) {
 #pragma unroll
@@ -497,24 +495,48 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
                 v[i] = ld_dev(&rcand[f < span ? f : span - 1]);
             }
         }
-        uint32_t km = 0u; /* bit i: slot i is kept (one evaluation per slot) */
+        /* bit i: slot i is kept (inside the row's span, below its chunk's
+         * count, key >= L); the counts are read unconditionally (clamped
+         * index) so that the LDS reads overlap */
+        uint32_t cnt_of[kBatchLoads];
 #pragma unroll
-        for (int i = 0; i < kBatchLoads; ++i)
-            km |= (uint32_t)keep(b0 + tid + i * BLOCK, v[i]) << i;
+        for (int i = 0; i < kBatchLoads; ++i) {
+            const int f = b0 + tid + i * BLOCK;
+            cnt_of[i] = sh.rec[(f < span ? f : span - 1) >> a.cap_log2].count;
+        }
+        uint32_t km = 0u;
+#pragma unroll
+        for (int i = 0; i < kBatchLoads; ++i) {
+            const int f = b0 + tid + i * BLOCK;
+            const bool k = (f < span) & ((uint32_t)(f & (cap - 1)) < cnt_of[i]) &
+                           (cand_key_of(v[i]) >= L);
+            km |= (uint32_t)k << i;
+        }
         const int cnt = __popc(km);
         const int incl = wave_inclusive_scan(cnt);
         int base = 0;
         if (lane == 63) base = atomicAdd(&sh.misc[1], incl);
         base = __builtin_amdgcn_readlane(base, 63);
         int pos = base + incl - cnt;
+        if (__builtin_amdgcn_readlane(base + incl, 63) <= MCAP) {
+            /* the wave's candidates all fit in LDS: a store per slot, no
+             * branch (a slot not kept goes to its lane's spare entry) */
 #pragma unroll
-        for (int i = 0; i < kBatchLoads; ++i) {
-            if ((km >> i) & 1u) {
-                if (pos < MCAP)
-                    sh.mc[pos] = v[i];
-                else
-                    gmerge[pos] = v[i];
-                ++pos;
+            for (int i = 0; i < kBatchLoads; ++i) {
+                const bool k = (km >> i) & 1u;
+                sh.mc[k ? pos : MCAP + lane] = v[i];
+                pos += k ? 1 : 0;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kBatchLoads; ++i) {
+                if ((km >> i) & 1u) {
+                    if (pos < MCAP)
+                        sh.mc[pos] = v[i];
+                    else
+                        gmerge[pos] = v[i];
+                    ++pos;
+                }
             }
         }
     }
@@ -716,26 +738,35 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         flags |= G4S_FLAG_DREW;
         const float thr = mul_u_p_cr32(u, rp.top_p);
         /* LCum := LCum + LVals[LI] left to right (broadcast LDS reads as
-         * for LSum); hit = the first position whose running sum reaches
-         * thr.  A +0 padding term leaves the sum unchanged, so it never
-         * reaches thr first. */
+         * for LSum); every running sum goes back to LDS (the e values are no
+         * longer needed), then lane l reads the one after term base + l and
+         * one ballot finds the first that reaches thr (a +0 padding term
+         * leaves the sum unchanged, so it never reaches thr first) */
         float cum = 0.0f;
         int hit = -1;
         __builtin_amdgcn_wave_barrier();
-        for (int base = 0; base < npad && hit < 0; base += 64) {
+        for (int base = 0; base < npad; base += 64) {
             const float4* src = reinterpret_cast<const float4*>(sh.prob + base);
+            float4* dst = reinterpret_cast<float4*>(sh.val + base);
 #pragma unroll
             for (int l4 = 0; l4 < 16; ++l4) {
                 const float4 x = src[l4];
-                const int j = base + 4 * l4;
+                float4 c;
                 cum = cum + x.x;
-                hit = (hit < 0 && cum >= thr) ? j : hit;
+                c.x = cum;
                 cum = cum + x.y;
-                hit = (hit < 0 && cum >= thr) ? j + 1 : hit;
+                c.y = cum;
                 cum = cum + x.z;
-                hit = (hit < 0 && cum >= thr) ? j + 2 : hit;
+                c.z = cum;
                 cum = cum + x.w;
-                hit = (hit < 0 && cum >= thr) ? j + 3 : hit;
+                c.w = cum;
+                dst[l4] = c; /* the same value from every lane */
+            }
+            __builtin_amdgcn_wave_barrier();
+            const uint64_t reach = __ballot(sh.val[base + lane] >= thr);
+            if (reach) {
+                hit = base + (int)__builtin_ctzll(reach);
+                break;
             }
         }
         if (hit >= 0) {
