@@ -221,6 +221,89 @@ G4H_API int g4h_batch_throughput(g4s_sampler* s, void* stream, const void* d_log
     return rc;
 }
 
+/*
+ * The decode stream launched from a hipGraph, as a device-resident decode
+ * loop runs it: g4s_sample_async for one row is captured once, on fixed
+ * device buffers (logits, parameters, uniform, id; the id stays on the
+ * device for the next step).  For each row i of d_rows (fp32, row i at
+ * d_rows + i*vocab, parameters and uniforms in device arrays) the row is
+ * copied into those buffers untimed, then the graph is launched:
+ * gpu_us[i] = event time around the launch on the stream, host_us[i] =
+ * launch until the host sees the closing event complete, ids[i] = the id
+ * (read back untimed).
+ */
+G4H_API int g4h_graph_decode(g4s_sampler* s, void* stream, const float* d_rows, int32_t vocab,
+                             int32_t nrows, const g4s_params* d_params, const double* d_u,
+                             int32_t k_bound, double* host_us, float* gpu_us, int32_t* ids)
+{
+    hipStream_t st = (hipStream_t)stream;
+    if (nrows < 1) return -100;
+    float* row = nullptr;
+    g4s_params* par = nullptr;
+    double* u = nullptr;
+    int32_t* did = nullptr;
+    int32_t* hid = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t gx = nullptr;
+    int rc = 0;
+    if (hipMalloc((void**)&row, (size_t)vocab * sizeof(float)) != hipSuccess ||
+        hipMalloc((void**)&par, sizeof(g4s_params)) != hipSuccess ||
+        hipMalloc((void**)&u, sizeof(double)) != hipSuccess ||
+        hipMalloc((void**)&did, sizeof(int32_t)) != hipSuccess ||
+        hipHostMalloc((void**)&hid, sizeof(int32_t), hipHostMallocDefault) != hipSuccess ||
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+        rc = -101;
+    if (rc == 0 && hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        rc = -102;
+    if (rc == 0) {
+        const int src = g4s_sample_async(s, row, G4S_DTYPE_F32, vocab, 1, par, u, k_bound, 0, did,
+                                         nullptr);
+        const hipError_t ec = hipStreamEndCapture(st, &g);
+        if (src != 0) rc = src;
+        if (rc == 0 && ec != hipSuccess) rc = -104;
+    }
+    if (rc == 0 && hipGraphInstantiate(&gx, g, nullptr, nullptr, 0) != hipSuccess) rc = -105;
+    for (int32_t i = 0; rc == 0 && i < nrows; ++i) {
+        if (hipMemcpyAsync(row, d_rows + (int64_t)i * vocab, (size_t)vocab * sizeof(float),
+                           hipMemcpyDeviceToDevice, st) != hipSuccess ||
+            hipMemcpyAsync(par, d_params + i, sizeof(g4s_params), hipMemcpyDeviceToDevice, st) !=
+                hipSuccess ||
+            hipMemcpyAsync(u, d_u + i, sizeof(double), hipMemcpyDeviceToDevice, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            rc = -106;
+            break;
+        }
+        const double t0 = now_us();
+        (void)hipEventRecord(e0, st);
+        if (hipGraphLaunch(gx, st) != hipSuccess) rc = -107;
+        (void)hipEventRecord(e1, st);
+        while (rc == 0 && hipEventQuery(e1) == hipErrorNotReady) {
+        }
+        const double t1 = now_us();
+        if (rc == 0 && (hipMemcpyAsync(hid, did, sizeof(int32_t), hipMemcpyDeviceToHost, st) !=
+                            hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess))
+            rc = -108;
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        host_us[i] = t1 - t0;
+        gpu_us[i] = ms * 1000.0f;
+        ids[i] = *hid;
+    }
+    (void)hipStreamSynchronize(st);
+    if (gx) (void)hipGraphExecDestroy(gx);
+    if (g) (void)hipGraphDestroy(g);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (row) (void)hipFree(row);
+    if (par) (void)hipFree(par);
+    if (u) (void)hipFree(u);
+    if (did) (void)hipFree(did);
+    if (hid) (void)hipHostFree(hid);
+    return rc;
+}
+
 namespace {
 
 /* Plain streaming copy, 16 bytes per lane per step: the calibration kernel
