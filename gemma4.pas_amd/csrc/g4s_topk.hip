@@ -72,6 +72,7 @@ struct TopkShared {
                                replay tiles; the last 64 absorb dropped lane writes */
     uint64_t surv[KCAP];   /* survivors (unsorted); min-heap storage during a replay */
     uint64_t sorted[KCAP]; /* survivors ascending by vocab index */
+    uint64_t byidx[128];          /* small merges: the candidates in index order */
     alignas(16) float val[KCAP];  /* tail: v, then e; +0 up to a multiple of 64 */
     alignas(16) float prob[KCAP]; /* tail: p; +0 up to a multiple of 64 */
 };
@@ -139,7 +140,8 @@ __device__ void heap_replay(const char* row, int vocab, int K, SH& sh, float* hv
  * surv (any order) and true is returned; otherwise false (copies of tau must
  * be split by the tie rules). */
 template <int NG>
-__device__ __forceinline__ bool wave_fast_select(const uint64_t* mc, int M, int K, uint64_t* surv)
+__device__ __forceinline__ bool wave_fast_select(const uint64_t* mc, int M, int K, uint64_t* surv,
+                                                 uint32_t* tau_out = nullptr)
 {
     const int lane = threadIdx.x & 63;
     uint32_t kk[NG];
@@ -150,6 +152,7 @@ __device__ __forceinline__ bool wave_fast_select(const uint64_t* mc, int M, int 
     }
     int G, E;
     const uint32_t tau = wave_select_kth<NG>(kk, K, &G, &E);
+    if (tau_out) *tau_out = tau;
     const bool fast = E == K - G;
     if (fast) {
         int off = 0;
@@ -483,6 +486,11 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     }
     if (any_exact) flags |= G4S_FLAG_CHUNK_EXACT;
     const uint32_t L = lb > l1 ? lb : l1;
+    /* counters of the small select below (the wave bounds are consumed; the
+     * compaction's barrier orders these stores before their use) */
+    constexpr int kSmallM = 128;
+    static_assert(kWaveBounds >= kSmallM, "small-select counters");
+    for (int i = tid; i < kSmallM; i += BLOCK) sh.wb[i] = 0u;
 
     /* keep the candidates >= L (wave-level compaction); LDS holds the first
      * MCAP of them, the rest go to the row's HBM merge area */
@@ -550,7 +558,67 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     /* exact top K of the M candidates */
     int nsurv = 0;
     bool general = any_exact || M > MCAP;
-    if (!general) {
+    bool ordered = false; /* survivors already in sh.sorted by index */
+    if (!general && M > K && M <= kSmallM && NW >= 4) {
+        /* wave 0 selects tau by its ballot search while the other waves rank
+         * the M candidates by vocabulary index (distinct indices; thread
+         * (i, s) counts the smaller indices in slice s into an LDS counter) */
+        uint32_t tau = 0u;
+        if (wid == 0) {
+            const bool fast = wave_fast_select<2>(sh.mc, M, K, sh.surv, &tau);
+            if (lane == 0) sh.misc[5] = fast ? 0 : 1;
+        } else {
+            constexpr int SL = (NW - 1) * 64 / kSmallM; /* slices over waves 1.. */
+            const int t = tid - 64;
+            const int ci = t % kSmallM, sl = t / kSmallM;
+            const int per = ((M + SL - 1) / SL + 7) & ~7; /* whole steps of 8 */
+            const int j0 = sl * per, j1 = j0 + per < M ? j0 + per : M;
+            if (sl < SL && ci < M) {
+                const uint32_t mi = cand_idx_of(sh.mc[ci]);
+                uint32_t r = 0u;
+                for (int j = j0; j < j1; j += 8) {
+                    /* 16-byte reads issued together; entries past the slice
+                     * (within the merge area) are read and masked */
+                    uint32_t ij[8];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint4 w = reinterpret_cast<const uint4*>(sh.mc + j)[q];
+                        ij[2 * q] = w.x;
+                        ij[2 * q + 1] = w.z;
+                    }
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) r += (j + q < j1 && ij[q] < mi) ? 1u : 0u;
+                }
+                atomicAdd(&sh.wb[ci], r);
+            }
+        }
+        __syncthreads();
+        general = sh.misc[5] != 0;
+        if (!general) {
+            /* exactly K keys >= tau: wave 0 places every candidate at its
+             * index rank, then compacts the ones >= tau in that order */
+            nsurv = K;
+            ordered = true;
+            if (wid == 0) {
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int i = lane + 64 * q;
+                    if (i < M) sh.byidx[sh.wb[i]] = sh.mc[i];
+                }
+                __builtin_amdgcn_wave_barrier();
+                int off = 0;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int i = lane + 64 * q;
+                    const uint64_t c = i < M ? sh.byidx[i] : 0ull;
+                    const bool keep = i < M && cand_key_of(c) >= tau;
+                    const uint64_t m = __ballot(keep);
+                    if (keep) sh.sorted[off + __popcll(m & ((1ull << lane) - 1ull))] = c;
+                    off += __popcll(m);
+                }
+            }
+        }
+    } else if (!general) {
         /* one wave finds the K-th largest key tau of the M candidates (ballot
          * search over registers); when the candidates hold exactly K keys
          * >= tau there is no choice to make and they are the survivors.
@@ -658,8 +726,8 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     }
 
     /* one survivor per thread (nsurv <= K <= BLOCK): its slot in vocab-index
-     * order (rank by count; indices are distinct), then the reference's
-     * per-survivor steps */
+     * order (given by the small select, else rank by count; indices are
+     * distinct), then the reference's per-survivor steps */
     const float cap_v = a.softcap;
     const float T = rp.temperature;
     const bool scale = (T > 0.0f) && (T != 1.0f);
@@ -668,18 +736,24 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     float vv = 0.0f;
     int pos = 0;
     if (tid < nsurv) {
-        const uint64_t my = sh.surv[tid];
-        const uint32_t mi = cand_idx_of(my);
-        int j = 0;
-        for (; j + 8 <= nsurv; j += 8) {
-            uint32_t xx[8];
+        uint64_t my;
+        if (ordered) {
+            pos = tid;
+            my = sh.sorted[tid];
+        } else {
+            my = sh.surv[tid];
+            const uint32_t mi = cand_idx_of(my);
+            int j = 0;
+            for (; j + 8 <= nsurv; j += 8) {
+                uint32_t xx[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) xx[t] = cand_idx_of(sh.surv[j + t]);
+                for (int t = 0; t < 8; ++t) xx[t] = cand_idx_of(sh.surv[j + t]);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) pos += xx[t] < mi;
+                for (int t = 0; t < 8; ++t) pos += xx[t] < mi;
+            }
+            for (; j < nsurv; ++j) pos += cand_idx_of(sh.surv[j]) < mi;
+            sh.sorted[pos] = my;
         }
-        for (; j < nsurv; ++j) pos += cand_idx_of(sh.surv[j]) < mi;
-        sh.sorted[pos] = my;
         const float x = key2f(cand_key_of(my));                         /* :2774 */
         vv = (cap_v > 0.0f) ? softcap_topk_cr32(x, cap_v) : x;          /* :2775-2776 */
         if (scale) vv = vv * inv_t;                                     /* :2783-2784 */
