@@ -315,6 +315,41 @@ __device__ __forceinline__ bool terms_e_t(const uint32_t (&raw)[kFullPer], int n
     return false;
 }
 
+/* Two 16-bit lanes of one dword, subtracted lane-wise (v_pk_sub_u16). */
+__device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b)
+{
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t,
+                              __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
+}
+
+/* The table terms of a whole bf16 chunk of a full row straight from its two
+ * 16-byte loads: the table index of both codes of a dword at once (16-bit
+ * lane arithmetic; the same index and window test as tab_index).  Returns
+ * false, uniformly, when some code of the wave lies outside the table
+ * window (the caller then takes the general route). */
+__device__ __forceinline__ bool terms_bf16_whole(const char* rowp, int64_t e0, const Ctx& c,
+                                                 const float* tab, float (&t)[kFullPer])
+{
+    const uint32_t base = (uint32_t)c.win_lo << 7;
+    const uint32_t base2 = base | (base << 16);
+    uint32_t miss = 0u;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint4 w4 = reinterpret_cast<const uint4*>(rowp + e0 * 2)[q];
+        const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d = pk_sub_u16(ww[i], base2);
+            const uint32_t ix = (d & 0x07FF07FFu) | ((ww[i] >> 4) & 0x08000800u);
+            miss |= d & (kTabMiss | (kTabMiss << 16));
+            t[8 * q + 2 * i] = tab[ix & 0xFFFFu];
+            t[8 * q + 2 * i + 1] = tab[ix >> 16];
+        }
+    }
+    return __ballot(miss != 0u) == 0;
+}
+
 /* Whole chunks of full rows (the common case) skip the per-term mask. */
 template <int DT, bool P = false>
 __device__ __forceinline__ bool terms_e(const uint32_t (&raw)[kFullPer], int nvalid, int64_t e0,
@@ -1674,11 +1709,17 @@ __global__ __launch_bounds__(kFullBlock) void full_lsum_kernel(FullArgs a)
     const int32_t betas = cw + lane < bend ? a.ws.beta_l[rbase + cw + lane] : 0;
 
     for (int b = cw; b < bend; ++b) {
-        uint32_t raw[kFullPer];
         const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
-        const int nvalid = load16<DT>(rowp, e0, V, raw);
         float t[kFullPer];
-        const bool tabbed = terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t); /* Tensors.pas:660 */
+        int nvalid = kFullPer;
+        bool tabbed = DT == 1 && k.cls == kRowFull && c.win_lo >= 0 &&
+                      (int64_t)(b + 1) * kFullChunk <= V &&
+                      terms_bf16_whole(rowp, e0, c, sh.tab, t);                /* Tensors.pas:660 */
+        if (!tabbed) {
+            uint32_t raw[kFullPer];
+            nvalid = load16<DT>(rowp, e0, V, raw);
+            tabbed = terms_e<DT>(raw, nvalid, e0, c, k, sh.tab, t);
+        }
         /* the terms with e = 1 - jj*2^-24, jj < kNear (the row maximum and
          * its near ties): looked at only in waves that hold one */
         constexpr float kNearLo = 1.0f - (float)(kNear - 1) * 0x1p-24f;
@@ -1871,11 +1912,17 @@ __global__ __launch_bounds__(kFullBlock) void full_cdf_kernel(FullArgs a)
     const int32_t soffs = (mine && all && k.cls != kRowFull) ? rc[cw + lane].soff : 0;
 
     for (int b = cw; b < bend; ++b) {
-        uint32_t raw[kFullPer];
+        uint32_t raw[kFullPer]; /* loaded on the general route only (wide rows take it) */
         const int64_t e0 = (int64_t)b * kFullChunk + (int64_t)lane * kFullPer;
-        const int nvalid = load16<DT>(rowp, e0, V, raw);
         float t[kFullPer];
-        const bool tabbed = terms_e<DT, true>(raw, nvalid, e0, c, k, sh.tab, t);
+        int nvalid = kFullPer;
+        bool tabbed = DT == 1 && k.cls == kRowFull && c.win_lo >= 0 &&
+                      (int64_t)(b + 1) * kFullChunk <= V &&
+                      terms_bf16_whole(rowp, e0, c, sh.tab, t);
+        if (!tabbed) {
+            nvalid = load16<DT>(rowp, e0, V, raw);
+            tabbed = terms_e<DT, true>(raw, nvalid, e0, c, k, sh.tab, t);
+        }
         if (all) {
             float* po = a.out.probs ? a.out.probs + (int64_t)row * a.out.capacity : nullptr;
             int32_t* io = a.out.indices ? a.out.indices + (int64_t)row * a.out.capacity : nullptr;
