@@ -44,6 +44,28 @@ def test_lmhead_small_bit_exact(orc, batch):
     s.close()
 
 
+def test_lmhead_odd_block_count_and_unaligned_hidden(orc):
+    """An odd number of Q4_0 blocks per row (the kernel stages hidden values
+    two blocks at a time, so the last group is half empty) and a hidden
+    matrix that starts 4 bytes past a 16-byte boundary (staged with scalar
+    loads instead of 16-byte ones)."""
+    rows, cols, B = 300, 5 * 32, 3
+    w = wl.host_q4_weights(81, rows, cols)
+    hidden = wl.host_hidden(82, B, cols)
+    s = native.Sampler(V, max_batch=1, softcap=30.0)
+    dw = hip.Buffer.from_array(w)
+    dh = hip.Buffer(4 * (B * cols + 1))
+    dh.upload(np.ascontiguousarray(hidden, F32), offset=4)
+    dl = hip.Buffer(4 * B * rows)
+    s.lmhead_q4_0(dw, rows, cols, dh.offset(4), B, dl, rows)
+    hip.synchronize()
+    got = dl.download(F32).reshape(B, rows)
+    want = orc.matvec_q4_batch(w, hidden, rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+        f"{np.sum(got != want)} logits differ"
+    s.close()
+
+
 def test_lmhead_scale_edge_cases(orc):
     """fp16 scales that are zero, subnormal (the reference's own decoding of
     them, Types.pas:452-466), the largest finite, and negative; tiny and
