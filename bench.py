@@ -75,6 +75,7 @@ def harness():
                                        i32, vp, vp, vp]
     H.g4h_copy_throughput.argtypes = [vp, vp, vp, i64, i32, vp]
     H.g4h_graph_decode.argtypes = [vp, vp, vp, i32, i32, vp, vp, i32, vp, vp, vp]
+    H.g4h_graph_chunks.argtypes = [vp, vp, vp, i32, i32, vp, vp, i32, vp, i32, vp]
     H.g4h_lmhead_sampler.argtypes = [vp, vp, vp, i32, i32, vp, i32, vp, vp, vp, i32, vp, i32, i32,
                                      vp, vp]
     return H
@@ -103,6 +104,61 @@ def decode_latency(H, stream, rows0, nrows, mode):
     s.close()
     d.free()
     return host_us, gpu_us, ids
+
+
+def graph_back_to_back(H, stream, rows0, nrows, chunk=100):
+    """The decode stream's rows rows0 .. rows0+nrows-1 sampled back to back
+    from hipGraphs of `chunk` rows each (rows resident on the device); returns
+    (per-row us of every chunk, ids)."""
+    from gemma4_sampler import hip, native, workload as wl
+    s = native.Sampler(V, max_batch=1, softcap=wl.SOFTCAP_GEMMA4, stream=stream)
+    d = hip.Buffer(nrows * V * 4)
+    wl.dev_peaky_rows(d, SEED, rows0, nrows, V, greedy_every=wl.GREEDY_EVERY, stream=stream)
+    t, k, p = wl.peaky_params(range(rows0, rows0 + nrows))
+    par = native.params_array([native.TSamplingParams.make(a, b, c) for a, b, c in zip(t, k, p)])
+    d_par = hip.Buffer.from_array(np.frombuffer(par, np.uint8))
+    d_u = hip.Buffer.from_array(wl.host_row_u(SEED, rows0, nrows))
+    d_ids = hip.Buffer(nrows * 4)
+    stream.synchronize()
+    nchunk = (nrows + chunk - 1) // chunk
+    chunk_us = np.zeros(nchunk, np.float32)
+    rc = H.g4h_graph_chunks(s.h, stream.handle, d.ptr, V, nrows, d_par.ptr, d_u.ptr,
+                            int(k.max()), d_ids.ptr, chunk, _vp(chunk_us))
+    if rc != 0:
+        raise RuntimeError(f"g4h_graph_chunks failed: {rc} {s.last_error()}")
+    ids = d_ids.download(np.int32, nrows)
+    s.close()
+    for b in (d, d_par, d_u, d_ids):
+        b.free()
+    sizes = np.array([min(chunk, nrows - c * chunk) for c in range(nchunk)], np.float64)
+    return chunk_us / sizes, ids
+
+
+def cpu_all_cores(threads, nrows=1024, reps=3):
+    """The C++ oracle over decode rows spread across `threads` host threads
+    (one call, rows split by the oracle's thread pool): rows/s, best of reps."""
+    from gemma4_sampler import workload as wl
+    from oracle import oracle as orc
+    rows = wl.host_peaky_rows(SEED, 0, nrows, V, greedy_every=wl.GREEDY_EVERY, threads=threads)
+    t, k, p = wl.peaky_params(range(nrows))
+    u = wl.host_row_u(SEED, 0, nrows)
+    best = 0.0
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        orc.sample_batch(rows, 0, V, V, (t, k, p), u, softcap=wl.SOFTCAP_GEMMA4, threads=threads)
+        best = max(best, nrows / (time.perf_counter() - t0))
+    return best
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def graph_decode(H, stream, rows0, nrows):
@@ -351,6 +407,11 @@ def main():
     log(f"decode stream (hipGraph launch per row, id kept on the device): p50 "
         f"{pct(g_gpu, 50):.2f} us GPU events, p99 {pct(g_gpu, 99):.2f} us, host sees it after "
         f"{pct(g_host, 50):.2f} us (p50), mismatches {bad_graph}")
+    b2b_us, b2b_ids = graph_back_to_back(H, stream, args.warmup, n_graph)
+    bad_b2b = int(np.sum(b2b_ids != ids[:n_graph]))
+    bad_graph += bad_b2b
+    log(f"decode stream (hipGraphs of 100 rows back to back): per-row p50 {pct(b2b_us, 50):.2f} "
+        f"us, p99 {pct(b2b_us, 99):.2f} us over {len(b2b_us)} graphs, mismatches {bad_b2b}")
 
     # ---- dominant kernel of the decode stream: top-k path at B=1 ------------
     d1 = hip.Buffer(V * 4)
@@ -425,13 +486,17 @@ def main():
     # ---- CPU baseline (timed above, on the same rows) ---------------------
     cpu = None
     if not args.no_cpu and len(cpu_lat):
+        rps = cpu_all_cores(threads)
         cpu = {"value": pct(cpu_lat, 50), "unit": "us", "cores": 1, "kind": "port",
                "sample": f"p50 per-row latency of the C++ oracle's DoSample (one call per row, "
                          f"one host core) over the first {len(cpu_lat)} rows of the same decode "
-                         f"stream; p99 {pct(cpu_lat, 99):.1f} us; "
-                         f"{platform.processor() or platform.machine()}, "
-                         f"{os.cpu_count()} host cpus visible"}
-        log(f"CPU oracle: p50 {cpu['value']:.1f} us over {len(cpu_lat)} rows")
+                         f"stream; p99 {pct(cpu_lat, 99):.1f} us; {cpu_model()}, "
+                         f"{os.cpu_count()} host cpus visible",
+               "all_cores": {"rows_per_s": rps, "threads": threads,
+                             "sample": "1024 decode rows in one oracle call over the threads, "
+                                       "best of 3"}}
+        log(f"CPU oracle: p50 {cpu['value']:.1f} us over {len(cpu_lat)} rows; "
+            f"{rps:.0f} rows/s on {threads} threads")
 
     algo_bytes = V * 4
     achieved = algo_bytes / (k_mean * 1e-6) / 1e9
@@ -457,6 +522,9 @@ def main():
         "async_readback_p50_us": pct(a_host, 50),
         "graph_launched": {"rows": n_graph, "gpu_event_p50_us": pct(g_gpu, 50),
                            "gpu_event_p99_us": pct(g_gpu, 99), "host_p50_us": pct(g_host, 50)},
+        "graph_back_to_back": {"rows": n_graph, "rows_per_graph": 100,
+                               "per_row_p50_us": pct(b2b_us, 50),
+                               "per_row_p99_us": pct(b2b_us, 99)},
         "id_mismatches": bad + bad_async + bad_graph,
         "null_kernel_roundtrip": floor,
         "roofline": {"bound": "hbm", "kernel": "topk_kernel (B=1)", "achieved": achieved,

@@ -304,6 +304,59 @@ G4H_API int g4h_graph_decode(g4s_sampler* s, void* stream, const float* d_rows, 
     return rc;
 }
 
+/*
+ * The decode stream sampled back to back from hipGraphs: rows i = 0 ..
+ * nrows-1 resident at d_rows + i*vocab (fp32, parameters and uniforms in
+ * device arrays); each run of `chunk` rows is captured once as one graph of
+ * `chunk` g4s_sample_async calls (one row each), launched once untimed and
+ * once between two events: chunk_us[c] = event time of chunk c's graph
+ * (chunk rows back to back); d_ids[i] receives row i's id.
+ */
+G4H_API int g4h_graph_chunks(g4s_sampler* s, void* stream, const float* d_rows, int32_t vocab,
+                             int32_t nrows, const g4s_params* d_params, const double* d_u,
+                             int32_t k_bound, int32_t* d_ids, int32_t chunk, float* chunk_us)
+{
+    hipStream_t st = (hipStream_t)stream;
+    if (nrows < 1 || chunk < 1) return -100;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = 0;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) rc = -101;
+    for (int32_t c0 = 0, c = 0; rc == 0 && c0 < nrows; c0 += chunk, ++c) {
+        const int32_t n = std::min(chunk, nrows - c0);
+        hipGraph_t g = nullptr;
+        hipGraphExec_t gx = nullptr;
+        if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+            rc = -102;
+            break;
+        }
+        for (int32_t i = 0; i < n && rc == 0; ++i) {
+            const int32_t r = c0 + i;
+            rc = g4s_sample_async(s, d_rows + (int64_t)r * vocab, G4S_DTYPE_F32, vocab, 1,
+                                  d_params + r, d_u + r, k_bound, 0, d_ids + r, nullptr);
+        }
+        const hipError_t ec = hipStreamEndCapture(st, &g);
+        if (rc == 0 && ec != hipSuccess) rc = -104;
+        if (rc == 0 && hipGraphInstantiate(&gx, g, nullptr, nullptr, 0) != hipSuccess) rc = -105;
+        if (rc == 0 && (hipGraphLaunch(gx, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess))
+            rc = -106;
+        if (rc == 0) {
+            (void)hipEventRecord(e0, st);
+            if (hipGraphLaunch(gx, st) != hipSuccess) rc = -107;
+            (void)hipEventRecord(e1, st);
+            if (rc == 0 && hipEventSynchronize(e1) != hipSuccess) rc = -108;
+            float ms = 0.0f;
+            (void)hipEventElapsedTime(&ms, e0, e1);
+            chunk_us[c] = ms * 1000.0f;
+        }
+        if (gx) (void)hipGraphExecDestroy(gx);
+        if (g) (void)hipGraphDestroy(g);
+    }
+    (void)hipStreamSynchronize(st);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    return rc;
+}
+
 namespace {
 
 /* Plain streaming copy, 16 bytes per lane per step: the calibration kernel
