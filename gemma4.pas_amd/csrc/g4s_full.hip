@@ -69,7 +69,6 @@ using ss::State;
 namespace {
 
 constexpr int NWF = kFullBlock / 64;                 /* waves per workgroup */
-constexpr int kRowCPT = kFullMaxChunks / kFullBlock;  /* most chunk records per thread */
 constexpr int kSelCPT = kSelMaxChunks / kFullBlock;   /* select records per thread */
 
 struct RowIn {

@@ -12,11 +12,12 @@
  *      from below (ballot binary search over 14 bits below their common
  *      prefix; distinct threads, so the wave holds at least that many keys
  *      >= its value) and the block keeps the minimum;
- *    - every key >= theta is a candidate (a superset of the chunk's top-K),
- *      written straight to the chunk's HBM slots by wave-level compaction;
- *      if more than the chunk's slot count qualify (heavy ties), an exact
- *      per-chunk radix select emits the keys above the chunk's K-th value
- *      plus its first K copies in index order;
+ *    - every key >= theta is a candidate (a superset of the chunk's top-K):
+ *      wave-level compaction into LDS with one store per item and no
+ *      branch, then coalesced stores to the chunk's HBM slots; if more than
+ *      the chunk's slot count qualify (heavy ties), an exact per-chunk radix
+ *      select emits the keys above the chunk's K-th value plus its first K
+ *      copies in index order;
  *    - per wave, the r-th largest of its 64 thread maxima, r =
  *      ceil(2K / waves in the row): the wave holds at least r distinct keys
  *      >= it, so the ceil(K/r)-th largest of these over the row's waves is a
@@ -24,16 +25,17 @@
  *      keys of a row rarely share a thread);
  *    - an atomic ticket elects the last workgroup of the row.
  *  merge + tail (last workgroup of each row)
- *    - loads every chunk record and candidate slot of the row with
- *      independent loads (one memory round trip), keeps candidates
- *      >= the larger bound, selects the exact K-th value tau,
- *      resolves ties at tau like the reference's min-heap (lowest index when
- *      the heap layout cannot matter, a full heap replay otherwise), and
- *      sorts the survivors by vocab index;
+ *    - loads every chunk record, wave bound and candidate slot of the row
+ *      with independent loads (one memory round trip), keeps candidates
+ *      >= the larger bound (branch-free LDS compaction), selects the exact
+ *      K-th value tau, resolves ties at tau like the reference's min-heap
+ *      (lowest index when the heap layout cannot matter, a full heap replay
+ *      otherwise), and orders the survivors by vocab index (for at most 128
+ *      candidates the other waves rank them by index while wave 0 selects);
  *    - wave 0 runs the reference's tail in index order: softcap, 1/T, max,
  *      exp, sequential binary32 LSum, division, argmax, sequential running
  *      sum against fl32(u*TopP).  The sequential sums are exact left-to-right
- *      binary32 chains (one readlane per term).
+ *      binary32 chains over broadcast LDS reads.
  */
 #include "g4s_topk.h"
 
@@ -76,11 +78,6 @@ struct TopkShared {
     alignas(16) float val[KCAP];  /* tail: v, then e; +0 up to a multiple of 64 */
     alignas(16) float prob[KCAP]; /* tail: p; +0 up to a multiple of 64 */
 };
-
-__device__ __forceinline__ float lane_f(float x, int l)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
-}
 
 /* ------------------------------------------------------------ heap replay */
 
