@@ -231,7 +231,6 @@ __device__ __forceinline__ void wave_kth_largest2(uint32_t v, int k1, int k2, in
     uint32_t p1 = pre, p2 = pre;
     const bool on1 = k1 >= 1 && k1 <= 64, on2 = k2 >= 1 && k2 <= 64;
     const int stop = top - bits < -1 ? -1 : top - bits;
-#pragma unroll 2
     for (int bit = top; bit > stop; --bit) {
         const uint32_t c1 = p1 | (1u << bit), c2 = p2 | (1u << bit);
         const int n1 = __popcll(__ballot(v >= c1));
