@@ -556,7 +556,30 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     int nsurv = 0;
     bool general = any_exact || M > MCAP;
     bool ordered = false; /* survivors already in sh.sorted by index */
-    if (!general && M > K && M <= kSmallM && NW >= 4) {
+    if (!general && K == 1 && M > 1) {
+        /* K = 1: the reference's one-entry heap keeps the first (lowest-index)
+         * copy of the largest key, as a later equal key is rejected (v <=
+         * root, Model.pas:2643-2644); every copy of it is a candidate */
+        if (wid == 0) {
+            uint32_t kmax = 0u;
+            for (int i = lane; i < M; i += 64) kmax = g4s_max_u(kmax, cand_key_of(sh.mc[i]));
+            kmax = wave_max_u32(kmax);
+            uint32_t imin = 0xFFFFFFFFu;
+            int copies = 0;
+            for (int i = lane; i < M; i += 64) {
+                const uint64_t c = sh.mc[i];
+                if (cand_key_of(c) == kmax) {
+                    imin = g4s_min_u(imin, cand_idx_of(c));
+                    ++copies;
+                }
+            }
+            imin = wave_min_u32(imin);
+            if (wave_sum_i32(copies) > 1) flags |= G4S_FLAG_TIE_LOWEST;
+            if (lane == 0) sh.sorted[0] = cand_pack(kmax, imin);
+        }
+        nsurv = 1;
+        ordered = true;
+    } else if (!general && M > K && M <= kSmallM && NW >= 4) {
         /* wave 0 selects tau by its ballot search while the other waves rank
          * the M candidates by vocabulary index (distinct indices; thread
          * (i, s) counts the smaller indices in slice s into an LDS counter) */
@@ -885,10 +908,11 @@ static hipError_t launch_cfg(const TopkArgs& a, int kcap, hipStream_t s)
 
 /* Launch shape: 512 x 16 for K bounds up to 64 (eight waves per 8192-term
  * chunk), 1024 x 32 above; twice the items per thread when the vocabulary
- * needs more than kMaxSplits chunks.  Slots per chunk: 4 x kbound when the
- * workspace holds them, else 2 x kbound (>= 2 x kbound keeps a chunk's
- * candidates >= theta within its slots except under heavy ties; 4 x also
- * covers the spread of theta when K is near kbound). */
+ * needs more than kMaxSplits chunks.  Slots per chunk: 4 x kbound (at least
+ * 128) when the workspace holds them, else 2 x kbound (>= 2 x kbound keeps a
+ * chunk's candidates >= theta within its slots except under heavy ties; 4 x
+ * also covers the spread of theta when K is near kbound, and the floor the
+ * several waves' candidates when K is small). */
 TopkConfig topk_plan(int32_t vocab, int32_t kbound)
 {
     struct Shape {
@@ -901,7 +925,9 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound)
     TopkConfig c{};
     c.ok = false;
     for (int mult = 4; mult >= 2 && !c.ok; mult -= 2) {
-        c.cap_log2 = 1;
+        /* at least 128 slots: with a small K the chunk bound is the least of
+         * the waves' own bounds, so every wave contributes candidates */
+        c.cap_log2 = 7;
         while ((1 << c.cap_log2) < mult * kbound) ++c.cap_log2;
         for (int i = 0; i < nshape && !c.ok; ++i) {
             c.block = shapes[i].block;
