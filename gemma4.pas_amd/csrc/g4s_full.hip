@@ -695,6 +695,42 @@ __device__ State head_walk(const float (&t)[kFullPer], float thr, int* hit)
     return ss::state_of(s);
 }
 
+/* The first n terms (a multiple of 64) of a staged chunk (terms in index
+ * order in LDS) added term by term with plain binary32 additions from 0,
+ * every lane computing the same sum from broadcast reads: the head of a
+ * row's first chunk, where the running sum changes binade every few dozen
+ * terms, costs less this way than round after round of lane maps.  The
+ * running sum is monotone, so a 64-term block whose end reaches thr is
+ * walked again to find the first term that does (*hit, chunk-relative). */
+constexpr int kSeqLanes = 24; /* lanes of the first chunk walked term by term */
+__device__ State seq_walk(const float* tv, int n, float thr, int* hit)
+{
+    float s = 0.0f;
+    for (int b = 0; b < n; b += 64) {
+        const float4* src = reinterpret_cast<const float4*>(tv + b);
+        const float s0 = s;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const float4 x = src[q];
+            s = s + x.x;
+            s = s + x.y;
+            s = s + x.z;
+            s = s + x.w;
+        }
+        if (s >= thr) {
+            float u = s0;
+            for (int j = 0; j < 64; ++j) {
+                u = u + tv[b + j];
+                if (u >= thr) {
+                    *hit = b + j;
+                    return ss::state_of(u);
+                }
+            }
+        }
+    }
+    return ss::state_of(s);
+}
+
 /*
  * Chain the chunk maps from chunk c on, 64 chunks per step: the maps are
  * composed over the wave and applied to the entering state, and accepted up
@@ -1008,9 +1044,9 @@ __device__ State chain_chunk(const FullArgs& a, const char* rowp, int c, State s
         const StageMaps* sm = L.sm + s;
         const int32_t b = sm->b;
         if (c == 0) {
-            st = head_walk(t, thr, hit);
+            st = seq_walk(L.tv + (size_t)s * kFullChunk, kSeqLanes * kFullPer, thr, hit);
             if (*hit >= 0) return st;
-            pos = kHeadLanes;
+            pos = kSeqLanes;
         } else if (st.e == b) {
             ++*rounds;
             if (round_step(sm->lo[lane], t, st, thr, pos, hit) || *hit >= 0) return st;
