@@ -562,15 +562,16 @@ __device__ __forceinline__ bool tie_possible(uint64_t mask, int base, int32_t e)
     return (unsigned)i >= 64u || ((mask >> i) & 1ull) != 0ull;
 }
 
-/* OR over the wave of a 64-bit value (every lane gets it). */
+/* OR over the wave of a 64-bit value (every lane gets it): DPP scans of
+ * both halves, lane 63's result broadcast. */
+__device__ __forceinline__ uint32_t g4s_or_u(uint32_t a, uint32_t b) { return a | b; }
 __device__ __forceinline__ uint64_t wave_or64(uint64_t v)
 {
     uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        lo |= (uint32_t)__shfl_xor((int)lo, o, 64);
-        hi |= (uint32_t)__shfl_xor((int)hi, o, 64);
-    }
+    G4S_DPP_SCAN(lo, g4s_or_u, 0u, uint32_t);
+    G4S_DPP_SCAN(hi, g4s_or_u, 0u, uint32_t);
+    lo = (uint32_t)__builtin_amdgcn_readlane((int)lo, 63);
+    hi = (uint32_t)__builtin_amdgcn_readlane((int)hi, 63);
     return ((uint64_t)hi << 32) | lo;
 }
 
