@@ -413,36 +413,48 @@ __device__ __forceinline__ int block_sum_int(int v, Scratch& sh)
     return r;
 }
 
-__device__ __forceinline__ double block_sum_d(double v, Scratch& sh)
+/* One DPP step of an inclusive wave scan of doubles: both halves move
+ * together; a lane without a source adds +0. */
+template <int CTRL, int RMASK>
+__device__ __forceinline__ double dpp_add_d(double x)
 {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    if (lane == 0) sh.dred[wid] = v;
-    __syncthreads();
-    double r = 0.0;
-#pragma unroll
-    for (int w = 0; w < NWF; ++w) r += sh.dred[w];
-    __syncthreads();
-    return r;
+    const uint64_t b = (uint64_t)__double_as_longlong(x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, RMASK, 0xf, false);
+    const uint32_t hi =
+        (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, RMASK, 0xf, false);
+    return x + __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-/* Exclusive prefix over the workgroup in thread order (doubles). */
-__device__ __forceinline__ double block_excl_scan_d(double v, Scratch& sh)
+/* Inclusive scan of doubles over the wave in lane order (DPP, as the
+ * integer scans). */
+__device__ __forceinline__ double wave_incl_scan_d(double x)
+{
+    x = dpp_add_d<0x111, 0xf>(x);
+    x = dpp_add_d<0x112, 0xf>(x);
+    x = dpp_add_d<0x114, 0xf>(x);
+    x = dpp_add_d<0x118, 0xf>(x);
+    x = dpp_add_d<0x142, 0xa>(x);
+    x = dpp_add_d<0x143, 0xc>(x);
+    return x;
+}
+
+/* Exclusive prefix over the workgroup in thread order (doubles), and the
+ * workgroup's total. */
+__device__ __forceinline__ double block_excl_scan_d(double v, Scratch& sh, double& total)
 {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    double x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
+    const double x = wave_incl_scan_d(v);
     if (lane == 63) sh.dred[wid] = x;
     __syncthreads();
-    double off = 0.0;
+    double off = 0.0, tot = 0.0;
 #pragma unroll
-    for (int w = 0; w < NWF; ++w) off += (w < wid) ? sh.dred[w] : 0.0;
+    for (int w = 0; w < NWF; ++w) {
+        const double d = sh.dred[w];
+        off += (w < wid) ? d : 0.0;
+        tot += d;
+    }
     __syncthreads();
+    total = tot;
     return off + x - v;
 }
 
@@ -1670,8 +1682,8 @@ __global__ __launch_bounds__(kFullBlock) void full_row_kernel(FullArgs a)
             fs = g4s_min_u(fs, (uint32_t)c.fsurv);
         }
     }
-    const double total = block_sum_d(tsum, sh);
-    double pre = block_excl_scan_d(tsum, sh);
+    double total;
+    double pre = block_excl_scan_d(tsum, sh, total);
     int count;
     int soff = block_excl_scan_i(tns, sh, count);
     fs = block_min_u(fs, sh);
