@@ -176,6 +176,45 @@ G4H_API int g4h_decode_latency(g4s_sampler* s, void* stream, void* d_row, uint64
 }
 
 /*
+ * A train of `steps` stream-ordered samples of the same resident batch with
+ * no event between them: *total_us is the event time from before the first
+ * to after the last, so total_us / steps is the average launch duration
+ * including only the gap between consecutive kernels.
+ */
+G4H_API int g4h_launch_train(g4s_sampler* s, void* stream, const void* d_logits, int32_t dtype,
+                             int64_t row_stride, int32_t batch, const g4s_params* d_params,
+                             const double* d_u, int32_t k_bound, int32_t full_rows,
+                             int32_t* d_ids, int32_t warmup, int32_t steps, float* total_us)
+{
+    hipStream_t st = (hipStream_t)stream;
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess) return -100;
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return -100;
+    }
+    int rc = 0;
+    for (int32_t i = 0; rc == 0 && i < warmup; ++i)
+        rc = g4s_sample_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound,
+                              full_rows, d_ids, nullptr);
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    if (rc == 0) (void)hipEventRecord(e0, st);
+    for (int32_t i = 0; rc == 0 && i < steps; ++i)
+        rc = g4s_sample_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound,
+                              full_rows, d_ids, nullptr);
+    if (rc == 0) (void)hipEventRecord(e1, st);
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    if (rc == 0) {
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        *total_us = ms * 1000.0f;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
+}
+
+/*
  * Batched throughput: `steps` stream-ordered samples of the same resident
  * batch (g4s_sample_async, parameters on the device), each bracketed by a
  * pair of events on the sampler's stream.  step_us[i] = event time of step
