@@ -30,6 +30,7 @@ thread_local std::string g_create_error;
 
 struct g4s_sampler {
     int device = 0;
+    int32_t ncu = 0; /* compute units of the device (top-k launch split) */
     int32_t vocab = 0;
     int32_t max_batch = 0;
     float softcap = 0.0f;
@@ -158,7 +159,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         a.done = done;
         a.seq = seq;
         a.out = out;
-        hipError_t e = g4s::topk_launch(cfg, a, dtype, s->stream);
+        hipError_t e = g4s::topk_launch(cfg, a, dtype, s->stream, s->ncu);
         if (e != hipSuccess) return hip_fail(s, e, "top-k kernel launch");
     }
     if (full_rows || wide) {
@@ -240,6 +241,7 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
 
     g4s_sampler* s = new g4s_sampler();
     s->device = dev;
+    s->ncu = prop.multiProcessorCount;
     s->vocab = vocab;
     s->max_batch = max_batch;
     s->softcap = softcap;

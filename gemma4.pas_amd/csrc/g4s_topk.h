@@ -39,6 +39,8 @@ struct TopkArgs {
     int32_t cap_log2; /* candidate slots per chunk = 1 << cap_log2 (>= 2 * kbound) */
     int32_t kbound;   /* every top-k row has TopK <= kbound */
     int32_t wide_on;  /* rows with TopK > kMaxTopK are left to the wide launches */
+    int32_t mode;     /* 0: chunks + last-workgroup merge in one launch; 1: chunks
+                         only; 2: merges only (one workgroup per row) */
     float softcap;
     uint64_t* cand;   /* [batch][kCandRow] chunk candidates */
     uint64_t* merge;  /* [batch][kCandRow] merge candidates beyond what LDS holds */
@@ -57,7 +59,12 @@ struct TopkConfig {
 };
 
 TopkConfig topk_plan(int32_t vocab, int32_t kbound);
-hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStream_t s);
+/* One launch (mode 0) while the batch's chunk workgroups fit the device at
+ * once (`ncu` compute units, 1024 resident threads each), else a chunk
+ * launch followed by a merge launch, so that no merge holds a compute unit
+ * that a later chunk is waiting for. */
+hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStream_t s,
+                       int32_t ncu = 0);
 
 }  // namespace g4s
 

@@ -238,7 +238,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     if (!(K >= 1 && K < V)) return; /* full-vocabulary row (Model.pas:2756) */
     if (K > a.kbound) {
         if (a.wide_on && K > kMaxTopK) return; /* a wide row (g4s_full.hip) */
-        if (chunk == 0 && wid == 0) {
+        if (chunk == 0 && wid == 0 && a.mode != 1) {
             if (lane == 0) {
                 a.ids[row] = -1;
                 if (a.out.flags) a.out.flags[row] = G4S_FLAG_ERROR | G4S_FLAG_TOPK_PATH;
@@ -260,6 +260,11 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         sh.misc[3] = 0; /* K-th key tie flag */
     }
 
+    const int nwave = S * NW;
+    /* rank of each wave's recorded bound among its 64 thread maxima */
+    int r1 = (2 * K + nwave - 1) / nwave;
+    r1 = r1 < 1 ? 1 : (r1 > 64 ? 64 : r1);
+    if (a.mode != 2) {
     /* ------------------------------------------------------- phase 1 */
     uint32_t keys[ITEMS];
     if (cbase + CHUNK <= V) {
@@ -288,9 +293,6 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
      * the 64 thread maxima (distinct elements, so the wave holds at least
      * that many keys >= each value) */
     const int kw = (K + NW - 1) / NW;
-    const int nwave = S * NW;
-    int r1 = (2 * K + nwave - 1) / nwave;
-    r1 = r1 < 1 ? 1 : (r1 > 64 ? 64 : r1);
     uint32_t wth, wr1;
     /* 14 bits below the common prefix of the thread maxima: a bound a hair
      * under the exact value costs a candidate or two and saves half of the
@@ -399,8 +401,11 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         st_dev(rp64 + 1, (uint64_t)rec_mode_e << 32);
     }
 
+    if (a.mode == 1) return; /* the merge launch follows */
+
     /* ----------------------------------------------- last workgroup elects */
     if (!elect_last(&a.tickets[row], (uint32_t)S, &sh.flag_last)) return;
+    } /* phase 1 */
 
     /* ------------------------------------------------------------ merge */
     uint32_t flags = G4S_FLAG_TOPK_PATH;
@@ -889,9 +894,9 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 /* ---------------------------------------------------------------- launch */
 
 template <int BLOCK, int ITEMS, int DT>
-static hipError_t launch_cfg(const TopkArgs& a, int kcap, hipStream_t s)
+static hipError_t launch_one(const TopkArgs& a, int kcap, hipStream_t s)
 {
-    dim3 grid((unsigned)a.splits, (unsigned)a.batch);
+    dim3 grid(a.mode == 2 ? 1u : (unsigned)a.splits, (unsigned)a.batch);
     if constexpr (BLOCK < 1024) {
         (void)kcap;
         hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 64>), grid, dim3(BLOCK), 0, s, a);
@@ -904,6 +909,19 @@ static hipError_t launch_cfg(const TopkArgs& a, int kcap, hipStream_t s)
             hipLaunchKernelGGL((topk_kernel<BLOCK, ITEMS, DT, 1024>), grid, dim3(BLOCK), 0, s, a);
     }
     return hipGetLastError();
+}
+
+template <int BLOCK, int ITEMS, int DT>
+static hipError_t launch_cfg(const TopkArgs& a, int kcap, hipStream_t s, int32_t ncu)
+{
+    if (ncu <= 0 || (int64_t)a.batch * a.splits * BLOCK <= (int64_t)ncu * 1024)
+        return launch_one<BLOCK, ITEMS, DT>(a, kcap, s);
+    TopkArgs b = a;
+    b.mode = 1;
+    hipError_t e = launch_one<BLOCK, ITEMS, DT>(b, kcap, s);
+    if (e != hipSuccess) return e;
+    b.mode = 2;
+    return launch_one<BLOCK, ITEMS, DT>(b, kcap, s);
 }
 
 /* Launch shape: 512 x 16 for K bounds up to 64 (eight waves per 8192-term
@@ -941,17 +959,18 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound)
     return c;
 }
 
-hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStream_t s)
+hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStream_t s,
+                       int32_t ncu)
 {
     const int kc = a.kbound;
     if (dtype == G4S_DTYPE_F32) {
-        if (c.block == 512 && c.items == 16) return launch_cfg<512, 16, 0>(a, kc, s);
-        if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 0>(a, kc, s);
-        return launch_cfg<1024, 64, 0>(a, kc, s);
+        if (c.block == 512 && c.items == 16) return launch_cfg<512, 16, 0>(a, kc, s, ncu);
+        if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 0>(a, kc, s, ncu);
+        return launch_cfg<1024, 64, 0>(a, kc, s, ncu);
     }
-    if (c.block == 512 && c.items == 16) return launch_cfg<512, 16, 1>(a, kc, s);
-    if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 1>(a, kc, s);
-    return launch_cfg<1024, 64, 1>(a, kc, s);
+    if (c.block == 512 && c.items == 16) return launch_cfg<512, 16, 1>(a, kc, s, ncu);
+    if (c.block == 1024 && c.items == 32) return launch_cfg<1024, 32, 1>(a, kc, s, ncu);
+    return launch_cfg<1024, 64, 1>(a, kc, s, ncu);
 }
 
 }  // namespace g4s
