@@ -23,8 +23,12 @@
  *      >= it, so the ceil(K/r)-th largest of these over the row's waves is a
  *      second lower bound of the row's K-th largest (a tight one: the top
  *      keys of a row rarely share a thread);
- *    - an atomic ticket elects the last workgroup of the row.
- *  merge + tail (last workgroup of each row)
+ *    - an atomic ticket elects the last workgroup of the row; a batch
+ *      whose chunk workgroups do not all fit the device at once skips the
+ *      ticket and runs the merges as a second launch (one workgroup per
+ *      row, TopkArgs::mode), so no merge holds a compute unit that a chunk
+ *      of the second round is waiting for.
+ *  merge + tail (last workgroup of each row, or the merge launch)
  *    - loads every chunk record, wave bound and candidate slot of the row
  *      with independent loads (one memory round trip), keeps candidates
  *      >= the larger bound (branch-free LDS compaction), selects the exact
