@@ -118,6 +118,23 @@ def test_mixed_batch(big, orc):
     print(f"mixed batch: boundary draws {nb}")
 
 
+@pytest.mark.parametrize("B", [16, 17, 40])
+def test_batch_launch_modes(big, orc, B):
+    """K <= 64 batches on both sides of the merge-launch split: 16 rows of 32
+    chunk workgroups fit the device at once (one launch, last-workgroup
+    merges); 17 and 40 rows do not (a chunk launch, then a merge launch)."""
+    rows = wl.host_peaky_rows(SEED + 7, 0, B, V)
+    ks = [1, 7, 33, 64]
+    k = np.array([ks[r % 4] for r in range(B)], np.int32)
+    t = np.array([(0.0, 0.7, 1.0, 1.3)[(r // 4) % 4] for r in range(B)], F32)
+    p = np.array([(0.9, 0.95, 1.0)[r % 3] for r in range(B)], F32)
+    u = wl.host_row_u(SEED + 7, 0, B)
+    d = hip.Buffer.from_array(rows)
+    outs = native.DeviceOutputs(B, 64)
+    _, ids = big.sample(d, B, _params(t, k, p), u, outputs=outs.struct)
+    check_rows(orc, rows, t, k, p, u, ids, outs.read(), label=f"B={B}")
+
+
 def test_async_matches_sync(big, orc):
     B = 16
     rows = wl.host_peaky_rows(SEED + 2, 0, B, V)
