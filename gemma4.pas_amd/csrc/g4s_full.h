@@ -127,6 +127,8 @@ struct FullArgs {
     int32_t nstage;   /* chunks each chain precomputes (set by full_launch) */
     int32_t cpw;      /* chunks per wave of the streaming passes (set by full_launch) */
     int32_t wide_on;  /* wide rows are handled by this launch */
+    int32_t topk_on;  /* a top-k launch takes the top-k rows; when 0 such a row gets
+                         id -1 and G4S_FLAG_ERROR | G4S_FLAG_TOPK_PATH here */
     FullWorkspace ws;
     int32_t* ids;
     uint32_t* done;

@@ -2024,6 +2024,13 @@ __global__ __launch_bounds__(kChainBlock) void full_cdf_chain_kernel(FullArgs a)
     const int tid = threadIdx.x, lane = tid & 63;
     const int row = blockIdx.y;
     const RowIn ri = row_in(a, row);
+    if (!a.topk_on && row_class(a, ri.p.top_k) == kRowTopk) {
+        /* no top-k launch in this call: reject the row rather than leave an
+         * earlier call's id in place */
+        if (tid < 64)
+            write_row_outputs(a, row, -1, -1, 0.0f, 0, G4S_FLAG_ERROR | G4S_FLAG_TOPK_PATH);
+        return;
+    }
     Mask k;
     if (!row_mask(a, row, ri, k)) return;
     const FullRow r = a.ws.rows[row];

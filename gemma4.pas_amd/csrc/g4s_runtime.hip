@@ -149,6 +149,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         a.cap_log2 = cfg.cap_log2;
         a.kbound = kbound;
         a.wide_on = wide ? 1 : 0;
+        a.full_on = (full_rows || wide) ? 1 : 0;
         a.softcap = s->softcap;
         a.cand = s->cand;
         a.merge = s->merge;
@@ -181,6 +182,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         f.nch = (s->vocab + g4s::kFullChunk - 1) / g4s::kFullChunk;
         f.nsel = (s->vocab + g4s::kSelChunk - 1) / g4s::kSelChunk;
         f.wide_on = wide ? 1 : 0;
+        f.topk_on = kbound > 0 ? 1 : 0;
         f.ws = s->full;
         f.ids = d_ids;
         f.done = done;

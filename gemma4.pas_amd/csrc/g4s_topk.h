@@ -39,6 +39,8 @@ struct TopkArgs {
     int32_t cap_log2; /* candidate slots per chunk = 1 << cap_log2 (>= 2 * kbound) */
     int32_t kbound;   /* every top-k row has TopK <= kbound */
     int32_t wide_on;  /* rows with TopK > kMaxTopK are left to the wide launches */
+    int32_t full_on;  /* the softmax launches follow for full rows; when 0 a full row
+                         gets id -1 and G4S_FLAG_ERROR | G4S_FLAG_FULL_PATH here */
     int32_t mode;     /* 0: chunks + last-workgroup merge in one launch; 1: chunks
                          only; 2: merges only (one workgroup per row) */
     float softcap;

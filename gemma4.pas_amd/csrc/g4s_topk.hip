@@ -239,7 +239,19 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     const g4s_params rp = a.params ? a.params[row] : a.p0;
     const double u = a.u ? a.u[row] : a.u0;
     const int K = rp.top_k;
-    if (!(K >= 1 && K < V)) return; /* full-vocabulary row (Model.pas:2756) */
+    if (!(K >= 1 && K < V)) {
+        /* full-vocabulary row (Model.pas:2756): the softmax launches take it,
+         * or, when none follows this launch, it is rejected here so that no
+         * stale id of an earlier call survives */
+        if (!a.full_on && chunk == 0 && wid == 0 && a.mode != 1) {
+            if (lane == 0) {
+                a.ids[row] = -1;
+                if (a.out.flags) a.out.flags[row] = G4S_FLAG_ERROR | G4S_FLAG_FULL_PATH;
+            }
+            publish_done(a.done, row, a.seq);
+        }
+        return;
+    }
     if (K > a.kbound) {
         if (a.wide_on && K > kMaxTopK) return; /* a wide row (g4s_full.hip) */
         if (chunk == 0 && wid == 0 && a.mode != 1) {

@@ -1,0 +1,251 @@
+{===============================================================================
+  Gemma4.Sampler - binding of libgemma4_sampler.so, the MI355X (gfx950) token
+  sampler, for the Gemma4.pas engine (Delphi Linux64, or FPC in Delphi mode).
+
+  The library replaces TModel.DoSample and its helpers
+  (src/Gemma4.Model.pas:2615-2827, src/Gemma4.Tensors.pas:638-673,
+  src/Gemma4.Layers.pas:300-316) on logits that stay in GPU memory.  Every
+  external below is one export of include/gemma4_sampler.h, with the same
+  argument order and the same C types: arrays and out-values are typed
+  pointers (PG4SParams, PDouble, PInteger, ...), passed by value, so nothing
+  depends on how a compiler passes `const` or `var` records.
+
+  TGpuSampler wraps one handle the way the engine wraps its GPU objects: a
+  failing call adds an esError entry to GetErrors() with a unit code
+  CSM_ERR_* and the library's message (StdApp.Base.pas TErrors.Add), and
+  returns False.
+===============================================================================}
+
+unit Gemma4.Sampler;
+
+{$IFDEF FPC}{$MODE DELPHI}{$ENDIF}
+
+interface
+
+uses
+  SysUtils,
+  StdApp.Base;
+
+const
+  CG4SLib = 'libgemma4_sampler.so';
+
+  CSM_ERR_CREATE = 'SM01';
+  CSM_ERR_SAMPLE = 'SM02';
+  CSM_ERR_LMHEAD = 'SM03';
+
+  G4S_ABI_VERSION = 1;
+
+  // g4s_status
+  G4S_OK = 0;
+  G4S_ERR_INVALID_ARGUMENT = -1;
+  G4S_ERR_UNSUPPORTED = -2;
+  G4S_ERR_NO_DEVICE = -3;
+  G4S_ERR_OUT_OF_MEMORY = -4;
+  G4S_ERR_HIP = -5;
+  G4S_ERR_EMPTY_ROW = -6;
+
+  // g4s_dtype
+  G4S_DTYPE_F32 = 0;
+  G4S_DTYPE_BF16 = 1;
+
+  // per-row flags (TG4SOutputs.Flags)
+  G4S_FLAG_TOPK_PATH = $1;
+  G4S_FLAG_FULL_PATH = $2;
+  G4S_FLAG_DREW = $4;
+  G4S_FLAG_REACHED = $8;
+  G4S_FLAG_TIE_LOWEST = $10;
+  G4S_FLAG_HEAP_REPLAY = $20;
+  G4S_FLAG_CHUNK_EXACT = $40;
+  G4S_FLAG_WIDE_MERGE = $80;
+  G4S_FLAG_WIDE_K = $100;
+  G4S_FLAG_EMPTY = $40000000;
+  G4S_FLAG_ERROR = $80000000;
+
+type
+  { PG4SSampler }
+  // opaque g4s_sampler*
+  PG4SSampler = Pointer;
+  PPG4SSampler = ^PG4SSampler;
+
+  { TG4SParams }
+  // g4s_params: the field order, types and meaning of TSamplingParams
+  // (src/Gemma4.Model.pas:70-76), so @AParams of the engine's record is a
+  // valid PG4SParams.
+  TG4SParams = record
+    Temperature: Single;
+    TopK: Integer;
+    TopP: Single;
+    RepetitionPenalty: Single;
+  end;
+  PG4SParams = ^TG4SParams;
+
+  { TG4SOutputs }
+  // g4s_outputs: optional per-row outputs; every pointer is GPU memory and
+  // may be nil
+  TG4SOutputs = record
+    Count: PInteger;
+    Indices: PInteger;
+    Probs: PSingle;
+    Capacity: Integer;
+    Argmax: PInteger;
+    LSum: PSingle;
+    Flags: PCardinal;
+  end;
+  PG4SOutputs = ^TG4SOutputs;
+
+function g4s_version(): PAnsiChar; cdecl; external CG4SLib;
+procedure g4s_params_set_defaults(AParams: PG4SParams); cdecl; external CG4SLib;
+function g4s_max_top_k(): Integer; cdecl; external CG4SLib;
+function g4s_create(AOut: PPG4SSampler; AVocab: Integer; AMaxBatch: Integer;
+  ASoftcap: Single; AHipStream: Pointer): Integer; cdecl; external CG4SLib;
+function g4s_destroy(ASampler: PG4SSampler): Integer; cdecl; external CG4SLib;
+function g4s_last_error(ASampler: PG4SSampler): PAnsiChar; cdecl; external CG4SLib;
+function g4s_sample(ASampler: PG4SSampler; ADevLogits: Pointer; ADType: Integer;
+  ARowStride: Int64; ABatch: Integer; AParams: PG4SParams; AU: PDouble;
+  AIds: PInteger): Integer; cdecl; external CG4SLib;
+function g4s_sample_ex(ASampler: PG4SSampler; ADevLogits: Pointer; ADType: Integer;
+  ARowStride: Int64; ABatch: Integer; AParams: PG4SParams; AU: PDouble;
+  AIds: PInteger; AOutputs: PG4SOutputs): Integer; cdecl; external CG4SLib;
+function g4s_sample_async(ASampler: PG4SSampler; ADevLogits: Pointer; ADType: Integer;
+  ARowStride: Int64; ABatch: Integer; ADevParams: PG4SParams; ADevU: PDouble;
+  AKBound: Integer; AFullRows: Integer; ADevIds: PInteger;
+  AOutputs: PG4SOutputs): Integer; cdecl; external CG4SLib;
+function g4s_lmhead_q4_0(ASampler: PG4SSampler; ADevWeights: Pointer; ARows: Integer;
+  ACols: Integer; ADevHidden: PSingle; ABatch: Integer; ADevLogits: PSingle;
+  ALogitsStride: Int64): Integer; cdecl; external CG4SLib;
+
+type
+  { TGpuSampler }
+  // One sampler handle of a model: opened next to the GPU logits buffer
+  // (Model.pas:791-792) and closed with it (Model.pas:701-702).
+  TGpuSampler = class(TBaseObject)
+  private
+    FHandle: PG4SSampler;
+    FVocab: Integer;
+    FMaxBatch: Integer;
+    function Fail(const ACode: string; const AStatus: Integer): Boolean;
+  public
+    destructor Destroy(); override;
+
+    // g4s_create: the whole workspace is allocated here, never per call
+    function Open(const AVocab: Integer; const AMaxBatch: Integer;
+      const ASoftcap: Single; const AHipStream: Pointer = nil): Boolean;
+    procedure Close();
+
+    // DoSample on one GPU-resident logits row: u is the engine's Random, as
+    // at Model.pas:2726,2813.  False (and ATokenId = -1) on failure.
+    function Sample(const ADevLogits: Pointer; const ADType: Integer;
+      const AParams: PG4SParams; out ATokenId: Integer): Boolean;
+
+    // ABatch rows at ADevLogits + i*ARowStride elements; AParams, AU and
+    // AIds point at ABatch host entries each
+    function SampleBatch(const ADevLogits: Pointer; const ADType: Integer;
+      const ARowStride: Int64; const ABatch: Integer; const AParams: PG4SParams;
+      const AU: PDouble; const AIds: PInteger): Boolean;
+
+    // Q4_0 LM head straight into the buffer the sampler reads
+    function LmHeadQ4_0(const ADevWeights: Pointer; const ARows: Integer;
+      const ACols: Integer; const ADevHidden: PSingle; const ABatch: Integer;
+      const ADevLogits: PSingle; const ALogitsStride: Int64): Boolean;
+
+    function LastError(): string;
+
+    property Handle: PG4SSampler read FHandle;
+    property Vocab: Integer read FVocab;
+    property MaxBatch: Integer read FMaxBatch;
+  end;
+
+implementation
+
+{ TGpuSampler }
+
+destructor TGpuSampler.Destroy();
+begin
+  Close();
+  inherited;
+end;
+
+function TGpuSampler.LastError(): string;
+begin
+  Result := string(AnsiString(g4s_last_error(FHandle)));
+end;
+
+function TGpuSampler.Fail(const ACode: string; const AStatus: Integer): Boolean;
+begin
+  GetErrors().Add(esError, ACode, 'Sampler status %d: %s', [AStatus, LastError()]);
+  Result := False;
+end;
+
+function TGpuSampler.Open(const AVocab: Integer; const AMaxBatch: Integer;
+  const ASoftcap: Single; const AHipStream: Pointer): Boolean;
+var
+  LStatus: Integer;
+  LHandle: PG4SSampler;
+begin
+  Close();
+  LHandle := nil;
+  LStatus := g4s_create(@LHandle, AVocab, AMaxBatch, ASoftcap, AHipStream);
+  if LStatus <> G4S_OK then
+  begin
+    // g4s_last_error(nil) holds the message of the failed create
+    FHandle := nil;
+    Exit(Fail(CSM_ERR_CREATE, LStatus));
+  end;
+  FHandle := LHandle;
+  FVocab := AVocab;
+  FMaxBatch := AMaxBatch;
+  Result := True;
+end;
+
+procedure TGpuSampler.Close();
+begin
+  if FHandle <> nil then
+  begin
+    g4s_destroy(FHandle);
+    FHandle := nil;
+  end;
+end;
+
+function TGpuSampler.Sample(const ADevLogits: Pointer; const ADType: Integer;
+  const AParams: PG4SParams; out ATokenId: Integer): Boolean;
+var
+  LU: Double;
+  LId: Integer;
+  LStatus: Integer;
+begin
+  ATokenId := -1;
+  LU := Random;
+  LId := -1;
+  LStatus := g4s_sample(FHandle, ADevLogits, ADType, FVocab, 1, AParams, @LU, @LId);
+  if LStatus <> G4S_OK then
+    Exit(Fail(CSM_ERR_SAMPLE, LStatus));
+  ATokenId := LId;
+  Result := True;
+end;
+
+function TGpuSampler.SampleBatch(const ADevLogits: Pointer; const ADType: Integer;
+  const ARowStride: Int64; const ABatch: Integer; const AParams: PG4SParams;
+  const AU: PDouble; const AIds: PInteger): Boolean;
+var
+  LStatus: Integer;
+begin
+  LStatus := g4s_sample(FHandle, ADevLogits, ADType, ARowStride, ABatch, AParams, AU, AIds);
+  if LStatus <> G4S_OK then
+    Exit(Fail(CSM_ERR_SAMPLE, LStatus));
+  Result := True;
+end;
+
+function TGpuSampler.LmHeadQ4_0(const ADevWeights: Pointer; const ARows: Integer;
+  const ACols: Integer; const ADevHidden: PSingle; const ABatch: Integer;
+  const ADevLogits: PSingle; const ALogitsStride: Int64): Boolean;
+var
+  LStatus: Integer;
+begin
+  LStatus := g4s_lmhead_q4_0(FHandle, ADevWeights, ARows, ACols, ADevHidden, ABatch,
+    ADevLogits, ALogitsStride);
+  if LStatus <> G4S_OK then
+    Exit(Fail(CSM_ERR_LMHEAD, LStatus));
+  Result := True;
+end;
+
+end.

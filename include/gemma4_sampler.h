@@ -147,8 +147,12 @@ int g4s_sample_ex(g4s_sampler* sampler, const void* d_logits, int32_t dtype, int
  * (0 < TopK < V; k_bound 0 when no row takes the top-k path) sizes the
  * launch: above g4s_max_top_k() the wide top-k launches are added;
  * `full_rows` != 0 when some row may take the full-vocabulary path.  Rows
- * that violate k_bound get id -1 and G4S_FLAG_ERROR.  Returns after
- * enqueueing; results are valid once the stream reaches this point. */
+ * that violate k_bound get id -1 and G4S_FLAG_ERROR, and so does a row whose
+ * path is not enqueued: a full-vocabulary row when full_rows == 0
+ * (G4S_FLAG_ERROR | G4S_FLAG_FULL_PATH) or a top-k row when k_bound == 0
+ * (G4S_FLAG_ERROR | G4S_FLAG_TOPK_PATH); no row keeps an earlier call's id.
+ * Returns after enqueueing; results are valid once the stream reaches this
+ * point. */
 int g4s_sample_async(g4s_sampler* sampler, const void* d_logits, int32_t dtype,
                      int64_t row_stride, int32_t batch, const g4s_params* d_params,
                      const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,

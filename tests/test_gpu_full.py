@@ -30,11 +30,21 @@ def _widen(b16):
     return (np.asarray(b16, np.uint16).astype(np.uint32) << 16).view(F32)
 
 
-def check(orc, rows, t, k, p, u, ids, o, softcap, label, probs=False):
+def check(orc, rows, t, k, p, u, ids, o, softcap, label, probs=False, threads=1):
     boundary = 0
+
+    def ref(r):
+        return orc.do_sample(rows[r], t[r], k[r], p[r], u[r], softcap=softcap, want_probs=probs)
+
+    if threads > 1:
+        # the oracle call releases the GIL (ctypes), so rows run in parallel
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(threads) as ex:
+            refs = list(ex.map(ref, range(len(rows))))
+    else:
+        refs = None
     for r in range(len(rows)):
-        tok, det, _, pr = orc.do_sample(rows[r], t[r], k[r], p[r], u[r], softcap=softcap,
-                                        want_probs=probs)
+        tok, det, _, pr = refs[r] if refs is not None else ref(r)
         ctx = f"{label} row {r} (T={t[r]}, K={k[r]}, P={p[r]}, u={u[r]!r}, cap={softcap})"
         assert ids[r] == tok, f"{ctx}: gpu id {ids[r]} != oracle {tok}"
         if o is not None:
@@ -184,4 +194,26 @@ def test_async_full_matches_sync(orc):
     _, ids = s.sample(d, B, _params(t, k, p), u, dtype=native.DTYPE_BF16)
     assert np.array_equal(di.download(np.int32), ids)
     check(orc, _widen(b16), t, k, p, u, ids, None, CAP, "async-full")
+    s.close()
+
+
+@pytest.mark.parametrize("B", [128, 256])
+def test_flat_bf16_large_batches(orc, B):
+    """The flat worst case at the batch sizes whose streaming passes take 2
+    (B=128) and 4 (B=256) vocabulary chunks per wave: every id, LSum and
+    greedy id against the oracle, and at B=256 every probability of every row
+    (capacity >= V).  Boundary draws are counted and printed."""
+    b16 = wl.host_flat_bf16_rows(SEED + 10 + B, 0, B, V)
+    rows = _widen(b16)
+    t, k, p = wl.flat_params(B)
+    u = wl.host_row_u(SEED + 10 + B, 0, B)
+    s = native.Sampler(V, max_batch=B, softcap=CAP)
+    d = hip.Buffer.from_array(b16)
+    cap = V if B == 256 else 1
+    outs = native.DeviceOutputs(B, cap)
+    _, ids = s.sample(d, B, _params(t, k, p), u, dtype=native.DTYPE_BF16, outputs=outs.struct)
+    o = outs.read()
+    del outs
+    nb = check(orc, rows, t, k, p, u, ids, o, CAP, f"flat B={B}", probs=(cap == V), threads=16)
+    print(f"flat bf16 B={B}: {B} rows bit-exact, boundary draws (|u*P - cum| < 1e-6): {nb}")
     s.close()

@@ -281,3 +281,101 @@ def test_argument_errors_on_device(big):
     rc, _ = big.sample(d, 65, [native.TSamplingParams.make(1.0, 5, 0.9)] * 65, [0.5] * 65,
                        check=False)
     assert rc == native.G4S_ERR_INVALID_ARGUMENT
+
+
+def _heap_select(x, K, right_if_le=False):
+    """The reference's min-heap pass (Model.pas:2632-2676), used here only to
+    show that a planted row tells the child-tie rule apart: right_if_le=True
+    swaps the strict `<` of :2653-2654 for `<=`.  The oracle, pinned by hand
+    traces, stays the checker."""
+    hv = [F32(-1e30)] * K
+    hi = [-1] * K
+    xs = np.asarray(x, F32)
+    cand = np.nonzero(xs > F32(-1e30))[0]
+    for i in cand:
+        v = xs[i]
+        if v <= hv[0]:
+            continue
+        p = 0
+        while True:
+            c = 2 * p + 1
+            if c >= K:
+                break
+            if c + 1 < K and ((hv[c + 1] <= hv[c]) if right_if_le else (hv[c + 1] < hv[c])):
+                c += 1
+            if hv[c] >= v:
+                break
+            hv[p], hi[p] = hv[c], hi[c]
+            p = c
+        hv[p], hi[p] = v, int(i)
+    return sorted(i for i in hi if i >= 0)
+
+
+def test_heap_child_tie_full_size(big, orc):
+    """Full-size rows where the surviving tied copies depend on the heap's
+    child-tie rule (Model.pas:2653-2654): the 0,0,0,1,1 pattern (K=4) on an
+    excluded (-1e30) background and on a random background, and a wide row
+    (K=1500 > g4s_max_top_k) with 1000 ones and 1000 zeros scattered over a
+    random background.  Every row is checked to give a different survivor
+    set under `<=`, so a kernel using the wrong rule fails."""
+    rng = np.random.default_rng(2653)
+    rows = np.empty((3, V), F32)
+    rows[0] = F32(-1e30)
+    pos = np.sort(rng.choice(V, 5, replace=False))
+    rows[0][pos] = [0, 0, 0, 1, 1]
+    for attempt in range(50):
+        bg = (F32(-20) - np.abs(rng.normal(0, 1, V))).astype(F32)
+        pos1 = np.sort(rng.choice(V, 5, replace=False))
+        bg[pos1] = [0, 0, 0, 1, 1]
+        if _heap_select(bg, 4) != _heap_select(bg, 4, right_if_le=True):
+            break
+    rows[1] = bg
+    for attempt in range(50):
+        bg = (F32(-20) - np.abs(rng.normal(0, 1, V))).astype(F32)
+        pl = rng.choice(V, 2000, replace=False)
+        bg[pl[:1000]] = 1.0
+        bg[pl[1000:]] = 0.0
+        if _heap_select(bg, 1500) != _heap_select(bg, 1500, right_if_le=True):
+            break
+    rows[2] = bg
+    k = np.array([4, 4, 1500], np.int32)
+    t = np.array([0.7, 1.0, 1.0], F32)
+    p = np.array([0.95, 0.9, 0.99], F32)
+    u = np.array([0.3, 0.6, 0.45])
+    want_sets = [_heap_select(rows[r], int(k[r])) for r in range(3)]
+    for r in range(3):
+        assert want_sets[r] != _heap_select(rows[r], int(k[r]), right_if_le=True), \
+            f"row {r} does not tell the child-tie rules apart"
+        assert list(orc.select_topk_indices(rows[r], int(k[r]))) == want_sets[r], r
+    s = native.Sampler(V, max_batch=3, softcap=CAP)
+    d = hip.Buffer.from_array(rows)
+    outs = native.DeviceOutputs(3, 1500)
+    _, ids = s.sample(d, 3, _params(t, k, p), u, outputs=outs.struct)
+    o = outs.read()
+    check_rows(orc, rows, t, k, p, u, ids, o, label="child-tie")
+    for r in range(3):
+        assert list(o["indices"][r][:o["count"][r]]) == want_sets[r], r
+        assert o["flags"][r] & native.FLAG_HEAP_REPLAY, (r, hex(o["flags"][r]))
+    assert o["flags"][2] & native.FLAG_WIDE_K
+    s.close()
+
+
+def test_async_rejects_rows_whose_path_is_not_enqueued(big):
+    """g4s_sample_async with full_rows = 0 leaves no full-vocabulary row
+    with an earlier call's id, and k_bound = 0 none of the top-k rows: such
+    rows get id -1 and G4S_FLAG_ERROR plus the path they would have taken."""
+    rows = wl.host_peaky_rows(SEED, 0, 2, V)
+    d = hip.Buffer.from_array(rows)
+    for k_bound, full_rows, ks, bad, path in ((64, 0, [64, 0], 1, native.FLAG_FULL_PATH),
+                                              (0, 1, [0, 5], 1, native.FLAG_TOPK_PATH)):
+        parr = native.params_array(_params([0.7, 0.7], ks, [0.95, 0.95]))
+        dp = hip.Buffer(16 * 2)
+        hip.check(hip.lib().hipMemcpy(dp.ptr, parr, 32, hip.H2D))
+        du = hip.Buffer.from_array(np.array([0.5, 0.5]))
+        di = hip.Buffer.from_array(np.array([12345, 12345], np.int32))
+        outs = native.DeviceOutputs(2, 1)
+        big.sample_async(d, 2, dp, du, k_bound, full_rows, di, outputs=outs.struct)
+        hip.synchronize()
+        ids, fl = di.download(np.int32), outs.read()["flags"]
+        assert ids[bad] == -1 and fl[bad] & native.FLAG_ERROR and fl[bad] & path, (ids, fl)
+        assert ids[1 - bad] != 12345 and not (fl[1 - bad] & native.FLAG_ERROR), (ids, fl)

@@ -261,3 +261,71 @@ def test_matvec_q4_one_hot_and_ones(orc):
     got = orc.matvec_q4(w, ones, rows, cols)
     want = np.array([np.cumsum(deq[r], dtype=F32)[-1] for r in range(rows)], F32)
     assert np.array_equal(got, want)
+
+
+# ------------------------------------------- pins written out by hand
+def test_heap_child_tie_rule(orc):
+    # Hand trace of Model.pas:2632-2664 on [0,0,0,1,1], K=4.  The sift-down
+    # takes the right child only when it is strictly smaller
+    # (LHeapVal[LChild+1] < LHeapVal[LChild], :2653-2654):
+    #   after 0@0, 0@1, 0@2 the heap is [-1e30, (0,1), (0,2), (0,0)];
+    #   1@3: children (0,1), (0,2) tie -> left: heap [(0,1), (0,0), (0,2), (1,3)];
+    #   1@4: children (0,0), (0,2) tie -> left, then (1,3) >= 1 stops:
+    #        heap [(0,0), (1,4), (0,2), (1,3)]  -> indices {0,2,3,4}.
+    # Under `<=` the right child would be taken and the result is {0,1,3,4}.
+    assert list(orc.select_topk_indices([0, 0, 0, 1, 1], 4)) == [0, 2, 3, 4]
+    # [2,2,2,2,3,3] K=5: after the four 2s the heap is
+    # [-1e30, (2,2), (2,3), (2,0), (2,1)]; 3@4 walks the left children (2,2),
+    # (2,0): [(2,2), (2,0), (2,3), (3,4), (2,1)]; 3@5 goes left to (2,0),
+    # then right to the strictly smaller (2,1): [(2,0), (2,1), (2,3), (3,4),
+    # (3,5)] -> {0,1,3,4,5}.  Under `<=` the same row gives {1,2,3,4,5}.
+    assert list(orc.select_topk_indices([2, 2, 2, 2, 3, 3], 5)) == [0, 1, 3, 4, 5]
+
+
+# Q4_0 block = fp16 scale (little-endian) + 16 bytes; byte j holds element 2j
+# in its low nibble and element 2j+1 in its high nibble, value = nibble - 8
+# (Types.pas:139-142, Quant.pas:209-239, Tensors.pas:581-593).
+_HAND_BLOCK = bytes([0x00, 0x3C,                      # scale 1.0
+                     0x9A, 0x0F, 0xF0] + [0x88] * 13)
+_HAND_VALUES = [2.0, 1.0, 7.0, -8.0, -8.0, 7.0] + [0.0] * 26
+
+
+def test_q4_dequant_hand_built_blocks(orc):
+    blk = np.frombuffer(_HAND_BLOCK, np.uint8)
+    assert list(orc.dequant_q4_block(blk)) == _HAND_VALUES
+    half = np.frombuffer(bytes([0x00, 0x38]) + _HAND_BLOCK[2:], np.uint8)   # scale 0.5
+    assert list(orc.dequant_q4_block(half)) == [v * 0.5 for v in _HAND_VALUES]
+    neg = np.frombuffer(bytes([0x00, 0xB8]) + _HAND_BLOCK[2:], np.uint8)    # scale -0.5
+    assert list(orc.dequant_q4_block(neg)) == [v * -0.5 + 0.0 for v in _HAND_VALUES]
+
+
+def test_q4_quantize_bankers_round_and_interleave(orc):
+    # max |x| = 7 -> scale = 7/7 = 1 exactly, 1/scale = 1: Round(x) applies to
+    # x itself, and Delphi's Round sends exact halves to the even integer
+    x1 = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 6.5, 7.0, -7.0, 4.5, -3.5, 5.5, -5.5, 0.0, 1.0,
+          -6.5, 0.25, 0.75, -4.5, 2.0, -2.0, 3.0, -3.0, 4.0, -4.0, 5.0, -5.0, 6.0, -6.0, 0.4, -0.6]
+    # q = 0 2 2 0 -2 -2 4 6 7 -7 4 -4 6 -6 0 1 -6 0 1 -4 2 -2 3 -3 4 -4 5 -5 6 -6 0 -1
+    want1 = [0x00, 0x3C, 0xA8, 0x8A, 0x66, 0xEC, 0x1F, 0x4C, 0x2E, 0x98,
+             0x82, 0x49, 0x6A, 0x5B, 0x4C, 0x3D, 0x2E, 0x78]
+    # max |x| = 3.5 -> scale 0.5 (fp16 0x3800), 1/scale = 2: 0.25 -> Round(0.5) = 0,
+    # 0.75 -> Round(1.5) = 2, -0.75 -> -2, 1.25 -> Round(2.5) = 2, -1.25 -> -2
+    x2 = [3.5, 0.25, 0.75, -0.75, 1.25, -1.25] + [0.0] * 26
+    want2 = [0x00, 0x38, 0x8F, 0x6A, 0x6A] + [0x88] * 13
+    q = orc.f32_to_q4(np.array(x1 + x2, F32))
+    assert list(q[:18]) == want1
+    assert list(q[18:36]) == want2
+
+
+def test_matvec_q4_hand_values(orc):
+    cols = 32
+    w = np.frombuffer(_HAND_BLOCK + bytes([0x00, 0x3C, 0x99, 0x79] + [0x88] * 14), np.uint8)
+    # row 0: 2*1 + 1*10 + 7*100 - 8*1000 - 8*0.5 + 7*0.25 = -7290.25
+    h = np.zeros(cols, F32)
+    h[:6] = [1, 10, 100, 1000, 0.5, 0.25]
+    assert orc.matvec_q4(w, h, 2, cols)[0] == F32(-7290.25)
+    # row 1 (q = 1, 1, 1, -1) with h = (2^24, 1, 1, 2^24): the left-to-right
+    # binary32 sum is ((2^24 + 1) + 1) - 2^24 = 0 (each +1 is a tie that
+    # rounds to the even 2^24); a pairwise sum would give 1, a reversed one 2
+    h = np.zeros(cols, F32)
+    h[:4] = [2.0 ** 24, 1.0, 1.0, 2.0 ** 24]
+    assert orc.matvec_q4(w, h, 2, cols)[1] == F32(0.0)

@@ -1,0 +1,186 @@
+"""The Pascal binding unit (gemma4.pas_amd/pascal/Gemma4.Sampler.pas) against
+the C header (include/gemma4_sampler.h) and the built library, on the CPU.
+
+No Pascal compiler exists in this image, so the unit is checked by reading
+it: every `external` declaration must name an export of the header with the
+same number, order and C types of arguments (a Pascal value parameter of a
+pointer type is the C pointer; `const`, `var` and `out` parameters are
+refused, since how a compiler passes them is not the C ABI), the records must
+have the C structs' fields in order, and every constant must equal the
+header's.  Then every export is called through ctypes with argument types
+derived from the Pascal declaration, on paths that need no GPU.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+UNIT = os.path.join(ROOT, "gemma4.pas_amd", "pascal", "Gemma4.Sampler.pas")
+HEADER = os.path.join(ROOT, "include", "gemma4_sampler.h")
+
+# Pascal type -> canonical C type
+PAS2C = {
+    "Integer": "int32_t", "Int64": "int64_t", "Single": "float", "Double": "double",
+    "Cardinal": "uint32_t", "Pointer": "void*", "PAnsiChar": "char*",
+    "PG4SSampler": "g4s_sampler*", "PPG4SSampler": "g4s_sampler**",
+    "PG4SParams": "g4s_params*", "PG4SOutputs": "g4s_outputs*", "PDouble": "double*",
+    "PInteger": "int32_t*", "PSingle": "float*", "PCardinal": "uint32_t*",
+}
+# canonical C type -> ctypes type
+C2CT = {
+    "int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
+    "double": ctypes.c_double, "uint32_t": ctypes.c_uint32, "char*": ctypes.c_char_p,
+    None: None,
+}
+
+
+def _strip_pascal_comments(s):
+    s = re.sub(r"\{.*?\}", "", s, flags=re.S)
+    s = re.sub(r"\(\*.*?\*\)", "", s, flags=re.S)
+    return re.sub(r"//[^\n]*", "", s)
+
+
+def _strip_c_comments(s):
+    s = re.sub(r"/\*.*?\*/", "", s, flags=re.S)
+    return re.sub(r"//[^\n]*", "", s)
+
+
+def _canon_c(t):
+    t = t.replace("const", " ")
+    t = re.sub(r"\s*\*\s*", "*", t)
+    t = re.sub(r"\s+", " ", t).strip()
+    return "int32_t" if t == "int" else t  # C int is 32 bits on LP64 Linux
+
+
+def pascal_externals():
+    src = _strip_pascal_comments(open(UNIT).read())
+    decls = {}
+    pat = re.compile(r"\b(function|procedure)\s+(g4s_\w+)\s*\((.*?)\)\s*(?::\s*(\w+))?\s*;"
+                     r"\s*cdecl\s*;\s*external\s+CG4SLib\s*;", re.S)
+    for kind, name, args, ret in pat.findall(src):
+        params = []
+        for group in [g.strip() for g in args.split(";") if g.strip()]:
+            assert not re.match(r"(const|var|out)\b", group), \
+                f"{name}: parameter '{group}' is not passed by value"
+            names, typ = group.split(":")
+            for _ in names.split(","):
+                params.append(PAS2C[typ.strip()])
+        decls[name] = (PAS2C[ret] if kind == "function" else "void", params)
+    return decls
+
+
+def header_prototypes():
+    src = _strip_c_comments(open(HEADER).read())
+    protos = {}
+    for ret, name, args in re.findall(r"([A-Za-z_][\w \*]*?)\s*\b(g4s_\w+)\s*\(([^)]*)\)\s*;",
+                                      src):
+        params = []
+        if args.strip() not in ("", "void"):
+            for a in args.split(","):
+                a = a.strip()
+                m = re.match(r"(.*?)(\w+)$", a)
+                params.append(_canon_c(m.group(1)))
+        protos[name] = (_canon_c(ret), params)
+    return protos
+
+
+def c_struct_fields(name):
+    src = _strip_c_comments(open(HEADER).read())
+    body = re.search(r"typedef struct %s \{(.*?)\}" % name, src, re.S).group(1)
+    return [(_canon_c(m.group(1)), m.group(2))
+            for m in re.finditer(r"([\w \*]+?)\s*\b(\w+)\s*;", body)]
+
+
+def pascal_record_fields(name):
+    src = _strip_pascal_comments(open(UNIT).read())
+    body = re.search(r"\b%s\s*=\s*record(.*?)\bend;" % name, src, re.S).group(1)
+    out = []
+    for line in [x.strip() for x in body.split(";") if x.strip()]:
+        fname, typ = [x.strip() for x in line.split(":")]
+        out.append((PAS2C[typ], fname))
+    return out
+
+
+def test_every_external_matches_the_header():
+    pas, hdr = pascal_externals(), header_prototypes()
+    assert set(pas) == set(hdr), (set(pas) ^ set(hdr))
+    for name in hdr:
+        assert pas[name] == hdr[name], f"{name}: Pascal {pas[name]} vs C {hdr[name]}"
+
+
+@pytest.mark.parametrize("c_name,p_name", [("g4s_params", "TG4SParams"),
+                                            ("g4s_outputs", "TG4SOutputs")])
+def test_records_match_the_structs(c_name, p_name):
+    c = c_struct_fields(c_name)
+    p = pascal_record_fields(p_name)
+    assert [t for t, _ in p] == [t for t, _ in c], (p, c)
+    # same field names up to case and underscores
+    assert [n.lower() for _, n in p] == [n.replace("_", "").lower() for _, n in c]
+
+
+def test_constants_match_the_header():
+    hsrc = _strip_c_comments(open(HEADER).read())
+    want = {m.group(1): int(m.group(2), 0)
+            for m in re.finditer(r"#define\s+(G4S_\w+)\s+(0x[0-9a-fA-F]+|\d+)u?", hsrc)}
+    for m in re.finditer(r"\b(G4S_\w+)\s*=\s*(-?\d+)", hsrc):
+        want[m.group(1)] = int(m.group(2))
+    psrc = _strip_pascal_comments(open(UNIT).read())
+    got = {}
+    for m in re.finditer(r"\b(G4S_\w+)\s*=\s*(-?\$?[0-9A-Fa-f]+)\s*;", psrc):
+        v = m.group(2)
+        got[m.group(1)] = int(v.replace("$", "0x"), 0) if "$" in v else int(v)
+    assert set(got) == set(want), set(got) ^ set(want)
+    for k in want:
+        assert got[k] == want[k], k
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from gemma4_sampler import native
+    return ctypes.CDLL(native.LIB_PATH)
+
+
+def _bind(lib, decls, name):
+    ret, params = decls[name]
+    f = getattr(lib, name)
+    f.restype = C2CT.get(ret) if ret != "void" else None
+    f.argtypes = [C2CT[p] if p in C2CT else ctypes.c_void_p for p in params]
+    return f
+
+
+def test_call_every_export_with_the_declared_shapes(lib):
+    """No GPU here: create reports G4S_ERR_NO_DEVICE, the sampling and LM-head
+    entry points reject a nil handle with G4S_ERR_INVALID_ARGUMENT, and the
+    pure host exports answer."""
+    d = pascal_externals()
+    f = {n: _bind(lib, d, n) for n in d}
+    assert f["g4s_version"]().decode().startswith("gemma4_sampler")
+    assert f["g4s_max_top_k"]() == 1024
+
+    class Params(ctypes.Structure):
+        _fields_ = [("Temperature", ctypes.c_float), ("TopK", ctypes.c_int32),
+                    ("TopP", ctypes.c_float), ("RepetitionPenalty", ctypes.c_float)]
+    p = Params(0.0, 0, 0.0, 0.0)
+    f["g4s_params_set_defaults"](ctypes.addressof(p))
+    assert (p.Temperature, p.TopK, round(p.TopP, 6), p.RepetitionPenalty) == (1.0, 64, 0.95, 1.0)
+
+    h = ctypes.c_void_p(0)
+    rc = f["g4s_create"](ctypes.addressof(h), 262144, 1, 30.0, None)
+    assert rc in (-3, 0)  # NO_DEVICE here; OK where a GPU is visible
+    if rc != 0:
+        assert h.value is None
+        assert len(f["g4s_last_error"](None)) > 0
+    u = ctypes.c_double(0.5)
+    ids = ctypes.c_int32(-7)
+    assert f["g4s_sample"](None, None, 0, 262144, 1, ctypes.addressof(p), ctypes.addressof(u),
+                           ctypes.addressof(ids)) == -1
+    assert f["g4s_sample_ex"](None, None, 0, 262144, 1, ctypes.addressof(p),
+                              ctypes.addressof(u), ctypes.addressof(ids), None) == -1
+    assert f["g4s_sample_async"](None, None, 0, 262144, 1, None, None, 64, 0, None, None) == -1
+    assert f["g4s_lmhead_q4_0"](None, None, 262144, 2560, None, 1, None, 262144) == -1
+    assert f["g4s_last_error"](None).decode() == "sampler is NULL"
+    if rc == 0:
+        assert f["g4s_destroy"](h) == 0
+    assert f["g4s_destroy"](None) == 0
