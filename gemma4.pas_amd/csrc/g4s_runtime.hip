@@ -18,6 +18,7 @@
 
 #include "g4s_full.h"
 #include "g4s_lmhead.h"
+#include "g4s_runtime.h"
 #include "g4s_topk.h"
 
 #define G4S_API extern "C" __attribute__((visibility("default")))
@@ -27,6 +28,23 @@ namespace {
 thread_local std::string g_create_error;
 
 }  // namespace
+
+namespace g4s {
+
+int set_null_handle_error(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_create_error = buf;
+    return code;
+}
+
+void clear_null_handle_error() { g_create_error.clear(); }
+
+}  // namespace g4s
 
 struct g4s_sampler {
     int device = 0;

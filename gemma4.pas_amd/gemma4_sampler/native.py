@@ -42,7 +42,7 @@ FLAG_ERROR = 0x80000000
 
 EXPORTS = ("g4s_version", "g4s_params_set_defaults", "g4s_max_top_k", "g4s_create",
            "g4s_destroy", "g4s_last_error", "g4s_sample", "g4s_sample_ex", "g4s_sample_async",
-           "g4s_lmhead_q4_0")
+           "g4s_sample_topk_noalloc", "g4s_lmhead_q4_0")
 
 
 class TSamplingParams(ctypes.Structure):
@@ -100,8 +100,33 @@ def load():
         L.g4s_lmhead_q4_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
                                       ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                       ctypes.c_void_p, ctypes.c_int64]
+        L.g4s_sample_topk_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                              ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
+                                              ctypes.c_void_p, ctypes.c_int32, ctypes.c_float,
+                                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         _lib = L
     return _lib
+
+
+NOALLOC_MAX_ROWS = 32
+NOALLOC_SCRATCH_BYTES = 8585472
+
+
+def sample_topk_noalloc(d_logits, batch, d_params, d_u, k_bound, d_ids, vocab,
+                        dtype=DTYPE_F32, row_stride=None, softcap=30.0, outputs=None,
+                        stream=None, check=True):
+    """g4s_sample_topk_noalloc: the handle-free top-k path whose workspace is
+    a fixed device array; returns the status (raises unless check=False)."""
+    L = load()
+    stride = vocab if row_stride is None else int(row_stride)
+    rc = L.g4s_sample_topk_noalloc(_ptr(d_logits), int(dtype), int(vocab), stride, int(batch),
+                                   _ptr(d_params), _ptr(d_u), int(k_bound), float(softcap),
+                                   _ptr(d_ids),
+                                   ctypes.byref(outputs) if outputs is not None else None,
+                                   stream.handle if stream is not None else None)
+    if check and rc != G4S_OK:
+        raise SamplerError(rc, L.g4s_last_error(None).decode())
+    return rc
 
 
 def version():

@@ -61,6 +61,10 @@ const
   G4S_FLAG_EMPTY = $40000000;
   G4S_FLAG_ERROR = $80000000;
 
+  // g4s_sample_topk_noalloc: rows per call and bytes of its device array
+  G4S_NOALLOC_MAX_ROWS = 32;
+  G4S_NOALLOC_SCRATCH_BYTES = 8585472;
+
 type
   { PG4SSampler }
   // opaque g4s_sampler*
@@ -110,6 +114,12 @@ function g4s_sample_async(ASampler: PG4SSampler; ADevLogits: Pointer; ADType: In
   ARowStride: Int64; ABatch: Integer; ADevParams: PG4SParams; ADevU: PDouble;
   AKBound: Integer; AFullRows: Integer; ADevIds: PInteger;
   AOutputs: PG4SOutputs): Integer; cdecl; external CG4SLib;
+// no counterpart in the engine: for callers that cannot allocate GPU memory
+// (graph capture, serving loops); no handle, errors via g4s_last_error(nil)
+function g4s_sample_topk_noalloc(ADevLogits: Pointer; ADType: Integer; AVocab: Integer;
+  ARowStride: Int64; ABatch: Integer; ADevParams: PG4SParams; ADevU: PDouble;
+  AKBound: Integer; ASoftcap: Single; ADevIds: PInteger; AOutputs: PG4SOutputs;
+  AHipStream: Pointer): Integer; cdecl; external CG4SLib;
 function g4s_lmhead_q4_0(ASampler: PG4SSampler; ADevWeights: Pointer; ARows: Integer;
   ACols: Integer; ADevHidden: PSingle; ABatch: Integer; ADevLogits: PSingle;
   ALogitsStride: Int64): Integer; cdecl; external CG4SLib;

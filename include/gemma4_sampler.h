@@ -121,7 +121,8 @@ int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, float softca
 int g4s_destroy(g4s_sampler* sampler);
 
 /* Message of the most recent failure on this handle ("" if none).  With a
- * NULL handle, the message of the most recent failed g4s_create. */
+ * NULL handle, the message of the most recent failed g4s_create or
+ * g4s_sample_topk_noalloc on the calling thread. */
 const char* g4s_last_error(const g4s_sampler* sampler);
 
 /* Sample `batch` rows synchronously.  Replaces TModel.DoSample
@@ -157,6 +158,33 @@ int g4s_sample_async(g4s_sampler* sampler, const void* d_logits, int32_t dtype,
                      int64_t row_stride, int32_t batch, const g4s_params* d_params,
                      const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,
                      const g4s_outputs* outputs);
+
+/* Rows and bytes of the device scratch array behind g4s_sample_topk_noalloc
+ * (held by every GPU the library runs on until the process ends). */
+#define G4S_NOALLOC_MAX_ROWS 32
+#define G4S_NOALLOC_SCRATCH_BYTES 8585472
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the top-k path of g4s_sample_async without a handle,
+ * with its workspace in a fixed device array of G4S_NOALLOC_SCRATCH_BYTES
+ * per GPU instead of memory allocated by g4s_create.  Calls no hipMalloc,
+ * hipFree or allocating library routine.
+ *   d_logits, dtype, row_stride  as for g4s_sample_async (`vocab` logits per row)
+ *   batch      1 .. G4S_NOALLOC_MAX_ROWS; larger batches are rejected
+ *   d_params, d_u, d_ids  device arrays of `batch` entries
+ *   k_bound    1 .. min(g4s_max_top_k(), vocab - 1), >= every row's TopK
+ *   softcap    final_logit_softcapping (<= 0 disables it)
+ *   outputs    optional device outputs, as for g4s_sample_ex
+ *   hip_stream the stream the work is enqueued on (NULL = default stream)
+ * Rows whose TopK is <= 0, >= vocab or above k_bound get id -1 and
+ * G4S_FLAG_ERROR.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU race, so run one at a time per device.  Returns after
+ * enqueueing; failures are reported by g4s_last_error(NULL). */
+int g4s_sample_topk_noalloc(const void* d_logits, int32_t dtype, int32_t vocab,
+                            int64_t row_stride, int32_t batch, const g4s_params* d_params,
+                            const double* d_u, int32_t k_bound, float softcap, int32_t* d_ids,
+                            const g4s_outputs* outputs, void* hip_stream);
 
 /* LM head for the sampler's config-5 workload: logits = W * h for `batch`
  * hidden vectors, with W in the engine's Q4_0 layout (TQ4Block rows,
