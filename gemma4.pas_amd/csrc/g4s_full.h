@@ -90,6 +90,45 @@ struct TieRec {
     int32_t pad;
 };
 
+/* Streaming pipeline of full bf16 rows (g4s_fullbf.hip). */
+constexpr int kBfTab = 8192;       /* e / p table: 32 binades of |x| x 128 mantissas x 2 signs */
+constexpr int kBfWin = 32;         /* binades of |x| in the table */
+constexpr int kBfStage = 16;       /* chunks per row staged for a chain */
+constexpr int kBfBlock = 512;      /* threads of the table-lookup passes */
+constexpr int kBfMaxChunks = 1024; /* chunks per row: vocab <= 2^20 */
+
+/* Per-row words of the streaming pipeline that several workgroups update. */
+struct FbRow {
+    uint32_t kmax;  /* largest key of the row (atomic max, max pass) */
+    uint32_t amax;  /* largest |x| of the row as binary32 bits (atomic max, max pass) */
+    uint32_t key1;  /* smallest order key of a code whose e is 1 (atomic min) */
+    int32_t amx;    /* first index whose key >= key1: the argmax of p (atomic min) */
+    float s0;       /* LSum after chunk 0, exact */
+    float c0;       /* the draw's running sum after chunk 0, exact (when hit0 < 0) */
+    int32_t hit0;   /* first index of chunk 0 whose running sum reaches thr, -1: none */
+    int32_t nsl;    /* chunks staged for the LSum chain */
+    int32_t nsc;    /* chunks staged for the draw chain */
+    /* the terms of codes outside the table: -inf, +inf, and every code below
+     * the table's binades when they share one value (NaN: they do not) --
+     * e (row kernel), then p (LSum chain) */
+    float e_ninf, e_pinf, e_tiny;
+    float p_ninf, p_pinf, p_tiny;
+    int32_t pad;
+};
+static_assert(sizeof(FbRow) == 64, "FbRow layout");
+
+/* A chunk staged for a chain (a predicted binade crossing): its lane maps
+ * in binade b and b + 1 and its 1024 terms (lane l's 16 at l*16). */
+struct BfStage {
+    ss::PMap lo[64];
+    ss::PMap hi[64];
+    int32_t b;
+    int32_t chunk;
+    int32_t pad[2];
+    float t[kFullChunk];
+};
+static_assert(sizeof(BfStage) % 16 == 0, "BfStage copies in 16-byte units");
+
 struct FullWorkspace {
     FullRow* rows = nullptr;     /* [max_batch] */
     FullChunk* chunks = nullptr; /* [max_batch][cstride] */
@@ -108,6 +147,14 @@ struct FullWorkspace {
     uint32_t* bits = nullptr;    /* [max_batch][ceil(vocab/32)] surviving tied copies */
     float* heap_v = nullptr;     /* [vocab] replay heap (one row at a time) */
     int32_t* heap_i = nullptr;   /* [vocab] */
+    /* streaming pipeline of full bf16 rows */
+    float* ytab = nullptr;       /* [65536] y = softcap(x) of every bf16 code (full-row form) */
+    FbRow* fbrow = nullptr;      /* [max_batch] */
+    float* etab8 = nullptr;      /* [max_batch][kBfTab] e of the tabulated codes */
+    float* ptab8 = nullptr;      /* [max_batch][kBfTab] p of the same codes */
+    BfStage* stage = nullptr;    /* [max_batch][kBfStage] staged chunks (LSum, then the draw) */
+    float* cpost = nullptr;      /* [max_batch][cstride] exact LSum after every chunk */
+    float* head = nullptr;       /* [max_batch][kFullChunk] e of every row's chunk 0 */
     int32_t bits_stride = 0;     /* words per row of `bits` */
     int32_t cstride = 0;         /* chunk records per row (= chunks of the vocabulary) */
 };
@@ -138,8 +185,15 @@ struct FullArgs {
 
 hipError_t full_alloc(FullWorkspace& ws, int32_t vocab, int32_t max_batch);
 void full_free(FullWorkspace& ws);
-hipError_t full_init(FullWorkspace& ws, int32_t max_batch, hipStream_t s);
+hipError_t full_init(FullWorkspace& ws, int32_t max_batch, float softcap, hipStream_t s);
 bool full_supported(int32_t vocab);
+
+/* The streaming pipeline (g4s_fullbf.hip): full bf16 rows of a batch
+ * without wide rows, vocab a multiple of kFullChunk up to kBfMaxChunks
+ * chunks. */
+bool fb_supported(int32_t vocab);
+hipError_t fb_init(FullWorkspace& ws, int32_t max_batch, float softcap, hipStream_t s);
+hipError_t fb_launch(const FullArgs& a, hipStream_t s);
 hipError_t full_launch(const FullArgs& a, int dtype, hipStream_t s);
 
 }  // namespace g4s

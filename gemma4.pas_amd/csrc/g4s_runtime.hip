@@ -300,7 +300,7 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
      * start below the first sequence value */
     std::memset(s->h_done, 0, mb * sizeof(uint32_t));
     hipError_t e = hipMemsetAsync(s->tickets, 0, mb * sizeof(uint32_t), s->stream);
-    if (e == hipSuccess) e = g4s::full_init(s->full, max_batch, s->stream);
+    if (e == hipSuccess) e = g4s::full_init(s->full, max_batch, softcap, s->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) {
         release(s);

@@ -1,0 +1,135 @@
+"""GPU parity of the streaming pipeline of full bf16 rows (vocabulary a
+multiple of 1024) in its rare regimes, against the CPU oracle through the C
+ABI: codes outside the per-row table of e (infinities, codes far below the
+row's largest |x|, with and without one shared value), rows whose set of
+codes with e == 1 reaches below the table, masked rows, +inf maxima, and the
+probabilities of every code.
+
+The reference path is CpuLogitSoftcap + DoSampleTopP + CpuSoftmaxF32
+(src/Gemma4.Layers.pas:300-316, src/Gemma4.Model.pas:2691-2737,
+src/Gemma4.Tensors.pas:638-673).  Ids, LSum, the greedy id and the
+probabilities must equal the oracle's bit for bit.
+"""
+import numpy as np
+import pytest
+
+from gemma4_sampler import hip, native, workload as wl
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+V = wl.V_GEMMA4
+CAP = wl.SOFTCAP_GEMMA4
+
+
+def _b16(x):
+    """Round-to-nearest-even bf16 codes of float32 values (NaN-free input)."""
+    b = np.asarray(x, F32).view(np.uint32).astype(np.uint64)
+    r = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
+
+
+def _widen(codes):
+    return (codes.astype(np.uint32) << 16).view(F32)
+
+
+def _run(orc, codes, t, k, p, u, softcap, probs):
+    B = codes.shape[0]
+    s = native.Sampler(V, max_batch=B, softcap=softcap)
+    d = hip.Buffer.from_array(np.ascontiguousarray(codes))
+    params = [native.TSamplingParams.make(float(a), int(b), float(c)) for a, b, c in zip(t, k, p)]
+    outs = native.DeviceOutputs(B, V if probs else 1)
+    _, ids = s.sample(d, B, params, u, outputs=outs.struct, dtype=native.DTYPE_BF16)
+    o = outs.read()
+    rows = _widen(codes)
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(8) as ex:
+        refs = list(ex.map(lambda r: orc.do_sample(rows[r], t[r], k[r], p[r], u[r], softcap=softcap,
+                                                   want_probs=probs), range(B)))
+    for r in range(B):
+        tok, det, _, pr = refs[r]
+        ctx = f"row {r} (T={t[r]}, K={k[r]}, P={p[r]}, u={u[r]!r}, cap={softcap})"
+        assert ids[r] == tok, f"{ctx}: gpu id {ids[r]} != oracle {tok}"
+        assert o["flags"][r] & native.FLAG_FULL_PATH, ctx
+        assert o["lsum"][r].view(np.uint32) == np.float32(det["lsum"]).view(np.uint32), \
+            f"{ctx}: lsum {o['lsum'][r]!r} != {det['lsum']!r}"
+        assert o["argmax"][r] == det["argmax_pos"], f"{ctx}: argmax {o['argmax'][r]} != {det['argmax_pos']}"
+        if probs:
+            assert np.array_equal(o["probs"][r].view(np.uint32), pr.view(np.uint32)), f"{ctx}: probs"
+    s.close()
+
+
+def _settings(rng, B):
+    t = rng.choice([1.0, 0.7, 1.3], B).astype(F32)
+    k = rng.choice([0, -1, V], B).astype(np.int32)
+    p = rng.choice([0.9, 0.99, 1.0], B).astype(F32)
+    u = np.floor(rng.random(B) * 2**32) / 2**32
+    return t, k, p, u
+
+
+@pytest.mark.parametrize("softcap", [CAP, 0.0])
+@pytest.mark.parametrize("probs", [False, True])
+def test_tiny_codes_and_zeros(orc, softcap, probs):
+    """N(0, 0.5^2) rows with planted +-0, subnormal and far-below codes (below
+    the table's 32 binades of |x|): they share one e, so the streaming passes
+    take it from the row's constants."""
+    rng = np.random.default_rng(11 + int(softcap) + 2 * probs)
+    B = 4
+    codes = _b16(rng.normal(0, 0.5, (B, V)))
+    for r in range(B):
+        pos = rng.choice(V, 600, replace=False)
+        codes[r, pos[:100]] = 0x0000
+        codes[r, pos[100:200]] = 0x8000
+        codes[r, pos[200:300]] = rng.integers(1, 0x80, 100)            # +subnormals
+        codes[r, pos[300:400]] = 0x8000 | rng.integers(1, 0x80, 100)   # -subnormals
+        codes[r, pos[400:600]] = _b16(rng.choice([1e-20, -3e-25, 2e-30, -1e-33], 200))
+    _run(orc, codes, *_settings(rng, B), softcap, probs)
+
+
+@pytest.mark.parametrize("softcap", [CAP, 0.0])
+def test_masked_rows(orc, softcap):
+    """Rows with -inf at 5 % and 50 % of the positions (masked logits): the
+    table follows the largest finite |x|, -inf takes e(-inf)."""
+    rng = np.random.default_rng(21 + int(softcap))
+    B = 4
+    codes = _b16(rng.normal(0, 0.5, (B, V)))
+    for r in range(B):
+        frac = 0.05 if r % 2 == 0 else 0.5
+        codes[r, rng.random(V) < frac] = 0xFF80
+    _run(orc, codes, *_settings(rng, B), softcap, probs=(softcap > 0))
+
+
+def test_plus_inf_maxima(orc):
+    """+inf logits under the softcap (y = cap): e(+inf) == 1, the argmax is the
+    first +inf, which lies outside the table."""
+    rng = np.random.default_rng(31)
+    B = 3
+    codes = _b16(rng.normal(0, 2.0, (B, V)))
+    for r in range(B):
+        codes[r, rng.choice(V, 3 + r, replace=False)] = 0x7F80
+    t, k, p, u = _settings(rng, B)
+    t[:] = 1.0
+    _run(orc, codes, t, k, p, u, CAP, probs=True)
+
+
+def test_all_tiny_rows(orc):
+    """Every logit within 1e-30 of 0: every e rounds to 1 near the maximum,
+    and the codes with e == 1 reach the bottom of the table (every chunk is
+    searched for the argmax); T <= 0 rows take the greedy id."""
+    rng = np.random.default_rng(41)
+    B = 4
+    codes = _b16(rng.normal(0, 1e-31, (B, V)))
+    t, k, p, u = _settings(rng, B)
+    t[0] = 0.0
+    _run(orc, codes, t, k, p, u, CAP, probs=True)
+
+
+def test_below_table_codes_that_differ(orc):
+    """A row whose largest |x| is far larger than the rest (-1e6 among
+    N(0, 0.01^2)): codes below the table's binades have different e, so the
+    chunks holding them are left to the chains' exact re-evaluation."""
+    rng = np.random.default_rng(51)
+    B = 2
+    codes = _b16(rng.normal(0, 0.01, (B, V)))
+    codes[:, 12345] = _b16(np.float32(-1e6))
+    t, k, p, u = _settings(rng, B)
+    _run(orc, codes, t, k, p, u, CAP, probs=False)
