@@ -431,21 +431,13 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
 
     /* the terms of codes outside the table: e(-inf), e(+inf), and the codes
      * below its binades -- e is monotone in x, so when the largest negative and
-     * the largest positive one give the same e, every code between does */
-    if (tid == 0) {
-        fr->e_ninf = bf_e(ytab, 0xFF80u, scale, inv_t, m);
-        fr->e_pinf = bf_e(ytab, 0x7F80u, scale, inv_t, m);
-        float et = __builtin_nanf("");
-        if (win > 0) {
-            const uint32_t top = ((uint32_t)win << 7) - 1u;
-            const float en = bf_e(ytab, 0x8000u | top, scale, inv_t, m);
-            const float ep = bf_e(ytab, top, scale, inv_t, m);
-            if (en == ep) et = ep;
-        }
-        fr->e_tiny = et;
-        /* infinities with e == 1 hold the argmax's value too */
-        if (fr->e_pinf == 1.0f) atomicMin(&fr->key1, f2key(__builtin_inff()));
-        if (fr->e_ninf == 1.0f) atomicMin(&fr->key1, f2key(-__builtin_inff()));
+     * the largest positive one give the same e, every code between does
+     * (threads 0-3, one evaluation each; combined after the barriers below) */
+    __shared__ float s_out[4];
+    if (tid < 4) {
+        const uint32_t top = win > 0 ? ((uint32_t)win << 7) - 1u : 0u;
+        const uint32_t code = tid == 0 ? 0xFF80u : (tid == 1 ? 0x7F80u : (tid == 2 ? 0x8000u | top : top));
+        s_out[tid] = bf_e(ytab, code, scale, inv_t, m);
     }
 
     /* chunk 0: e of terms 4*tid .. 4*tid+3, its first e == 1 */
@@ -528,6 +520,13 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
         }
     }
     if (tid == 0) {
+        const float en = s_out[0], ep = s_out[1];
+        fr->e_ninf = en;
+        fr->e_pinf = ep;
+        fr->e_tiny = (win > 0 && s_out[2] == s_out[3]) ? s_out[3] : __builtin_nanf("");
+        /* infinities with e == 1 hold the argmax's value too */
+        if (ep == 1.0f) atomicMin(&fr->key1, f2key(__builtin_inff()));
+        if (en == 1.0f) atomicMin(&fr->key1, f2key(-__builtin_inff()));
         FullRow r;
         r.maxkey = km;
         r.amax = am;
@@ -572,7 +571,7 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
 
 /* ------------------------------------------ 3 and 5: chunk maps (e, then p) */
 
-constexpr int kRing = 3; /* chunks a wave keeps in flight */
+constexpr int kRing = 2; /* chunks a wave keeps in flight */
 
 /* Chunks per wave of the table-lookup passes: three times the max pass's
  * runs, so that a 256-chunk row takes three 512-thread workgroups and the
@@ -786,20 +785,15 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(1, 6))
         w[0] = src[0];
         w[1] = src[1];
     };
-    uint4 w0[2], w1[2], w2[2];
+    uint4 w0[2], w1[2];
     load(w0, cw);
     if (1 < n) load(w1, cw + 1);
-    if (2 < n) load(w2, cw + 2);
     for (int q = 0; q < n; q += kRing) {
         maps_chunk<P, ALL>(R, w0, q);
         if (q + kRing < n) load(w0, cw + q + kRing);
         if (q + 1 < n) {
             maps_chunk<P, ALL>(R, w1, q + 1);
             if (q + 1 + kRing < n) load(w1, cw + q + 1 + kRing);
-        }
-        if (q + 2 < n) {
-            maps_chunk<P, ALL>(R, w2, q + 2);
-            if (q + 2 + kRing < n) load(w2, cw + q + 2 + kRing);
         }
     }
 }
