@@ -108,9 +108,15 @@ class Buffer:
 
 
 class Stream:
-    def __init__(self):
+    def __init__(self, nonblocking=False):
+        """A HIP stream (default priority); nonblocking: hipStreamNonBlocking,
+        no implicit ordering with the null stream."""
         self.handle = ctypes.c_void_p()
-        check(lib().hipStreamCreate(ctypes.byref(self.handle)), "hipStreamCreate")
+        if nonblocking:
+            check(lib().hipStreamCreateWithFlags(ctypes.byref(self.handle), ctypes.c_uint(1)),
+                  "hipStreamCreateWithFlags")
+        else:
+            check(lib().hipStreamCreate(ctypes.byref(self.handle)), "hipStreamCreate")
 
     def synchronize(self):
         check(lib().hipStreamSynchronize(self.handle), "hipStreamSynchronize")

@@ -80,6 +80,46 @@ G4H_API int g4h_null_roundtrip(void* stream, int32_t n, int32_t mode, double* us
 }
 
 /*
+ * The floor of a one-kernel hipGraph launch on this stream, measured as the
+ * graph leg of the decode stream measures the sampler (g4h_graph_decode): a
+ * graph holding one launch of a null kernel, captured once, launched `n`
+ * times from an idle stream, each launch between two events; gpu_us[i] =
+ * event time of launch i.
+ */
+G4H_API int g4h_graph_floor(void* stream, int32_t n, float* gpu_us)
+{
+    hipStream_t st = (hipStream_t)stream;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t gx = nullptr;
+    int rc = 0;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) rc = -101;
+    if (rc == 0 && hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        rc = -102;
+    if (rc == 0) {
+        hipLaunchKernelGGL(g4h_null_kernel, dim3(1), dim3(64), 0, st, nullptr, 1u);
+        if (hipStreamEndCapture(st, &g) != hipSuccess) rc = -103;
+    }
+    if (rc == 0 && hipGraphInstantiate(&gx, g, nullptr, nullptr, 0) != hipSuccess) rc = -104;
+    for (int32_t i = 0; rc == 0 && i < n; ++i) {
+        if (hipStreamSynchronize(st) != hipSuccess) rc = -105;
+        (void)hipEventRecord(e0, st);
+        if (rc == 0 && hipGraphLaunch(gx, st) != hipSuccess) rc = -106;
+        (void)hipEventRecord(e1, st);
+        if (rc == 0 && hipEventSynchronize(e1) != hipSuccess) rc = -107;
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        gpu_us[i] = ms * 1000.0f;
+    }
+    (void)hipStreamSynchronize(st);
+    if (gx) (void)hipGraphExecDestroy(gx);
+    if (g) (void)hipGraphDestroy(g);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    return rc;
+}
+
+/*
  * Decode-style latency: `nrows` single-row samples back to back.  Row r of
  * the peaky workload (every `greedy_every`-th row greedy, TopK = 1, with the
  * maximum planted 2-4 more times) is generated into d_row, then sampled with
