@@ -154,7 +154,221 @@ __global__ __launch_bounds__(kLmBlock) void lmhead_q4_kernel(const uint8_t* __re
     }
 }
 
+/* ------------------------------------------------------------------
+ * TILED64 layout and the LM head over it.
+ *
+ * One wave per 64 weight rows (lane = row), waves independent (no LDS, no
+ * barrier).  Per 32-column block a lane loads its row's binary32 scale and
+ * 16 nibble bytes from the tile (256 + 1024 contiguous bytes per wave) one
+ * block ahead, and dequantises the 32 weights once for the 32 hidden
+ * vectors of the batch tile.  The hidden values reach the fma without LDS:
+ * a 16-byte load per lane brings two vectors' 32 values of the block into
+ * four VGPRs (lanes 0-7 of every 16-lane row: vector b, columns 4n..4n+3;
+ * lanes 8-15: vector b+1), and v_fmac_f32 with the DPP modifier
+ * row_newbcast:n hands lane n's value of its 16-lane row to all lanes of
+ * that row -- the same value in all four rows, so every lane sees it.  Each
+ * logit is still one fma per term in column order (the order argument at
+ * the top of this file), the 32 vectors being 32 independent chains.
+ * ------------------------------------------------------------------ */
+
+constexpr int kTileB = 32;        /* hidden vectors per pass over the weights */
+constexpr int kTileWaves = 4;     /* waves (64-row groups) per workgroup */
+constexpr int kXAhead = 4;        /* vector pairs whose values are in flight */
+
+__global__ __launch_bounds__(256) void q4_tile_kernel(const uint8_t* __restrict__ src, int32_t rows,
+                                                      int32_t nblk, uint8_t* __restrict__ dst)
+{
+    const int32_t groups = (rows + kQ4TileRows - 1) / kQ4TileRows;
+    const int64_t total = (int64_t)groups * kQ4TileRows * nblk;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        /* t = (g * nblk + k) * 64 + lane: the destination is written in order */
+        const int32_t lane = (int32_t)(t % kQ4TileRows);
+        const int64_t tile = t / kQ4TileRows;
+        const int32_t k = (int32_t)(tile % nblk);
+        const int32_t g = (int32_t)(tile / nblk);
+        const int32_t r = g * kQ4TileRows + lane;
+        uint8_t* tp = dst + tile * kQ4TileBytes;
+        float sc = 0.0f;
+        uint32_t q[4] = {0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+        if (r < rows) {
+            const uint16_t* b = reinterpret_cast<const uint16_t*>(src + ((int64_t)r * nblk + k) * 18);
+            sc = f16_to_f32_ref(b[0]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = (uint32_t)b[1 + 2 * i] | ((uint32_t)b[2 + 2 * i] << 16);
+        }
+        reinterpret_cast<float*>(tp)[lane] = sc;
+        reinterpret_cast<uint4*>(tp + kQ4TileRows * 4)[lane] = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+}
+
+/* 16 fmas: S0 (vector b) and S1 (vector b+1) take terms 8p .. 8p+7 of the
+ * block, in order, interleaved; x0..x3 hold the pair's values (lane n:
+ * columns 4n..4n+3 of b, lane n+8: of b+1) and q0..q7 the weights. */
+#define G4S_FMAC_BCAST(N0, N1, N2, N3)                                                          \
+    asm("v_fmac_f32_dpp %0, %2, %6 row_newbcast:" N0 " row_mask:0xf bank_mask:0xf\n\t"          \
+        "v_fmac_f32_dpp %1, %2, %6 row_newbcast:" N1 " row_mask:0xf bank_mask:0xf\n\t"          \
+        "v_fmac_f32_dpp %0, %3, %7 row_newbcast:" N0 " row_mask:0xf bank_mask:0xf\n\t"          \
+        "v_fmac_f32_dpp %1, %3, %7 row_newbcast:" N1 " row_mask:0xf bank_mask:0xf\n\t"          \
+        "v_fmac_f32_dpp %0, %4, %8 row_newbcast:" N0 " row_mask:0xf bank_mask:0xf\n\t"          \
+        "v_fmac_f32_dpp %1, %4, %8 row_newbcast:" N1 " row_mask:0xf bank_mask:0xf\n\t"          \
+        "v_fmac_f32_dpp %0, %5, %9 row_newbcast:" N0 " row_mask:0xf bank_mask:0xf\n\t"          \
+        "v_fmac_f32_dpp %1, %5, %9 row_newbcast:" N1 " row_mask:0xf bank_mask:0xf\n\t"          \
+        "v_fmac_f32_dpp %0, %2, %10 row_newbcast:" N2 " row_mask:0xf bank_mask:0xf\n\t"         \
+        "v_fmac_f32_dpp %1, %2, %10 row_newbcast:" N3 " row_mask:0xf bank_mask:0xf\n\t"         \
+        "v_fmac_f32_dpp %0, %3, %11 row_newbcast:" N2 " row_mask:0xf bank_mask:0xf\n\t"         \
+        "v_fmac_f32_dpp %1, %3, %11 row_newbcast:" N3 " row_mask:0xf bank_mask:0xf\n\t"         \
+        "v_fmac_f32_dpp %0, %4, %12 row_newbcast:" N2 " row_mask:0xf bank_mask:0xf\n\t"         \
+        "v_fmac_f32_dpp %1, %4, %12 row_newbcast:" N3 " row_mask:0xf bank_mask:0xf\n\t"         \
+        "v_fmac_f32_dpp %0, %5, %13 row_newbcast:" N2 " row_mask:0xf bank_mask:0xf\n\t"         \
+        "v_fmac_f32_dpp %1, %5, %13 row_newbcast:" N3 " row_mask:0xf bank_mask:0xf"             \
+        : "+v"(S0), "+v"(S1)                                                                    \
+        : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "v"(q0), "v"(q1), "v"(q2), "v"(q3), "v"(q4),      \
+          "v"(q5), "v"(q6), "v"(q7))
+
+/* The 64 terms of one block for vectors b and b+1 (x: the pair's values). */
+__device__ __forceinline__ void fma_pair(float& S0, float& S1, const float4 x, const float (&q)[32])
+{
+    const float x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
+    {
+        const float q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
+        const float q4 = q[4], q5 = q[5], q6 = q[6], q7 = q[7];
+        G4S_FMAC_BCAST("0", "8", "1", "9");
+    }
+    {
+        const float q0 = q[8], q1 = q[9], q2 = q[10], q3 = q[11];
+        const float q4 = q[12], q5 = q[13], q6 = q[14], q7 = q[15];
+        G4S_FMAC_BCAST("2", "10", "3", "11");
+    }
+    {
+        const float q0 = q[16], q1 = q[17], q2 = q[18], q3 = q[19];
+        const float q4 = q[20], q5 = q[21], q6 = q[22], q7 = q[23];
+        G4S_FMAC_BCAST("4", "12", "5", "13");
+    }
+    {
+        const float q0 = q[24], q1 = q[25], q2 = q[26], q3 = q[27];
+        const float q4 = q[28], q5 = q[29], q6 = q[30], q7 = q[31];
+        G4S_FMAC_BCAST("6", "14", "7", "15");
+    }
+}
+#undef G4S_FMAC_BCAST
+
+/* Weight j of the block: term (Single(q) * LScale) of CpuMatVecQ4
+ * (Tensors.pas:586,590) with q = nibble - 8; fma(nibble, s, -8s) is exact
+ * and equal to it (both are (nibble - 8) * s, at most 15 significant bits). */
+__device__ __forceinline__ void dequant(const uint4 w, float sc, float (&q)[32])
+{
+    const float m8 = -8.0f * sc;
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        /* the nibble masks stay opaque so that each nibble converts with one
+         * v_cvt_f32_ubyteN (instead of a field extract and a convert) */
+        uint32_t lo, hi;
+        asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(ws[d]));
+        asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi) : "v"(ws[d] >> 4));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[8 * d + 2 * i] = __builtin_fmaf((float)((lo >> (8 * i)) & 0xFFu), sc, m8);
+            q[8 * d + 2 * i + 1] = __builtin_fmaf((float)((hi >> (8 * i)) & 0xFFu), sc, m8);
+        }
+    }
+}
+
+__global__ __launch_bounds__(64 * kTileWaves) void lmhead_tiled_kernel(
+    const uint8_t* __restrict__ tiles, int32_t rows, int32_t nblk, const float* __restrict__ h,
+    int32_t cols, int32_t batch, float* __restrict__ out, int64_t stride, uint32_t* __restrict__ gmax,
+    int32_t ngroups)
+{
+    const int lane = threadIdx.x & 63;
+    const int32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x * kTileWaves + (threadIdx.x >> 6));
+    if (g >= ngroups) return; /* whole waves: no barrier below */
+    const int32_t r = g * kQ4TileRows + lane;
+    const float* tsc = reinterpret_cast<const float*>(tiles + (int64_t)g * nblk * kQ4TileBytes);
+    const uint4* tq = reinterpret_cast<const uint4*>(tiles + (int64_t)g * nblk * kQ4TileBytes +
+                                                     kQ4TileRows * 4);
+    const uint32_t ul = (uint32_t)lane;
+    constexpr int kTileF = kQ4TileBytes / 4;  /* floats per tile */
+    constexpr int kTileQ = kQ4TileBytes / 16; /* uint4 per tile */
+    /* lane's share of a pair load: vector 2p + (n >> 3), columns 4 (n & 7) .. +3 */
+    const int n = lane & 15;
+    const int32_t xlane = (n >> 3) * cols + 4 * (n & 7);
+    for (int32_t b0 = 0; b0 < batch; b0 += kTileB) {
+        /* offset of pair p's load: vectors past the batch read vector batch-1
+         * (any valid row; their sums are discarded) */
+        /* 32-bit byte offsets from the uniform base (the hidden matrix is
+         * below 2 GiB: checked by the launcher) */
+        const auto xload = [&](int p, int32_t k) -> float4 {
+            const int32_t ub = b0 + 2 * p;
+            const int32_t o = ub + 1 < batch ? ub * cols + xlane : (batch - 1) * cols + 4 * (n & 7);
+            const uint32_t byte = (uint32_t)(o + 32 * k) * 4u;
+            return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(h) + byte);
+        };
+        float S[kTileB];
+#pragma unroll
+        for (int b = 0; b < kTileB; ++b) S[b] = 0.0f;
+        /* the first block's weights and vector pairs */
+        float sc = tsc[ul];
+        uint4 w = tq[ul];
+        float4 xr[kXAhead];
+#pragma unroll
+        for (int p = 0; p < kXAhead; ++p) xr[p] = xload(p, 0);
+        for (int32_t k = 0; k < nblk; ++k) {
+            float q[32];
+            dequant(w, sc, q);
+            const int32_t kn = k + 1 < nblk ? k + 1 : k;
+            sc = tsc[(uint32_t)(kn * kTileF) + ul];
+            w = tq[(uint32_t)(kn * kTileQ) + ul];
+            /* the scheduler keeps each load where it is issued: kXAhead pairs
+             * before its use, after the block's weight loads */
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int p = 0; p < kTileB / 2; ++p) {
+                const float4 x = xr[p % kXAhead];
+                /* the pair kXAhead ahead (wrapping into the next block) */
+                const int pa = p + kXAhead;
+                const int32_t ka = pa < kTileB / 2 ? k : kn;
+                xr[p % kXAhead] = xload(pa % (kTileB / 2), ka);
+                __builtin_amdgcn_sched_barrier(0);
+                fma_pair(S[2 * p], S[2 * p + 1], x, q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        const bool live = r < rows;
+#pragma unroll
+        for (int b = 0; b < kTileB; ++b) {
+            if (b0 + b < batch) {
+                if (live) out[(int64_t)(b0 + b) * stride + r] = S[b];
+                if (gmax) {
+                    const uint32_t key = wave_max_u32(live ? cand_key(S[b]) : 0u);
+                    if (lane == 0) gmax[(int64_t)(b0 + b) * ngroups + g] = key;
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t q4_tile_launch(const uint8_t* src, int32_t rows, int32_t nblk, uint8_t* dst, hipStream_t s)
+{
+    const int64_t total = (int64_t)((rows + kQ4TileRows - 1) / kQ4TileRows) * kQ4TileRows * nblk;
+    const int64_t want = (total + 255) / 256;
+    const unsigned grid = (unsigned)(want < 65536 ? want : 65536);
+    hipLaunchKernelGGL(q4_tile_kernel, dim3(grid), dim3(256), 0, s, src, rows, nblk, dst);
+    return hipGetLastError();
+}
+
+hipError_t lmhead_tiled_launch(const uint8_t* tiles, int32_t rows, int32_t cols, const float* h,
+                               int32_t batch, float* logits, int64_t stride, uint32_t* gmax,
+                               hipStream_t s)
+{
+    const int32_t ngroups = (rows + kQ4TileRows - 1) / kQ4TileRows;
+    const unsigned grid = (unsigned)((ngroups + kTileWaves - 1) / kTileWaves);
+    hipLaunchKernelGGL(lmhead_tiled_kernel, dim3(grid), dim3(64 * kTileWaves), 0, s, tiles, rows,
+                       cols / 32, h, cols, batch, logits, stride, gmax, ngroups);
+    return hipGetLastError();
+}
 
 hipError_t lmhead_q4_0_launch(const uint8_t* w, int32_t rows, int32_t cols, const float* h,
                               int32_t batch, float* logits, int64_t stride, hipStream_t s)

@@ -61,6 +61,7 @@ struct g4s_sampler {
     g4s::ChunkRec* recs = nullptr;
     uint32_t* wbounds = nullptr;
     uint32_t* tickets = nullptr;
+    uint32_t* gmax = nullptr;     /* [max_batch][ceil(vocab/64)] LM-head group maxima */
     /* full path workspace */
     g4s::FullWorkspace full{};
     /* per-call staging */
@@ -108,6 +109,7 @@ void release(g4s_sampler* s)
     f(s->recs);
     f(s->wbounds);
     f(s->tickets);
+    f(s->gmax);
     g4s::full_free(s->full);
     f(s->d_params);
     f(s->d_u);
@@ -145,7 +147,8 @@ int check_logits(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t ro
 int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride, int32_t batch,
             const g4s_params* d_params, const double* d_u, const g4s_params* p0, double u0,
             int32_t kbound, bool full_rows, bool wide, int32_t* d_ids,
-            const g4s_outputs* outputs, uint32_t* done = nullptr, uint32_t seq = 0)
+            const g4s_outputs* outputs, uint32_t* done = nullptr, uint32_t seq = 0,
+            const uint32_t* gmax = nullptr)
 {
     g4s_outputs out{};
     if (outputs) out = *outputs;
@@ -178,7 +181,13 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         a.done = done;
         a.seq = seq;
         a.out = out;
-        hipError_t e = g4s::topk_launch(cfg, a, dtype, s->stream, s->ncu);
+        hipError_t e = hipErrorNotSupported;
+        if (gmax && dtype == G4S_DTYPE_F32)
+            e = g4s::topk_groups_launch(cfg, a, gmax, (s->vocab + 63) / 64, s->stream);
+        if (e == hipErrorNotSupported) {
+            (void)hipGetLastError();
+            e = g4s::topk_launch(cfg, a, dtype, s->stream, s->ncu);
+        }
         if (e != hipSuccess) return hip_fail(s, e, "top-k kernel launch");
     }
     if (full_rows || wide) {
@@ -280,6 +289,7 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
     dm((void**)&s->recs, mb * g4s::kMaxSplits * sizeof(g4s::ChunkRec));
     dm((void**)&s->wbounds, mb * g4s::kWaveBounds * sizeof(uint32_t));
     dm((void**)&s->tickets, mb * sizeof(uint32_t));
+    dm((void**)&s->gmax, mb * (size_t)((vocab + 63) / 64) * sizeof(uint32_t));
     dm((void**)&s->d_params, mb * sizeof(g4s_params));
     dm((void**)&s->d_u, mb * sizeof(double));
     hm((void**)&s->h_params, mb * sizeof(g4s_params));
@@ -320,16 +330,27 @@ G4S_API int g4s_destroy(g4s_sampler* s)
     return G4S_OK;
 }
 
-G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
-                          int32_t batch, const g4s_params* params, const double* u, int32_t* ids,
-                          const g4s_outputs* outputs)
+namespace {
+
+int check_params(g4s_sampler* s, int32_t batch, const g4s_params* params, const double* u,
+                 int32_t* ids)
 {
-    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
-    s->err.clear();
-    int rc = check_logits(s, d_logits, dtype, row_stride, batch);
-    if (rc) return rc;
     if (!params || !u || !ids)
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "params, u and ids must be non-NULL");
+    /* u must be a probability-like number; the reference's Random is in [0,1) */
+    for (int32_t r = 0; r < batch; ++r)
+        if (!(u[r] >= 0.0 && u[r] < 1.0))
+            return fail(s, G4S_ERR_INVALID_ARGUMENT, "row %d: u = %g outside [0, 1)", r, u[r]);
+    return G4S_OK;
+}
+
+/* The synchronous sample of g4s_sample_ex (arguments checked), optionally on
+ * logits from the tiled LM head with their group maxima. */
+int sample_sync(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
+                int32_t batch, const g4s_params* params, const double* u, int32_t* ids,
+                const g4s_outputs* outputs, const uint32_t* gmax)
+{
+    int rc;
     int32_t kbound = 0;
     bool full_rows = false, wide = false;
     for (int32_t r = 0; r < batch; ++r) {
@@ -342,11 +363,6 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
             full_rows = true;
         }
     }
-    /* u must be a probability-like number; the reference's Random is in [0,1) */
-    for (int32_t r = 0; r < batch; ++r)
-        if (!(u[r] >= 0.0 && u[r] < 1.0))
-            return fail(s, G4S_ERR_INVALID_ARGUMENT, "row %d: u = %g outside [0, 1)", r, u[r]);
-
     g4s_outputs out{};
     if (outputs) out = *outputs;
     /* ids (and flags, unless the caller wants them on the device) are written
@@ -366,7 +382,7 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
 
     if (batch == 1) {
         rc = enqueue(s, d_logits, dtype, row_stride, 1, nullptr, nullptr, &params[0], u[0], kbound,
-                     full_rows, wide, s->h_ids, &out, done, seq);
+                     full_rows, wide, s->h_ids, &out, done, seq, gmax);
     } else {
         std::memcpy(s->h_params, params, sizeof(g4s_params) * batch);
         std::memcpy(s->h_u, u, sizeof(double) * batch);
@@ -377,7 +393,7 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
                                s->stream);
         if (e != hipSuccess) return hip_fail(s, e, "parameter upload");
         rc = enqueue(s, d_logits, dtype, row_stride, batch, s->d_params, s->d_u, nullptr, 0.0,
-                     kbound, full_rows, wide, s->h_ids, &out, done, seq);
+                     kbound, full_rows, wide, s->h_ids, &out, done, seq, gmax);
     }
     if (rc) return rc;
     hipError_t e = hipSuccess;
@@ -409,6 +425,21 @@ G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, i
         if (s->h_flags[r] & G4S_FLAG_EMPTY)
             return fail(s, G4S_ERR_EMPTY_ROW, "row %d: no logit above -1e30 on the top-k path", r);
     return G4S_OK;
+}
+
+}  // namespace
+
+G4S_API int g4s_sample_ex(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
+                          int32_t batch, const g4s_params* params, const double* u, int32_t* ids,
+                          const g4s_outputs* outputs)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    int rc = check_logits(s, d_logits, dtype, row_stride, batch);
+    if (rc) return rc;
+    rc = check_params(s, batch, params, u, ids);
+    if (rc) return rc;
+    return sample_sync(s, d_logits, dtype, row_stride, batch, params, u, ids, outputs, nullptr);
 }
 
 G4S_API int g4s_sample(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
@@ -457,4 +488,61 @@ G4S_API int g4s_lmhead_q4_0(g4s_sampler* s, const void* d_weights, int32_t rows,
         return fail(s, G4S_ERR_UNSUPPORTED, "LM-head shape not supported (batch %d)", batch);
     if (e != hipSuccess) return hip_fail(s, e, "LM-head kernel launch");
     return G4S_OK;
+}
+
+namespace {
+
+int check_tiled(g4s_sampler* s, const void* d_tiles, int32_t rows, int32_t cols,
+                const float* d_hidden, int32_t batch, float* d_logits, int64_t logits_stride)
+{
+    if (!d_tiles || !d_hidden || !d_logits)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (rows < 1 || cols < 32 || (cols % 32) != 0)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "rows %d / cols %d (cols must be a multiple of 32)",
+                    rows, cols);
+    if (batch < 1 || logits_stride < rows)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "batch %d / logits_stride %lld", batch,
+                    (long long)logits_stride);
+    if (((uintptr_t)d_tiles & 15u) != 0 || ((uintptr_t)d_hidden & 15u) != 0)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "d_tiles and d_hidden must be 16-byte aligned");
+    if ((int64_t)batch * cols * 4 > INT32_MAX)
+        return fail(s, G4S_ERR_UNSUPPORTED, "hidden matrix of %d x %d floats above 2 GiB", batch,
+                    cols);
+    return G4S_OK;
+}
+
+}  // namespace
+
+G4S_API int g4s_lmhead_q4_0_tiled(g4s_sampler* s, const void* d_tiles, int32_t rows, int32_t cols,
+                                  const float* d_hidden, int32_t batch, float* d_logits,
+                                  int64_t logits_stride)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    int rc = check_tiled(s, d_tiles, rows, cols, d_hidden, batch, d_logits, logits_stride);
+    if (rc) return rc;
+    hipError_t e = g4s::lmhead_tiled_launch((const uint8_t*)d_tiles, rows, cols, d_hidden, batch,
+                                            d_logits, logits_stride, nullptr, s->stream);
+    if (e != hipSuccess) return hip_fail(s, e, "LM-head kernel launch");
+    return G4S_OK;
+}
+
+G4S_API int g4s_lmhead_sample_q4_0(g4s_sampler* s, const void* d_tiles, int32_t cols,
+                                   const float* d_hidden, int32_t batch, float* d_logits,
+                                   int64_t logits_stride, const g4s_params* params,
+                                   const double* u, int32_t* ids, const g4s_outputs* outputs)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    int rc = check_tiled(s, d_tiles, s->vocab, cols, d_hidden, batch, d_logits, logits_stride);
+    if (rc) return rc;
+    rc = check_logits(s, d_logits, G4S_DTYPE_F32, logits_stride, batch);
+    if (rc) return rc;
+    rc = check_params(s, batch, params, u, ids);
+    if (rc) return rc;
+    hipError_t e = g4s::lmhead_tiled_launch((const uint8_t*)d_tiles, s->vocab, cols, d_hidden,
+                                            batch, d_logits, logits_stride, s->gmax, s->stream);
+    if (e != hipSuccess) return hip_fail(s, e, "LM-head kernel launch");
+    return sample_sync(s, d_logits, G4S_DTYPE_F32, logits_stride, batch, params, u, ids, outputs,
+                       s->gmax);
 }

@@ -68,6 +68,13 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound);
 hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStream_t s,
                        int32_t ncu = 0);
 
+/* Rows whose f32 logits come from the tiled LM head with its 64-logit group
+ * maxima (gmax [batch][ngroups], candidate keys): candidates from the groups
+ * whose maximum reaches the K-th largest group maximum, then the merge launch
+ * (mode 2).  hipErrorNotSupported above 8192 groups. */
+hipError_t topk_groups_launch(const TopkConfig& c, const TopkArgs& a, const uint32_t* gmax,
+                              int32_t ngroups, hipStream_t s);
+
 }  // namespace g4s
 
 #endif

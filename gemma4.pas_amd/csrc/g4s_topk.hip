@@ -907,6 +907,151 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     publish_done(a.done, row, a.seq);
 }
 
+/* ------------------------------------- candidates from 64-row group maxima */
+
+/* The top-k candidates of rows whose logits come from the tiled LM head,
+ * which also leaves each 64-logit group's largest candidate key.  tau0 is
+ * the K-th largest group maximum (1 when at most K groups hold a key): K
+ * groups hold a key >= tau0, so tau0 is at most the row's K-th largest key,
+ * and every key >= tau0 lies in a group whose maximum is >= tau0.  Those
+ * groups (about K of them) are read back and their keys >= tau0 become the
+ * merge's candidates, laid out as the chunk launch would leave them: slot i
+ * of the row belongs to chunk i >> cap_log2, every chunk's record carries
+ * tau0 as its bound, and the per-wave bounds are 0 (no information).  When
+ * the keys >= tau0 outnumber the row's slots (heavy ties), the row is
+ * written as one exact chunk record instead: the keys above the row's K-th
+ * largest key tau and the first min(copies, K) copies of tau in index order,
+ * as the chunk launch's exact select does.  The merge launch (mode 2) then
+ * runs unchanged on the materialized logits. */
+constexpr int kGcBlock = 1024;
+constexpr int kGcItems = 8; /* group maxima per thread: up to 8192 groups */
+
+__global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const uint32_t* gmax,
+                                                              int32_t ngroups, int32_t nwave)
+{
+    __shared__ uint32_t s_hist[256];
+    __shared__ int s_misc[8];
+    __shared__ int s_scan[kGcBlock / 64];
+    __shared__ int s_list[kGcBlock * kGcItems];
+    __shared__ int s_cnt;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    constexpr int NW = kGcBlock / 64;
+    const int row = blockIdx.x;
+    const g4s_params rp = a.params ? a.params[row] : a.p0;
+    const int K = rp.top_k;
+    if (!(K >= 1 && K < a.vocab) || K > a.kbound) return; /* the merge launch flags the row */
+    const float* lg = reinterpret_cast<const float*>(a.logits) + (int64_t)row * a.row_stride;
+    const uint32_t* gm = gmax + (int64_t)row * ngroups;
+    const int S = a.splits;
+    const int cap = 1 << a.cap_log2;
+    const int slots = S << a.cap_log2;
+    uint64_t* rc = a.cand + (int64_t)row * kCandRow;
+    if (tid == 0) s_cnt = 0;
+
+    uint32_t keys[kGcItems];
+    int nz = 0;
+#pragma unroll
+    for (int q = 0; q < kGcItems; ++q) {
+        const int g = tid + q * kGcBlock;
+        keys[q] = g < ngroups ? gm[g] : 0u;
+        nz += keys[q] != 0u;
+    }
+    nz = block_sum_i32<kGcBlock>(nz, s_scan);
+    uint32_t tau0 = 1u;
+    if (nz > K) {
+        int gt, eq;
+        tau0 = regs_radix_kth<kGcBlock, kGcItems>(keys, K, s_hist, s_misc, &gt, &eq);
+    }
+    /* the candidate groups, ascending */
+    int ng = 0;
+#pragma unroll
+    for (int q = 0; q < kGcItems; ++q) {
+        const int f = keys[q] >= tau0 ? 1 : 0;
+        int tot;
+        const int pos = block_exclusive_scan<kGcBlock>(f, s_scan, tot);
+        if (f) s_list[ng + pos] = tid + q * kGcBlock;
+        ng += tot;
+    }
+    __syncthreads();
+    /* their keys >= tau0, one group per wave at a time (lane = logit) */
+    const auto gkey = [&](int g) -> uint32_t {
+        const int64_t i = (int64_t)g * 64 + lane;
+        return i < a.vocab ? cand_key(lg[i]) : 0u;
+    };
+    for (int t = wid; t < ng; t += NW) {
+        const int g = s_list[t];
+        const uint32_t k = gkey(g);
+        const bool c = k >= tau0;
+        const uint64_t m = __ballot(c);
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&s_cnt, __popcll(m));
+        base = __builtin_amdgcn_readfirstlane(base);
+        const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+        if (c && pos < slots) rc[pos] = cand_pack(k, (uint32_t)(g * 64 + lane));
+    }
+    __syncthreads();
+    const int M0 = s_cnt;
+    for (int i = tid; i < nwave && i < kWaveBounds; i += kGcBlock)
+        a.wbounds[(int64_t)row * kWaveBounds + i] = 0u;
+    ChunkRec* recs = a.recs + (int64_t)row * kMaxSplits;
+    if (M0 <= slots) {
+        for (int c = tid; c < S; c += kGcBlock) {
+            const int n = M0 - c * cap;
+            const int cnt = n < 0 ? 0 : (n > cap ? cap : n);
+            recs[c] = ChunkRec{(uint32_t)cnt, cnt > 0 ? tau0 : 1u, 0u, 0u};
+        }
+        return;
+    }
+    /* heavy ties: the row's K-th largest key over the candidate groups (M0 >
+     * slots >= 2K keys >= tau0 hold it) */
+    int gt, eq;
+    const uint32_t tau = block_radix_kth<kGcBlock>(
+        ng * 64, K,
+        [&](int i) -> uint32_t {
+            const int64_t e = (int64_t)s_list[i >> 6] * 64 + (i & 63);
+            return e < a.vocab ? cand_key(lg[e]) : 0u;
+        },
+        [&](int) { return true; }, s_hist, s_misc, &gt, &eq);
+    /* keys above tau (fewer than K), any order */
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();
+    for (int t = wid; t < ng; t += NW) {
+        const int g = s_list[t];
+        const uint32_t k = gkey(g);
+        const bool c = k > tau;
+        const uint64_t m = __ballot(c);
+        int base = 0;
+        if (lane == 0 && m) base = atomicAdd(&s_cnt, __popcll(m));
+        base = __builtin_amdgcn_readfirstlane(base);
+        if (c) rc[base + __popcll(m & ((1ull << lane) - 1ull))] = cand_pack(k, (uint32_t)(g * 64 + lane));
+    }
+    /* the first min(eq, K) copies of tau in index order: NW groups per step,
+     * in list order */
+    const int want = eq < K ? eq : K;
+    int taken = 0;
+    for (int t0 = 0; t0 < ng && taken < want; t0 += NW) {
+        const int t = t0 + wid;
+        const int g = t < ng ? s_list[t] : 0;
+        const bool c = t < ng && gkey(g) == tau;
+        const uint64_t m = __ballot(c);
+        if (lane == 0) s_scan[wid] = __popcll(m);
+        __syncthreads();
+        int off = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            off += w < wid ? s_scan[w] : 0;
+            tot += s_scan[w];
+        }
+        const int r = taken + off + __popcll(m & ((1ull << lane) - 1ull));
+        if (c && r < want) rc[gt + r] = cand_pack(tau, (uint32_t)(g * 64 + lane));
+        taken += tot;
+        __syncthreads();
+    }
+    for (int c = tid; c < S; c += kGcBlock)
+        recs[c] = c == 0 ? ChunkRec{(uint32_t)(gt + want), tau, 0u, 0x80000000u | (uint32_t)eq}
+                         : ChunkRec{0u, 1u, 0u, 0u};
+}
+
 /* ---------------------------------------------------------------- launch */
 
 template <int BLOCK, int ITEMS, int DT>
@@ -973,6 +1118,21 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound)
         }
     }
     return c;
+}
+
+hipError_t topk_groups_launch(const TopkConfig& c, const TopkArgs& a, const uint32_t* gmax,
+                              int32_t ngroups, hipStream_t s)
+{
+    if (ngroups > kGcBlock * kGcItems) return hipErrorNotSupported;
+    hipLaunchKernelGGL(group_cand_kernel, dim3((unsigned)a.batch), dim3(kGcBlock), 0, s, a, gmax,
+                       ngroups, (int32_t)(c.splits * (c.block / 64)));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    TopkArgs b = a;
+    b.mode = 2;
+    if (c.block == 512 && c.items == 16) return launch_one<512, 16, 0>(b, a.kbound, s);
+    if (c.block == 1024 && c.items == 32) return launch_one<1024, 32, 0>(b, a.kbound, s);
+    return launch_one<1024, 64, 0>(b, a.kbound, s);
 }
 
 hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStream_t s,

@@ -24,6 +24,15 @@ G4S_ERR_NO_DEVICE = -3
 G4S_ERR_OUT_OF_MEMORY = -4
 G4S_ERR_HIP = -5
 G4S_ERR_EMPTY_ROW = -6
+G4S_ERR_IO = -7
+G4S_ERR_FORMAT = -8
+G4S_ERR_NOT_FOUND = -9
+
+# TDtypeKind (src/Gemma4.Types.pas:94-100)
+WDTYPE_UNKNOWN, WDTYPE_BF16, WDTYPE_F16, WDTYPE_F32, WDTYPE_Q4_0 = range(5)
+Q4_LAYOUT_ROWS = 0
+Q4_LAYOUT_TILED64 = 1
+MAX_DIMS = 8
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -42,7 +51,11 @@ FLAG_ERROR = 0x80000000
 
 EXPORTS = ("g4s_version", "g4s_params_set_defaults", "g4s_max_top_k", "g4s_create",
            "g4s_destroy", "g4s_last_error", "g4s_sample", "g4s_sample_ex", "g4s_sample_async",
-           "g4s_sample_topk_noalloc", "g4s_lmhead_q4_0")
+           "g4s_sample_topk_noalloc", "g4s_lmhead_q4_0", "g4s_lmhead_q4_0_tiled",
+           "g4s_lmhead_sample_q4_0", "g4s_store_open", "g4s_store_close", "g4s_store_last_error",
+           "g4s_store_tensor_count", "g4s_store_tensor_info", "g4s_store_find_tensor",
+           "g4s_store_raw_pointer", "g4s_store_verify", "g4s_q4_0_device_bytes",
+           "g4s_store_upload_q4_0", "g4s_q4_0_repack")
 
 
 class TSamplingParams(ctypes.Structure):
@@ -64,6 +77,17 @@ class Outputs(ctypes.Structure):
                 ("probs", ctypes.c_void_p), ("capacity", ctypes.c_int32),
                 ("argmax", ctypes.c_void_p), ("lsum", ctypes.c_void_p),
                 ("flags", ctypes.c_void_p)]
+
+
+class TensorInfo(ctypes.Structure):
+    """g4s_tensor_info == TTensorInfo (src/Gemma4.Types.pas:119-129) minus the name."""
+    _fields_ = [("SourceDtype", ctypes.c_int32), ("OutputDtype", ctypes.c_int32),
+                ("Offset", ctypes.c_uint64), ("DataSize", ctypes.c_uint64),
+                ("ndim", ctypes.c_int32), ("shape_", ctypes.c_int32 * MAX_DIMS)]
+
+    @property
+    def Shape(self):
+        return tuple(self.shape_[i] for i in range(self.ndim))
 
 
 class SamplerError(RuntimeError):
@@ -100,6 +124,32 @@ def load():
         L.g4s_lmhead_q4_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
                                       ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                       ctypes.c_void_p, ctypes.c_int64]
+        L.g4s_lmhead_q4_0_tiled.argtypes = L.g4s_lmhead_q4_0.argtypes
+        L.g4s_lmhead_sample_q4_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+                                             ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
+                                             ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_void_p, ctypes.c_void_p]
+        L.g4s_store_open.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p,
+                                     ctypes.c_char_p, ctypes.c_char_p]
+        L.g4s_store_close.argtypes = [ctypes.c_void_p]
+        L.g4s_store_last_error.restype = ctypes.c_char_p
+        L.g4s_store_last_error.argtypes = [ctypes.c_void_p]
+        L.g4s_store_tensor_count.restype = ctypes.c_int32
+        L.g4s_store_tensor_count.argtypes = [ctypes.c_void_p]
+        L.g4s_store_tensor_info.argtypes = [ctypes.c_void_p, ctypes.c_int32,
+                                            ctypes.POINTER(TensorInfo), ctypes.c_char_p,
+                                            ctypes.c_int32]
+        L.g4s_store_find_tensor.argtypes = [ctypes.c_void_p, ctypes.c_char_p,
+                                            ctypes.POINTER(TensorInfo)]
+        L.g4s_store_raw_pointer.restype = ctypes.c_void_p
+        L.g4s_store_raw_pointer.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
+        L.g4s_store_verify.argtypes = [ctypes.c_void_p]
+        L.g4s_q4_0_device_bytes.restype = ctypes.c_int64
+        L.g4s_q4_0_device_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+        L.g4s_store_upload_q4_0.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int32,
+                                            ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+        L.g4s_q4_0_repack.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                      ctypes.c_void_p, ctypes.c_void_p]
         L.g4s_sample_topk_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                               ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
                                               ctypes.c_void_p, ctypes.c_int32, ctypes.c_float,
@@ -231,6 +281,34 @@ class Sampler:
                                int(rows if logits_stride is None else logits_stride))
         self._check(rc)
 
+    def lmhead_q4_0_tiled(self, d_tiles, rows, cols, d_hidden, batch, d_logits,
+                          logits_stride=None):
+        L = load()
+        rc = L.g4s_lmhead_q4_0_tiled(self.h, _ptr(d_tiles), int(rows), int(cols), _ptr(d_hidden),
+                                     int(batch), _ptr(d_logits),
+                                     int(rows if logits_stride is None else logits_stride))
+        self._check(rc)
+
+    def lmhead_sample_q4_0(self, d_tiles, cols, d_hidden, batch, d_logits, params, u,
+                           logits_stride=None, outputs=None, check=True):
+        """g4s_lmhead_sample_q4_0: LM head + sample; returns (status, ids)."""
+        L = load()
+        if isinstance(params, TSamplingParams):
+            params = [params] * batch
+        parr = params_array(params)
+        uarr = np.ascontiguousarray(np.asarray(u, dtype=np.float64).reshape(-1))
+        assert uarr.size == batch
+        ids = np.full(batch, -7, dtype=np.int32)
+        stride = self.vocab if logits_stride is None else int(logits_stride)
+        rc = L.g4s_lmhead_sample_q4_0(self.h, _ptr(d_tiles), int(cols), _ptr(d_hidden),
+                                      int(batch), _ptr(d_logits), stride, parr,
+                                      uarr.ctypes.data_as(ctypes.c_void_p),
+                                      ids.ctypes.data_as(ctypes.c_void_p),
+                                      ctypes.byref(outputs) if outputs is not None else None)
+        if check:
+            self._check(rc)
+        return rc, ids
+
     def close(self):
         if self.h is not None and self.h.value:
             load().g4s_destroy(self.h)
@@ -264,3 +342,97 @@ class DeviceOutputs:
                     argmax=self.argmax.download(np.int32),
                     lsum=self.lsum.download(np.float32),
                     flags=self.flags.download(np.uint32))
+
+
+def q4_0_device_bytes(rows, cols, layout):
+    return int(load().g4s_q4_0_device_bytes(int(rows), int(cols), int(layout)))
+
+
+def q4_0_repack(d_rows, rows, cols, d_tiled, stream=None):
+    """g4s_q4_0_repack: ROWS -> TILED64 on the device (stream-ordered)."""
+    L = load()
+    rc = L.g4s_q4_0_repack(_ptr(d_rows), int(rows), int(cols), _ptr(d_tiled),
+                           stream.handle if stream is not None else None)
+    if rc != G4S_OK:
+        raise SamplerError(rc, L.g4s_store_last_error(None).decode())
+
+
+class WeightStore:
+    """TWeightStore (src/Gemma4.Tensors.pas:321-516) over the C ABI:
+    Open / Close / FindTensor / TensorCount / GetTensorInfo / GetRawPointer,
+    plus the Q4_0 upload into device memory."""
+
+    def __init__(self):
+        self.h = None
+
+    def Open(self, vpk_path, manifest_path=None, weights_path=None):
+        """Returns True on success; LastError() says why not (the engine's
+        Boolean-plus-errors convention)."""
+        L = load()
+        self.Close()
+        h = ctypes.c_void_p()
+        enc = lambda x: None if x is None else str(x).encode()
+        rc = L.g4s_store_open(ctypes.byref(h), enc(vpk_path), enc(manifest_path),
+                              enc(weights_path))
+        self._open_rc = rc
+        self._open_err = "" if rc == G4S_OK else L.g4s_store_last_error(None).decode()
+        if rc == G4S_OK:
+            self.h = h
+        return rc == G4S_OK
+
+    def IsOpen(self):
+        return self.h is not None
+
+    def LastError(self):
+        if self.h is None:
+            return getattr(self, "_open_err", "")
+        return load().g4s_store_last_error(self.h).decode()
+
+    def Close(self):
+        if self.h is not None:
+            load().g4s_store_close(self.h)
+        self.h = None
+
+    def TensorCount(self):
+        return int(load().g4s_store_tensor_count(self.h)) if self.h is not None else 0
+
+    def GetTensorInfo(self, index):
+        info = TensorInfo()
+        name = ctypes.create_string_buffer(1024)
+        rc = load().g4s_store_tensor_info(self.h, int(index), ctypes.byref(info), name, 1024)
+        if rc != G4S_OK:
+            raise SamplerError(rc, self.LastError())
+        return name.value.decode(), info
+
+    def FindTensor(self, name):
+        """(found, TensorInfo) as TWeightStore.FindTensor's Boolean + out."""
+        info = TensorInfo()
+        rc = load().g4s_store_find_tensor(self.h, name.encode(), ctypes.byref(info))
+        return rc == G4S_OK, info
+
+    def GetRawBytes(self, name):
+        """The tensor's bytes in the mapped archive (GetRawPointer + DataSize)."""
+        ok, info = self.FindTensor(name)
+        if not ok:
+            raise SamplerError(G4S_ERR_NOT_FOUND, self.LastError())
+        p = load().g4s_store_raw_pointer(self.h, name.encode())
+        if not p:
+            raise SamplerError(G4S_ERR_FORMAT, self.LastError())
+        return ctypes.string_at(p, info.DataSize)
+
+    def Verify(self):
+        rc = load().g4s_store_verify(self.h)
+        return rc == G4S_OK
+
+    def UploadQ4_0(self, name, layout, d_dst, dst_bytes, stream=None):
+        L = load()
+        rc = L.g4s_store_upload_q4_0(self.h, name.encode(), int(layout), _ptr(d_dst),
+                                     int(dst_bytes), stream.handle if stream is not None else None)
+        if rc != G4S_OK:
+            raise SamplerError(rc, self.LastError())
+
+    def __del__(self):
+        try:
+            self.Close()
+        except Exception:
+            pass

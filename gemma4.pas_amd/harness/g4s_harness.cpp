@@ -526,3 +526,58 @@ G4H_API int g4h_lmhead_sampler(g4s_sampler* s, void* stream, const void* d_weigh
     for (auto& e : ev) (void)hipEventDestroy(e);
     return rc;
 }
+
+/*
+ * The LM head on TILED64 weights alone: `steps` launches of
+ * g4s_lmhead_q4_0_tiled, each bracketed by events (us[i]).
+ */
+G4H_API int g4h_lmhead_tiled(g4s_sampler* s, void* stream, const void* d_tiles, int32_t rows,
+                             int32_t cols, const float* d_hidden, int32_t batch, float* d_logits,
+                             int32_t warmup, int32_t steps, float* us)
+{
+    hipStream_t st = (hipStream_t)stream;
+    std::vector<hipEvent_t> ev((size_t)steps * 2);
+    for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) return -100;
+    int rc = 0;
+    for (int32_t i = 0; rc == 0 && i < warmup; ++i)
+        rc = g4s_lmhead_q4_0_tiled(s, d_tiles, rows, cols, d_hidden, batch, d_logits, rows);
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    for (int32_t i = 0; rc == 0 && i < steps; ++i) {
+        (void)hipEventRecord(ev[(size_t)i * 2], st);
+        rc = g4s_lmhead_q4_0_tiled(s, d_tiles, rows, cols, d_hidden, batch, d_logits, rows);
+        (void)hipEventRecord(ev[(size_t)i * 2 + 1], st);
+    }
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -104;
+    if (rc == 0)
+        for (int32_t i = 0; i < steps; ++i) {
+            float a = 0.0f;
+            (void)hipEventElapsedTime(&a, ev[(size_t)i * 2], ev[(size_t)i * 2 + 1]);
+            us[i] = a * 1000.0f;
+        }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    return rc;
+}
+
+/*
+ * The fused LM head + sample (g4s_lmhead_sample_q4_0, synchronous): host
+ * wall time of each call in us[i]; the last call's ids in ids.
+ */
+G4H_API int g4h_lmhead_sample_fused(g4s_sampler* s, const void* d_tiles, int32_t rows,
+                                    int32_t cols, const float* d_hidden, int32_t batch,
+                                    float* d_logits, const g4s_params* params, const double* u,
+                                    int32_t* ids, int32_t warmup, int32_t steps, float* us)
+{
+    int rc = 0;
+    for (int32_t i = 0; rc == 0 && i < warmup; ++i)
+        rc = g4s_lmhead_sample_q4_0(s, d_tiles, cols, d_hidden, batch, d_logits, rows, params, u,
+                                    ids, nullptr);
+    for (int32_t i = 0; rc == 0 && i < steps; ++i) {
+        const auto t0 = std::chrono::steady_clock::now();
+        rc = g4s_lmhead_sample_q4_0(s, d_tiles, cols, d_hidden, batch, d_logits, rows, params, u,
+                                    ids, nullptr);
+        const auto t1 = std::chrono::steady_clock::now();
+        us[i] = (float)std::chrono::duration<double, std::micro>(t1 - t0).count();
+    }
+    return rc;
+}

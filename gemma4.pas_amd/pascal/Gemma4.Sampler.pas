@@ -32,6 +32,7 @@ const
   CSM_ERR_CREATE = 'SM01';
   CSM_ERR_SAMPLE = 'SM02';
   CSM_ERR_LMHEAD = 'SM03';
+  CSM_ERR_STORE = 'SM04';
 
   G4S_ABI_VERSION = 1;
 
@@ -43,6 +44,9 @@ const
   G4S_ERR_OUT_OF_MEMORY = -4;
   G4S_ERR_HIP = -5;
   G4S_ERR_EMPTY_ROW = -6;
+  G4S_ERR_IO = -7;
+  G4S_ERR_FORMAT = -8;
+  G4S_ERR_NOT_FOUND = -9;
 
   // g4s_dtype
   G4S_DTYPE_F32 = 0;
@@ -60,6 +64,18 @@ const
   G4S_FLAG_WIDE_K = $100;
   G4S_FLAG_EMPTY = $40000000;
   G4S_FLAG_ERROR = $80000000;
+
+  // g4s_wdtype: TDtypeKind (src/Gemma4.Types.pas:94-100), same order
+  G4S_WDTYPE_UNKNOWN = 0;
+  G4S_WDTYPE_BF16 = 1;
+  G4S_WDTYPE_F16 = 2;
+  G4S_WDTYPE_F32 = 3;
+  G4S_WDTYPE_Q4_0 = 4;
+  G4S_MAX_DIMS = 8;
+
+  // device layouts of a Q4_0 matrix
+  G4S_Q4_LAYOUT_ROWS = 0;
+  G4S_Q4_LAYOUT_TILED64 = 1;
 
   // g4s_sample_topk_noalloc: rows per call and bytes of its device array
   G4S_NOALLOC_MAX_ROWS = 32;
@@ -97,6 +113,24 @@ type
   end;
   PG4SOutputs = ^TG4SOutputs;
 
+  { PG4SStore }
+  // opaque g4s_store*
+  PG4SStore = Pointer;
+  PPG4SStore = ^PG4SStore;
+
+  { TG4STensorInfo }
+  // g4s_tensor_info: TTensorInfo (src/Gemma4.Types.pas:119-129) without the
+  // name, with the shape in a fixed array
+  TG4STensorInfo = record
+    SourceDtype: Integer;
+    OutputDtype: Integer;
+    Offset: UInt64;
+    Size: UInt64;
+    NDim: Integer;
+    Shape: array[0..G4S_MAX_DIMS - 1] of Integer;
+  end;
+  PG4STensorInfo = ^TG4STensorInfo;
+
 function g4s_version(): PAnsiChar; cdecl; external CG4SLib;
 procedure g4s_params_set_defaults(AParams: PG4SParams); cdecl; external CG4SLib;
 function g4s_max_top_k(): Integer; cdecl; external CG4SLib;
@@ -123,6 +157,31 @@ function g4s_sample_topk_noalloc(ADevLogits: Pointer; ADType: Integer; AVocab: I
 function g4s_lmhead_q4_0(ASampler: PG4SSampler; ADevWeights: Pointer; ARows: Integer;
   ACols: Integer; ADevHidden: PSingle; ABatch: Integer; ADevLogits: PSingle;
   ALogitsStride: Int64): Integer; cdecl; external CG4SLib;
+function g4s_lmhead_q4_0_tiled(ASampler: PG4SSampler; ADevTiles: Pointer; ARows: Integer;
+  ACols: Integer; ADevHidden: PSingle; ABatch: Integer; ADevLogits: PSingle;
+  ALogitsStride: Int64): Integer; cdecl; external CG4SLib;
+function g4s_lmhead_sample_q4_0(ASampler: PG4SSampler; ADevTiles: Pointer; ACols: Integer;
+  ADevHidden: PSingle; ABatch: Integer; ADevLogits: PSingle; ALogitsStride: Int64;
+  AParams: PG4SParams; AU: PDouble; AIds: PInteger;
+  AOutputs: PG4SOutputs): Integer; cdecl; external CG4SLib;
+function g4s_store_open(AOut: PPG4SStore; AVpkPath: PAnsiChar; AManifestPath: PAnsiChar;
+  AWeightsPath: PAnsiChar): Integer; cdecl; external CG4SLib;
+function g4s_store_close(AStore: PG4SStore): Integer; cdecl; external CG4SLib;
+function g4s_store_last_error(AStore: PG4SStore): PAnsiChar; cdecl; external CG4SLib;
+function g4s_store_tensor_count(AStore: PG4SStore): Integer; cdecl; external CG4SLib;
+function g4s_store_tensor_info(AStore: PG4SStore; AIndex: Integer; AInfo: PG4STensorInfo;
+  AName: PAnsiChar; ANameCapacity: Integer): Integer; cdecl; external CG4SLib;
+function g4s_store_find_tensor(AStore: PG4SStore; AName: PAnsiChar;
+  AInfo: PG4STensorInfo): Integer; cdecl; external CG4SLib;
+function g4s_store_raw_pointer(AStore: PG4SStore; AName: PAnsiChar): Pointer; cdecl;
+  external CG4SLib;
+function g4s_store_verify(AStore: PG4SStore): Integer; cdecl; external CG4SLib;
+function g4s_q4_0_device_bytes(ARows: Integer; ACols: Integer; ALayout: Integer): Int64; cdecl;
+  external CG4SLib;
+function g4s_store_upload_q4_0(AStore: PG4SStore; AName: PAnsiChar; ALayout: Integer;
+  ADevDst: Pointer; ADstBytes: UInt64; AHipStream: Pointer): Integer; cdecl; external CG4SLib;
+function g4s_q4_0_repack(ADevRows: Pointer; ARows: Integer; ACols: Integer;
+  ADevTiled: Pointer; AHipStream: Pointer): Integer; cdecl; external CG4SLib;
 
 type
   { TGpuSampler }
@@ -158,11 +217,41 @@ type
       const ACols: Integer; const ADevHidden: PSingle; const ABatch: Integer;
       const ADevLogits: PSingle; const ALogitsStride: Int64): Boolean;
 
+    // The tied LM head (TILED64 weights from TGpuWeightStore.UploadQ4_0)
+    // fused with the sampler: Forward's last projection + DoSample for
+    // ABatch hidden vectors (Model.pas:1285-1300,2739-2827)
+    function LmHeadSampleQ4_0(const ADevTiles: Pointer; const ACols: Integer;
+      const ADevHidden: PSingle; const ABatch: Integer; const ADevLogits: PSingle;
+      const AParams: PG4SParams; const AU: PDouble; const AIds: PInteger): Boolean;
+
     function LastError(): string;
 
     property Handle: PG4SSampler read FHandle;
     property Vocab: Integer read FVocab;
     property MaxBatch: Integer read FMaxBatch;
+  end;
+
+  { TGpuWeightStore }
+  // TWeightStore (src/Gemma4.Tensors.pas:321-516) on the library: the VPK
+  // archive's manifest and the GPU upload of a Q4_0 tensor.
+  TGpuWeightStore = class(TBaseObject)
+  private
+    FHandle: PG4SStore;
+    function Fail(const AStatus: Integer): Boolean;
+  public
+    destructor Destroy(); override;
+    // AManifestPath / AWeightsPath empty: the engine's E4B/ paths
+    function Open(const AVpkPath: string; const AManifestPath: string = '';
+      const AWeightsPath: string = ''): Boolean;
+    procedure Close();
+    function IsOpen(): Boolean;
+    function TensorCount(): Integer;
+    function FindTensor(const AName: string; out AInfo: TG4STensorInfo): Boolean;
+    // into ADevDst (ADstBytes >= g4s_q4_0_device_bytes(rows, cols, ALayout))
+    function UploadQ4_0(const AName: string; const ALayout: Integer;
+      const ADevDst: Pointer; const ADstBytes: UInt64;
+      const AHipStream: Pointer = nil): Boolean;
+    function LastError(): string;
   end;
 
 implementation
@@ -255,6 +344,107 @@ begin
     ADevLogits, ALogitsStride);
   if LStatus <> G4S_OK then
     Exit(Fail(CSM_ERR_LMHEAD, LStatus));
+  Result := True;
+end;
+
+function TGpuSampler.LmHeadSampleQ4_0(const ADevTiles: Pointer; const ACols: Integer;
+  const ADevHidden: PSingle; const ABatch: Integer; const ADevLogits: PSingle;
+  const AParams: PG4SParams; const AU: PDouble; const AIds: PInteger): Boolean;
+var
+  LStatus: Integer;
+begin
+  LStatus := g4s_lmhead_sample_q4_0(FHandle, ADevTiles, ACols, ADevHidden, ABatch, ADevLogits,
+    FVocab, AParams, AU, AIds, nil);
+  if LStatus <> G4S_OK then
+    Exit(Fail(CSM_ERR_LMHEAD, LStatus));
+  Result := True;
+end;
+
+{ TGpuWeightStore }
+
+destructor TGpuWeightStore.Destroy();
+begin
+  Close();
+  inherited;
+end;
+
+function TGpuWeightStore.LastError(): string;
+begin
+  Result := string(AnsiString(g4s_store_last_error(FHandle)));
+end;
+
+function TGpuWeightStore.Fail(const AStatus: Integer): Boolean;
+begin
+  GetErrors().Add(esError, CSM_ERR_STORE, 'Weight store status %d: %s', [AStatus, LastError()]);
+  Result := False;
+end;
+
+function TGpuWeightStore.Open(const AVpkPath: string; const AManifestPath: string;
+  const AWeightsPath: string): Boolean;
+var
+  LStatus: Integer;
+  LHandle: PG4SStore;
+  LPath, LManifest, LWeights: UTF8String;
+  LPManifest, LPWeights: PAnsiChar;
+begin
+  Close();
+  LHandle := nil;
+  LPath := UTF8String(AVpkPath);
+  LManifest := UTF8String(AManifestPath);
+  LWeights := UTF8String(AWeightsPath);
+  LPManifest := nil;
+  LPWeights := nil;
+  if AManifestPath <> '' then LPManifest := PAnsiChar(LManifest);
+  if AWeightsPath <> '' then LPWeights := PAnsiChar(LWeights);
+  LStatus := g4s_store_open(@LHandle, PAnsiChar(LPath), LPManifest, LPWeights);
+  if LStatus <> G4S_OK then
+  begin
+    // g4s_store_last_error(nil) holds the message of the failed open
+    FHandle := nil;
+    Exit(Fail(LStatus));
+  end;
+  FHandle := LHandle;
+  Result := True;
+end;
+
+procedure TGpuWeightStore.Close();
+begin
+  if FHandle <> nil then
+  begin
+    g4s_store_close(FHandle);
+    FHandle := nil;
+  end;
+end;
+
+function TGpuWeightStore.IsOpen(): Boolean;
+begin
+  Result := FHandle <> nil;
+end;
+
+function TGpuWeightStore.TensorCount(): Integer;
+begin
+  Result := g4s_store_tensor_count(FHandle);
+end;
+
+function TGpuWeightStore.FindTensor(const AName: string; out AInfo: TG4STensorInfo): Boolean;
+var
+  LName: UTF8String;
+begin
+  LName := UTF8String(AName);
+  Result := g4s_store_find_tensor(FHandle, PAnsiChar(LName), @AInfo) = G4S_OK;
+end;
+
+function TGpuWeightStore.UploadQ4_0(const AName: string; const ALayout: Integer;
+  const ADevDst: Pointer; const ADstBytes: UInt64; const AHipStream: Pointer): Boolean;
+var
+  LStatus: Integer;
+  LName: UTF8String;
+begin
+  LName := UTF8String(AName);
+  LStatus := g4s_store_upload_q4_0(FHandle, PAnsiChar(LName), ALayout, ADevDst, ADstBytes,
+    AHipStream);
+  if LStatus <> G4S_OK then
+    Exit(Fail(LStatus));
   Result := True;
 end;
 

@@ -50,7 +50,10 @@ typedef enum g4s_status {
     G4S_ERR_NO_DEVICE = -3,        /* no HIP device / wrong architecture */
     G4S_ERR_OUT_OF_MEMORY = -4,    /* workspace allocation failed at create */
     G4S_ERR_HIP = -5,              /* a HIP runtime call failed */
-    G4S_ERR_EMPTY_ROW = -6         /* a top-k row had no logit above -1e30 (id set to -1) */
+    G4S_ERR_EMPTY_ROW = -6,        /* a top-k row had no logit above -1e30 (id set to -1) */
+    G4S_ERR_IO = -7,               /* weight store: the archive could not be opened or mapped */
+    G4S_ERR_FORMAT = -8,           /* weight store: not a VPK / manifest the engine would accept */
+    G4S_ERR_NOT_FOUND = -9         /* weight store: no such archive entry or tensor */
 } g4s_status;
 
 /* TSamplingParams, src/Gemma4.Model.pas:70-76 (same fields, same meaning).
@@ -197,6 +200,129 @@ int g4s_sample_topk_noalloc(const void* d_logits, int32_t dtype, int32_t vocab,
 int g4s_lmhead_q4_0(g4s_sampler* sampler, const void* d_weights, int32_t rows, int32_t cols,
                     const float* d_hidden, int32_t batch, float* d_logits,
                     int64_t logits_stride);
+
+/* The LM head of g4s_lmhead_q4_0 (same arguments, same bit-exact logits) on
+ * weights in the TILED64 layout (g4s_store_upload_q4_0 / g4s_q4_0_repack):
+ * one wave per 64 weight rows with coalesced weight loads.  d_tiles and
+ * d_hidden 16-byte aligned, batch*cols*4 < 2 GiB.  Stream-ordered.
+ * Replaces the engine's LM-head projection before the sampler
+ * (src/Gemma4.Model.pas:1285-1300; CPU form CpuMatVecQ4,
+ * src/Gemma4.Tensors.pas:546-598). */
+int g4s_lmhead_q4_0_tiled(g4s_sampler* sampler, const void* d_tiles, int32_t rows, int32_t cols,
+                          const float* d_hidden, int32_t batch, float* d_logits,
+                          int64_t logits_stride);
+
+/* The LM head fused with the sampler: logits of `batch` hidden vectors over
+ * the handle's `vocab` rows of TILED64 weights, then g4s_sample_ex on them
+ * (same params / u / ids / outputs, same results).  While it writes the
+ * logits (d_logits, f32, logits_stride >= vocab, a multiple of 4) the LM
+ * head keeps each 64-row group's largest logit; top-k rows then read back
+ * only the groups that can hold their top K (the K-th largest group maximum
+ * bounds the K-th largest logit from below) instead of the whole row.
+ * Other rows take the usual paths on the written logits.  Synchronous.
+ * Replaces: Forward's LM head + readback + DoSample
+ * (src/Gemma4.Model.pas:1285-1300,1379-1387,2739-2827). */
+int g4s_lmhead_sample_q4_0(g4s_sampler* sampler, const void* d_tiles, int32_t cols,
+                           const float* d_hidden, int32_t batch, float* d_logits,
+                           int64_t logits_stride, const g4s_params* params, const double* u,
+                           int32_t* ids, const g4s_outputs* outputs);
+
+/* ------------------------------------------------------------------------
+ * Weight store: the engine's VPK archive and the Q4_0 LM head weight.
+ *
+ * TWeightStore (src/Gemma4.Tensors.pas:321-506) over TVFS
+ * (src/vendor/StdApp/StdApp.VFS.pas:243-363): a memory-mapped VPK0 archive
+ * holding a JSON manifest and one weights file.  The tied embedding of
+ * Gemma 4 ("model.language_model.embed_tokens.weight", Q4_0 [262144, 2560],
+ * src/Gemma4.Model.pas:1297-1298) is the LM head of the sampler's config-5
+ * workload; g4s_store_upload_q4_0 puts it in device memory.
+ * ---------------------------------------------------------------------- */
+
+typedef struct g4s_store g4s_store;
+
+/* TDtypeKind, src/Gemma4.Types.pas:94-100 (same order). */
+typedef enum g4s_wdtype {
+    G4S_WDTYPE_UNKNOWN = 0,
+    G4S_WDTYPE_BF16 = 1,
+    G4S_WDTYPE_F16 = 2,
+    G4S_WDTYPE_F32 = 3,
+    G4S_WDTYPE_Q4_0 = 4
+} g4s_wdtype;
+
+#define G4S_MAX_DIMS 8
+
+/* TTensorInfo, src/Gemma4.Types.pas:119-129 (the name is returned apart). */
+typedef struct g4s_tensor_info {
+    int32_t source_dtype; /* g4s_wdtype */
+    int32_t output_dtype; /* g4s_wdtype */
+    uint64_t offset;      /* bytes from the start of the weights file */
+    uint64_t size;        /* bytes */
+    int32_t ndim;
+    int32_t shape[G4S_MAX_DIMS];
+} g4s_tensor_info;
+
+/* Device layouts of a Q4_0 matrix [rows, cols] (cols % 32 == 0).
+ *   ROWS     the engine's TQ4Block rows as stored (src/Gemma4.Types.pas:
+ *            139-142): per 32 weights an fp16 scale and 16 bytes whose low
+ *            nibble is weight 2j and high nibble weight 2j+1;
+ *            rows*(cols/32)*18 bytes.  The layout of g4s_lmhead_q4_0.
+ *   TILED64  tiles of 64 rows x 32 columns, tile (g, k) at byte
+ *            (g*(cols/32) + k)*1280: 64 binary32 scales (each fp16 scale
+ *            widened as TFloat16.ToSingle, src/Gemma4.Types.pas:438-481),
+ *            then the 64 rows' 16 nibble bytes as stored; rows past the end
+ *            of the matrix have scale 0.  ceil(rows/64)*(cols/32)*1280 bytes.
+ *            The layout of g4s_lmhead_q4_0_tiled. */
+#define G4S_Q4_LAYOUT_ROWS 0
+#define G4S_Q4_LAYOUT_TILED64 1
+
+/* TWeightStore.Open (src/Gemma4.Tensors.pas:321-380): map the archive
+ * (its extension is forced to .vpk as TVFS.Open does), read and parse the
+ * manifest, find the weights file.  manifest_path / weights_path NULL mean
+ * the engine's "E4B/manifest.json" / "E4B/weights.bin" (Types.pas:79,85);
+ * paths are matched case-insensitively with '\' read as '/'.  On failure
+ * *out is NULL and g4s_store_last_error(NULL) says why. */
+int g4s_store_open(g4s_store** out, const char* vpk_path, const char* manifest_path,
+                   const char* weights_path);
+
+/* TWeightStore.Close (Tensors.pas:382-389): unmap and release.  NULL is accepted. */
+int g4s_store_close(g4s_store* store);
+
+/* Message of the last failure on `store`; with NULL, of the last failed
+ * g4s_store_open, g4s_q4_0_repack or handle-free call on this thread. */
+const char* g4s_store_last_error(const g4s_store* store);
+
+/* TWeightStore.TensorCount / GetTensorInfo / FindTensor (Tensors.pas:508-
+ * 516, 457-467).  `name` (optional) receives the NUL-terminated tensor name. */
+int32_t g4s_store_tensor_count(const g4s_store* store);
+int g4s_store_tensor_info(g4s_store* store, int32_t index, g4s_tensor_info* info, char* name,
+                          int32_t name_capacity);
+int g4s_store_find_tensor(g4s_store* store, const char* name, g4s_tensor_info* info);
+
+/* TWeightStore.GetRawPointer (Tensors.pas:469-475): the tensor's bytes in
+ * the mapped archive (host memory, valid until g4s_store_close), or NULL. */
+const void* g4s_store_raw_pointer(g4s_store* store, const char* name);
+
+/* CRC-32 of every archive entry against its directory record (the checksum
+ * TVFS writes when packing, StdApp.VFS.pas:600-602). */
+int g4s_store_verify(g4s_store* store);
+
+/* Bytes a Q4_0 matrix takes in `layout`, or -1 for bad sizes / layouts. */
+int64_t g4s_q4_0_device_bytes(int32_t rows, int32_t cols, int32_t layout);
+
+/* LoadTensor of a Q4_0 tensor (Tensors.pas:477-506) plus the engine's
+ * staged GPU upload (src/Gemma4.Model.pas:494-640): the [rows, cols] Q4_0
+ * tensor `name` is copied into d_dst (device, 16-byte aligned,
+ * dst_bytes >= g4s_q4_0_device_bytes) in `layout`.  Returns when the data
+ * is in place; work is ordered on hip_stream (NULL = default stream). */
+int g4s_store_upload_q4_0(g4s_store* store, const char* name, int32_t layout, void* d_dst,
+                          uint64_t dst_bytes, void* hip_stream);
+
+/* Device-side conversion of a ROWS-layout matrix into TILED64 (stream-
+ * ordered; d_tiled 16-byte aligned, g4s_q4_0_device_bytes(.., TILED64)
+ * bytes).  No counterpart in the reference: the engine repacks on the host
+ * (Model.pas:513-530) into its own planar layout. */
+int g4s_q4_0_repack(const void* d_rows, int32_t rows, int32_t cols, void* d_tiled,
+                    void* hip_stream);
 
 #ifdef __cplusplus
 }

@@ -27,12 +27,14 @@ PAS2C = {
     "PG4SSampler": "g4s_sampler*", "PPG4SSampler": "g4s_sampler**",
     "PG4SParams": "g4s_params*", "PG4SOutputs": "g4s_outputs*", "PDouble": "double*",
     "PInteger": "int32_t*", "PSingle": "float*", "PCardinal": "uint32_t*",
+    "UInt64": "uint64_t", "PG4SStore": "g4s_store*", "PPG4SStore": "g4s_store**",
+    "PG4STensorInfo": "g4s_tensor_info*",
 }
 # canonical C type -> ctypes type
 C2CT = {
     "int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
     "double": ctypes.c_double, "uint32_t": ctypes.c_uint32, "char*": ctypes.c_char_p,
-    None: None,
+    "uint64_t": ctypes.c_uint64, None: None,
 }
 
 
@@ -89,8 +91,8 @@ def header_prototypes():
 def c_struct_fields(name):
     src = _strip_c_comments(open(HEADER).read())
     body = re.search(r"typedef struct %s \{(.*?)\}" % name, src, re.S).group(1)
-    return [(_canon_c(m.group(1)), m.group(2))
-            for m in re.finditer(r"([\w \*]+?)\s*\b(\w+)\s*;", body)]
+    return [(_canon_c(m.group(1)) + (f"[{m.group(3)}]" if m.group(3) else ""), m.group(2))
+            for m in re.finditer(r"([\w \*]+?)\s*\b(\w+)\s*(?:\[(\w+)\])?\s*;", body)]
 
 
 def pascal_record_fields(name):
@@ -98,8 +100,12 @@ def pascal_record_fields(name):
     body = re.search(r"\b%s\s*=\s*record(.*?)\bend;" % name, src, re.S).group(1)
     out = []
     for line in [x.strip() for x in body.split(";") if x.strip()]:
-        fname, typ = [x.strip() for x in line.split(":")]
-        out.append((PAS2C[typ], fname))
+        fname, typ = [x.strip() for x in line.split(":", 1)]
+        arr = re.match(r"array\s*\[\s*0\s*\.\.\s*(\w+)\s*-\s*1\s*\]\s*of\s+(\w+)", typ)
+        if arr:
+            out.append((PAS2C[arr.group(2)] + "[" + arr.group(1) + "]", fname))
+        else:
+            out.append((PAS2C[typ], fname))
     return out
 
 
@@ -111,7 +117,8 @@ def test_every_external_matches_the_header():
 
 
 @pytest.mark.parametrize("c_name,p_name", [("g4s_params", "TG4SParams"),
-                                            ("g4s_outputs", "TG4SOutputs")])
+                                            ("g4s_outputs", "TG4SOutputs"),
+                                            ("g4s_tensor_info", "TG4STensorInfo")])
 def test_records_match_the_structs(c_name, p_name):
     c = c_struct_fields(c_name)
     p = pascal_record_fields(p_name)
@@ -180,7 +187,24 @@ def test_call_every_export_with_the_declared_shapes(lib):
                               ctypes.addressof(u), ctypes.addressof(ids), None) == -1
     assert f["g4s_sample_async"](None, None, 0, 262144, 1, None, None, 64, 0, None, None) == -1
     assert f["g4s_lmhead_q4_0"](None, None, 262144, 2560, None, 1, None, 262144) == -1
+    assert f["g4s_lmhead_q4_0_tiled"](None, None, 262144, 2560, None, 1, None, 262144) == -1
+    assert f["g4s_lmhead_sample_q4_0"](None, None, 2560, None, 1, None, 262144,
+                                       ctypes.addressof(p), ctypes.addressof(u),
+                                       ctypes.addressof(ids), None) == -1
     assert f["g4s_last_error"](None).decode() == "sampler is NULL"
+    # weight store: nil handles are refused, the pure host exports answer
+    st = ctypes.c_void_p(7)
+    assert f["g4s_store_open"](ctypes.addressof(st), b"/nonexistent/x.vpk", None, None) == -7
+    assert st.value is None and b"Failed to open VPK" in f["g4s_store_last_error"](None)
+    assert f["g4s_store_close"](None) == 0
+    assert f["g4s_store_tensor_count"](None) == 0
+    assert f["g4s_store_tensor_info"](None, 0, None, None, 0) == -1
+    assert f["g4s_store_find_tensor"](None, b"x", None) == -1
+    assert f["g4s_store_raw_pointer"](None, b"x") is None
+    assert f["g4s_store_verify"](None) == -1
+    assert f["g4s_store_upload_q4_0"](None, b"x", 0, None, 0, None) == -1
+    assert f["g4s_q4_0_device_bytes"](64, 64, 0) == 64 * 2 * 18
+    assert f["g4s_q4_0_repack"](None, 64, 64, None, None) == -1
     if rc == 0:
         assert f["g4s_destroy"](h) == 0
     assert f["g4s_destroy"](None) == 0
