@@ -909,13 +909,56 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
 
 /* ------------------------------------- candidates from 64-row group maxima */
 
+/* regs_radix_kth over the top DIGITS bytes only, with a wave-aggregated
+ * update of the wave's first digit.  The result is the k-th largest key with
+ * its lower bytes cleared: a lower bound of it that at least k keys reach.
+ * The group maxima of a row mostly share their leading digit, and LDS
+ * atomics to one address serialize, so the lanes holding the first active
+ * lane's digit add their count with one atomic; the other lanes (spread over
+ * many digits in the later pass) add theirs directly. */
+template <int BLOCK, int ITEMS, int DIGITS>
+__device__ uint32_t regs_radix_kth_agg(const uint32_t (&keys)[ITEMS], int k, uint32_t* s_hist,
+                                       int* s_misc)
+{
+    const int tid = threadIdx.x, lane = tid & 63;
+    uint32_t prefix = 0, mask = 0;
+    for (int shift = 24; shift >= 32 - 8 * DIGITS; shift -= 8) {
+        for (int b = tid; b < 256; b += BLOCK) s_hist[b] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < ITEMS; ++q) {
+            const uint32_t v = keys[q];
+            const bool act = v != 0u && (v & mask) == prefix;
+            const uint32_t d = (v >> shift) & 255u;
+            const uint64_t left = __ballot(act);
+            if (left) {
+                const int leader = __builtin_ctzll(left);
+                const uint32_t ld = (uint32_t)__builtin_amdgcn_readlane((int)d, leader);
+                const bool same = act && d == ld;
+                const uint64_t m = __ballot(same);
+                if (lane == leader) atomicAdd(&s_hist[ld], (uint32_t)__popcll(m));
+                if (act && !same) atomicAdd(&s_hist[d], 1u);
+            }
+        }
+        __syncthreads();
+        radix_digit_step(k, s_hist, s_misc);
+        __syncthreads();
+        k -= s_misc[1];
+        prefix |= (uint32_t)s_misc[0] << shift;
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    return prefix;
+}
+
 /* The top-k candidates of rows whose logits come from the tiled LM head,
  * which also leaves each 64-logit group's largest candidate key.  tau0 is
- * the K-th largest group maximum (1 when at most K groups hold a key): K
- * groups hold a key >= tau0, so tau0 is at most the row's K-th largest key,
- * and every key >= tau0 lies in a group whose maximum is >= tau0.  Those
- * groups (about K of them) are read back and their keys >= tau0 become the
- * merge's candidates, laid out as the chunk launch would leave them: slot i
+ * the K-th largest group maximum with its low 16 bits cleared (1 when at
+ * most K groups hold a key): K groups hold a key >= tau0, so tau0 is at most
+ * the row's K-th largest key, and every key >= tau0 lies in a group whose
+ * maximum is >= tau0.  Those groups (about K of them) are read back and
+ * their keys >= tau0 become the merge's candidates, laid out as the chunk
+ * launch would leave them: slot i
  * of the row belongs to chunk i >> cap_log2, every chunk's record carries
  * tau0 as its bound, and the per-wave bounds are 0 (no information).  When
  * the keys >= tau0 outnumber the row's slots (heavy ties), the row is
@@ -925,6 +968,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
  * runs unchanged on the materialized logits. */
 constexpr int kGcBlock = 1024;
 constexpr int kGcItems = 8; /* group maxima per thread: up to 8192 groups */
+constexpr int kGcLoads = 8; /* candidate groups per wave whose logits are loaded together */
 
 __global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const uint32_t* gmax,
                                                               int32_t ngroups, int32_t nwave)
@@ -948,29 +992,33 @@ __global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const 
     uint64_t* rc = a.cand + (int64_t)row * kCandRow;
     if (tid == 0) s_cnt = 0;
 
+    /* thread t holds groups kGcItems*t .. +kGcItems-1 */
     uint32_t keys[kGcItems];
     int nz = 0;
 #pragma unroll
     for (int q = 0; q < kGcItems; ++q) {
-        const int g = tid + q * kGcBlock;
+        const int g = tid * kGcItems + q;
         keys[q] = g < ngroups ? gm[g] : 0u;
         nz += keys[q] != 0u;
     }
     nz = block_sum_i32<kGcBlock>(nz, s_scan);
     uint32_t tau0 = 1u;
     if (nz > K) {
-        int gt, eq;
-        tau0 = regs_radix_kth<kGcBlock, kGcItems>(keys, K, s_hist, s_misc, &gt, &eq);
+        /* two bytes: the K-th largest group maximum to 7 mantissa bits; the
+         * few groups between it and the cleared bound are read back too */
+        tau0 = regs_radix_kth_agg<kGcBlock, kGcItems, 2>(keys, K, s_hist, s_misc);
+        tau0 = tau0 > 1u ? tau0 : 1u;
     }
     /* the candidate groups, ascending */
-    int ng = 0;
+    int ng;
+    {
+        int f = 0;
 #pragma unroll
-    for (int q = 0; q < kGcItems; ++q) {
-        const int f = keys[q] >= tau0 ? 1 : 0;
-        int tot;
-        const int pos = block_exclusive_scan<kGcBlock>(f, s_scan, tot);
-        if (f) s_list[ng + pos] = tid + q * kGcBlock;
-        ng += tot;
+        for (int q = 0; q < kGcItems; ++q) f += keys[q] >= tau0 ? 1 : 0;
+        int pos = block_exclusive_scan<kGcBlock>(f, s_scan, ng);
+#pragma unroll
+        for (int q = 0; q < kGcItems; ++q)
+            if (keys[q] >= tau0) s_list[pos++] = tid * kGcItems + q;
     }
     __syncthreads();
     /* their keys >= tau0, one group per wave at a time (lane = logit) */
@@ -978,16 +1026,27 @@ __global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const 
         const int64_t i = (int64_t)g * 64 + lane;
         return i < a.vocab ? cand_key(lg[i]) : 0u;
     };
-    for (int t = wid; t < ng; t += NW) {
-        const int g = s_list[t];
-        const uint32_t k = gkey(g);
-        const bool c = k >= tau0;
-        const uint64_t m = __ballot(c);
-        int base = 0;
-        if (lane == 0) base = atomicAdd(&s_cnt, __popcll(m));
-        base = __builtin_amdgcn_readfirstlane(base);
-        const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
-        if (c && pos < slots) rc[pos] = cand_pack(k, (uint32_t)(g * 64 + lane));
+    /* kGcLoads groups per wave per round: their loads are issued together */
+    for (int t0 = 0; t0 < ng; t0 += NW * kGcLoads) {
+        uint32_t k[kGcLoads];
+        int g[kGcLoads];
+#pragma unroll
+        for (int j = 0; j < kGcLoads; ++j) {
+            const int t = t0 + wid + NW * j;
+            g[j] = t < ng ? s_list[t] : -1;
+            k[j] = g[j] >= 0 ? gkey(g[j]) : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kGcLoads; ++j) {
+            const bool c = g[j] >= 0 && k[j] >= tau0;
+            const uint64_t m = __ballot(c);
+            if (m == 0ull) continue; /* wave-uniform */
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&s_cnt, __popcll(m));
+            base = __builtin_amdgcn_readfirstlane(base);
+            const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+            if (c && pos < slots) rc[pos] = cand_pack(k[j], (uint32_t)(g[j] * 64 + lane));
+        }
     }
     __syncthreads();
     const int M0 = s_cnt;
@@ -1124,11 +1183,15 @@ hipError_t topk_groups_launch(const TopkConfig& c, const TopkArgs& a, const uint
                               int32_t ngroups, hipStream_t s)
 {
     if (ngroups > kGcBlock * kGcItems) return hipErrorNotSupported;
-    hipLaunchKernelGGL(group_cand_kernel, dim3((unsigned)a.batch), dim3(kGcBlock), 0, s, a, gmax,
-                       ngroups, (int32_t)(c.splits * (c.block / 64)));
+    /* two chunks' slots (>= 8 x kbound) hold the candidates of all but
+     * heavily tied rows, which take the exact record; the merge then loads
+     * only those slots */
+    TopkArgs b = a;
+    b.splits = c.splits < 2 ? c.splits : 2;
+    hipLaunchKernelGGL(group_cand_kernel, dim3((unsigned)a.batch), dim3(kGcBlock), 0, s, b, gmax,
+                       ngroups, (int32_t)(b.splits * (c.block / 64)));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    TopkArgs b = a;
     b.mode = 2;
     if (c.block == 512 && c.items == 16) return launch_one<512, 16, 0>(b, a.kbound, s);
     if (c.block == 1024 && c.items == 32) return launch_one<1024, 32, 0>(b, a.kbound, s);
