@@ -27,6 +27,11 @@ hipError_t lmhead_tiled_launch(const uint8_t* tiles, int32_t rows, int32_t cols,
                                int32_t batch, float* logits, int64_t stride, uint32_t* gmax,
                                hipStream_t s);
 
+/* DoEmbeddingLookup of a ROWS-layout Q4_0 table: hidden[b] = dequantised
+ * row tokens[b] (device) times `scale`. */
+hipError_t embed_q4_0_launch(const uint8_t* w, int32_t rows, int32_t cols, const int32_t* tokens,
+                             int32_t batch, float scale, float* hidden, hipStream_t s);
+
 }  // namespace g4s
 
 #endif

@@ -348,7 +348,42 @@ __global__ __launch_bounds__(64 * kTileWaves) void lmhead_tiled_kernel(
     }
 }
 
+/* DoEmbeddingLookup for a Q4_0 table (src/Gemma4.Model.pas:2047-2080):
+ * row `token` dequantised as DequantQ4Block does (Single(q) * LScale,
+ * src/Gemma4.Quant.pas:209-239; exact) and multiplied by `scale`
+ * (CpuScaleF32, src/Gemma4.Tensors.pas:626-636; one rounding).  One thread
+ * per weight; tokens outside [0, rows) give a zero vector. */
+__global__ __launch_bounds__(256) void embed_q4_kernel(const uint8_t* __restrict__ w, int32_t rows,
+                                                       int32_t nblk, const int32_t* __restrict__ tokens,
+                                                       int32_t batch, float scale,
+                                                       float* __restrict__ out)
+{
+    const int32_t cols = nblk * 32;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)batch * cols) return;
+    const int32_t b = (int32_t)(i / cols), c = (int32_t)(i % cols);
+    const int32_t t = tokens[b];
+    float v = 0.0f;
+    if (t >= 0 && t < rows) {
+        const uint8_t* blk = w + ((int64_t)t * nblk + c / 32) * 18;
+        const float sc = f16_to_f32_ref((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        const uint32_t byte = blk[2 + (c % 32) / 2];
+        const int q = (int)((c & 1) ? (byte >> 4) : (byte & 0x0Fu)) - 8;
+        v = ((float)q * sc) * scale;
+    }
+    out[i] = v;
+}
+
 }  // namespace
+
+hipError_t embed_q4_0_launch(const uint8_t* w, int32_t rows, int32_t cols, const int32_t* tokens,
+                             int32_t batch, float scale, float* hidden, hipStream_t s)
+{
+    const int64_t n = (int64_t)batch * cols;
+    hipLaunchKernelGGL(embed_q4_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w, rows,
+                       cols / 32, tokens, batch, scale, hidden);
+    return hipGetLastError();
+}
 
 hipError_t q4_tile_launch(const uint8_t* src, int32_t rows, int32_t nblk, uint8_t* dst, hipStream_t s)
 {

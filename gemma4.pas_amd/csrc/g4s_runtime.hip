@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "g4s_full.h"
 #include "g4s_lmhead.h"
@@ -524,6 +525,111 @@ G4S_API int g4s_lmhead_q4_0_tiled(g4s_sampler* s, const void* d_tiles, int32_t r
     hipError_t e = g4s::lmhead_tiled_launch((const uint8_t*)d_tiles, rows, cols, d_hidden, batch,
                                             d_logits, logits_stride, nullptr, s->stream);
     if (e != hipSuccess) return hip_fail(s, e, "LM-head kernel launch");
+    return G4S_OK;
+}
+
+G4S_API int g4s_embed_q4_0(g4s_sampler* s, const void* d_weights, int32_t rows, int32_t cols,
+                           const int32_t* d_tokens, int32_t batch, float scale, float* d_hidden)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    if (!d_weights || !d_tokens || !d_hidden)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (rows < 1 || cols < 32 || (cols % 32) != 0 || batch < 1)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "rows %d / cols %d / batch %d", rows, cols, batch);
+    if (((uintptr_t)d_weights & 1u) != 0)
+        return fail(s, G4S_ERR_INVALID_ARGUMENT, "d_weights must be 2-byte aligned");
+    hipError_t e = g4s::embed_q4_0_launch((const uint8_t*)d_weights, rows, cols, d_tokens, batch,
+                                          scale, d_hidden, s->stream);
+    if (e != hipSuccess) return hip_fail(s, e, "embedding kernel launch");
+    return G4S_OK;
+}
+
+namespace {
+
+bool is_eos(int32_t t)
+{
+    return t == G4S_EOS_TOKEN_1 || t == G4S_EOS_TOKEN_2 || t == G4S_EOS_TOKEN_3;
+}
+
+/* DoSample for the rows b with want[b], as runs of consecutive rows (one
+ * synchronous sample per run); u comes from `random` for rows with T > 0. */
+int sample_rows(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
+                int32_t batch, const g4s_params* params, g4s_random_fn random, void* user,
+                const std::vector<uint8_t>& want, std::vector<int32_t>& ids)
+{
+    const int64_t esize = dtype == G4S_DTYPE_F32 ? 4 : 2;
+    std::vector<double> u((size_t)batch, 0.0);
+    for (int32_t b = 0; b < batch; ++b) {
+        if (!want[(size_t)b] || !(params[b].temperature > 0.0f)) continue;
+        u[(size_t)b] = random(user, b);
+        if (!(u[(size_t)b] >= 0.0 && u[(size_t)b] < 1.0))
+            return fail(s, G4S_ERR_INVALID_ARGUMENT, "sequence %d: random() = %g outside [0, 1)", b,
+                        u[(size_t)b]);
+    }
+    for (int32_t b0 = 0; b0 < batch;) {
+        if (!want[(size_t)b0]) {
+            ++b0;
+            continue;
+        }
+        int32_t b1 = b0;
+        while (b1 < batch && want[(size_t)b1]) ++b1;
+        const char* p = static_cast<const char*>(d_logits) + (int64_t)b0 * row_stride * esize;
+        const int rc = sample_sync(s, p, dtype, row_stride, b1 - b0, params + b0, u.data() + b0,
+                                   ids.data() + b0, nullptr, nullptr);
+        if (rc) return rc;
+        b0 = b1;
+    }
+    return G4S_OK;
+}
+
+}  // namespace
+
+G4S_API int g4s_generate(g4s_sampler* s, int32_t batch, const g4s_params* params,
+                         int32_t max_tokens, const void* d_logits, int32_t dtype,
+                         int64_t row_stride, g4s_forward_fn forward, g4s_random_fn random,
+                         g4s_token_fn on_token, void* user, int32_t* tokens, int32_t* lengths)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    int rc = check_logits(s, d_logits, dtype, row_stride, batch);
+    if (rc) return rc;
+    if (!params || !forward || !random || !lengths || (max_tokens > 0 && !tokens))
+        return fail(s, G4S_ERR_INVALID_ARGUMENT,
+                    "params, forward, random, lengths (and tokens) must be non-NULL");
+    const size_t B = (size_t)batch;
+    std::vector<uint8_t> live(B, 1), want(B, 1);
+    std::vector<int32_t> cur(B, -1), len(B, 0), fwd(B, -1);
+    for (size_t b = 0; b < B; ++b) lengths[b] = 0;
+    /* the first token of every sequence, from its prompt's logits (:2889) */
+    rc = sample_rows(s, d_logits, dtype, row_stride, batch, params, random, user, want, cur);
+    if (rc) return rc;
+    for (;;) {
+        bool any = false;
+        for (size_t b = 0; b < B; ++b) {
+            want[b] = 0;
+            fwd[b] = -1;
+            if (!live[b]) continue;
+            if (len[b] >= max_tokens) { /* while LI < AMaxTokens (:2904) */
+                live[b] = 0;
+                continue;
+            }
+            tokens[b * (size_t)max_tokens + (size_t)len[b]] = cur[b]; /* :2906 */
+            lengths[b] = ++len[b];
+            if (is_eos(cur[b]) || (on_token && on_token(user, (int32_t)b, cur[b]) == 0)) {
+                live[b] = 0; /* :2908-2916 */
+                continue;
+            }
+            fwd[b] = cur[b];
+            want[b] = 1;
+            any = true;
+        }
+        if (!any) break;
+        if (forward(user, fwd.data(), batch) != 0) /* :2919 */
+            return fail(s, G4S_ERR_ABORTED, "the forward callback failed");
+        rc = sample_rows(s, d_logits, dtype, row_stride, batch, params, random, user, want, cur);
+        if (rc) return rc; /* :2923 */
+    }
     return G4S_OK;
 }
 

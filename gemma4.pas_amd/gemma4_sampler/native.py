@@ -27,6 +27,9 @@ G4S_ERR_EMPTY_ROW = -6
 G4S_ERR_IO = -7
 G4S_ERR_FORMAT = -8
 G4S_ERR_NOT_FOUND = -9
+G4S_ERR_ABORTED = -10
+
+EOS_TOKENS = (1, 106, 50)  # IsEosToken, src/Gemma4.Types.pas:65-67,554-559
 
 # TDtypeKind (src/Gemma4.Types.pas:94-100)
 WDTYPE_UNKNOWN, WDTYPE_BF16, WDTYPE_F16, WDTYPE_F32, WDTYPE_Q4_0 = range(5)
@@ -55,7 +58,12 @@ EXPORTS = ("g4s_version", "g4s_params_set_defaults", "g4s_max_top_k", "g4s_creat
            "g4s_lmhead_sample_q4_0", "g4s_store_open", "g4s_store_close", "g4s_store_last_error",
            "g4s_store_tensor_count", "g4s_store_tensor_info", "g4s_store_find_tensor",
            "g4s_store_raw_pointer", "g4s_store_verify", "g4s_q4_0_device_bytes",
-           "g4s_store_upload_q4_0", "g4s_q4_0_repack")
+           "g4s_store_upload_q4_0", "g4s_q4_0_repack", "g4s_embed_q4_0", "g4s_generate")
+
+FORWARD_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int32),
+                              ctypes.c_int32)
+RANDOM_FN = ctypes.CFUNCTYPE(ctypes.c_double, ctypes.c_void_p, ctypes.c_int32)
+TOKEN_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32)
 
 
 class TSamplingParams(ctypes.Structure):
@@ -150,6 +158,13 @@ def load():
                                             ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
         L.g4s_q4_0_repack.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                       ctypes.c_void_p, ctypes.c_void_p]
+        L.g4s_embed_q4_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+                                     ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                     ctypes.c_float, ctypes.c_void_p]
+        L.g4s_generate.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                   ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, FORWARD_FN,
+                                   RANDOM_FN, TOKEN_FN, ctypes.c_void_p, ctypes.c_void_p,
+                                   ctypes.c_void_p]
         L.g4s_sample_topk_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                               ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
                                               ctypes.c_void_p, ctypes.c_int32, ctypes.c_float,
@@ -308,6 +323,58 @@ class Sampler:
         if check:
             self._check(rc)
         return rc, ids
+
+    def embed_q4_0(self, d_weights, rows, cols, d_tokens, batch, scale, d_hidden):
+        """DoEmbeddingLookup of a ROWS-layout Q4_0 table (Model.pas:2047-2080)."""
+        rc = load().g4s_embed_q4_0(self.h, _ptr(d_weights), int(rows), int(cols), _ptr(d_tokens),
+                                   int(batch), float(scale), _ptr(d_hidden))
+        self._check(rc)
+
+    def Generate(self, d_logits, batch, params, max_tokens, forward, random, on_token=None,
+                 dtype=DTYPE_F32, row_stride=None):
+        """g4s_generate: TModel.Generate for `batch` sequences.  forward(tokens
+        ndarray) -> bool (True = ok), random(seq) -> float, on_token(seq, token)
+        -> bool (False = stop).  Returns a list of token arrays."""
+        L = load()
+        if isinstance(params, TSamplingParams):
+            params = [params] * batch
+        parr = params_array(params)
+        mt = max(int(max_tokens), 0)
+        toks = np.zeros(max(batch * mt, 1), np.int32)
+        lens = np.zeros(batch, np.int32)
+        errors = []
+
+        def fwd(_, tp, n):
+            try:
+                return 0 if forward(np.ctypeslib.as_array(tp, (n,)).copy()) else 1
+            except Exception as e:  # noqa: BLE001 -- reported after the loop
+                errors.append(e)
+                return 1
+
+        def rnd(_, seq):
+            try:
+                return float(random(int(seq)))
+            except Exception as e:  # noqa: BLE001
+                errors.append(e)
+                return -1.0
+
+        def tok(_, seq, t):
+            try:
+                return 1 if on_token(int(seq), int(t)) else 0
+            except Exception as e:  # noqa: BLE001
+                errors.append(e)
+                return 0
+
+        cf, cr = FORWARD_FN(fwd), RANDOM_FN(rnd)
+        ct = TOKEN_FN(tok) if on_token is not None else ctypes.cast(None, TOKEN_FN)
+        stride = self.vocab if row_stride is None else int(row_stride)
+        rc = L.g4s_generate(self.h, int(batch), parr, int(max_tokens), _ptr(d_logits), int(dtype),
+                            stride, cf, cr, ct, None, toks.ctypes.data_as(ctypes.c_void_p),
+                            lens.ctypes.data_as(ctypes.c_void_p))
+        if errors:
+            raise errors[0]
+        self._check(rc)
+        return [toks[b * mt:b * mt + lens[b]].copy() for b in range(batch)]
 
     def close(self):
         if self.h is not None and self.h.value:

@@ -47,6 +47,12 @@ const
   G4S_ERR_IO = -7;
   G4S_ERR_FORMAT = -8;
   G4S_ERR_NOT_FOUND = -9;
+  G4S_ERR_ABORTED = -10;
+
+  // IsEosToken (src/Gemma4.Types.pas:65-67)
+  G4S_EOS_TOKEN_1 = 1;
+  G4S_EOS_TOKEN_2 = 106;
+  G4S_EOS_TOKEN_3 = 50;
 
   // g4s_dtype
   G4S_DTYPE_F32 = 0;
@@ -131,6 +137,12 @@ type
   end;
   PG4STensorInfo = ^TG4STensorInfo;
 
+  // g4s_generate callbacks (cdecl): the caller's Forward, System.Random per
+  // sequence, and Generate's ACallback per sequence
+  TG4SForwardFn = function(AUser: Pointer; ATokens: PInteger; ABatch: Integer): Integer; cdecl;
+  TG4SRandomFn = function(AUser: Pointer; ASeq: Integer): Double; cdecl;
+  TG4STokenFn = function(AUser: Pointer; ASeq: Integer; AToken: Integer): Integer; cdecl;
+
 function g4s_version(): PAnsiChar; cdecl; external CG4SLib;
 procedure g4s_params_set_defaults(AParams: PG4SParams); cdecl; external CG4SLib;
 function g4s_max_top_k(): Integer; cdecl; external CG4SLib;
@@ -164,6 +176,13 @@ function g4s_lmhead_sample_q4_0(ASampler: PG4SSampler; ADevTiles: Pointer; ACols
   ADevHidden: PSingle; ABatch: Integer; ADevLogits: PSingle; ALogitsStride: Int64;
   AParams: PG4SParams; AU: PDouble; AIds: PInteger;
   AOutputs: PG4SOutputs): Integer; cdecl; external CG4SLib;
+function g4s_embed_q4_0(ASampler: PG4SSampler; ADevWeights: Pointer; ARows: Integer;
+  ACols: Integer; ADevTokens: PInteger; ABatch: Integer; AScale: Single;
+  ADevHidden: PSingle): Integer; cdecl; external CG4SLib;
+function g4s_generate(ASampler: PG4SSampler; ABatch: Integer; AParams: PG4SParams;
+  AMaxTokens: Integer; ADevLogits: Pointer; ADType: Integer; ARowStride: Int64;
+  AForward: TG4SForwardFn; ARandom: TG4SRandomFn; AOnToken: TG4STokenFn; AUser: Pointer;
+  ATokens: PInteger; ALengths: PInteger): Integer; cdecl; external CG4SLib;
 function g4s_store_open(AOut: PPG4SStore; AVpkPath: PAnsiChar; AManifestPath: PAnsiChar;
   AWeightsPath: PAnsiChar): Integer; cdecl; external CG4SLib;
 function g4s_store_close(AStore: PG4SStore): Integer; cdecl; external CG4SLib;

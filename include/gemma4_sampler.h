@@ -53,7 +53,8 @@ typedef enum g4s_status {
     G4S_ERR_EMPTY_ROW = -6,        /* a top-k row had no logit above -1e30 (id set to -1) */
     G4S_ERR_IO = -7,               /* weight store: the archive could not be opened or mapped */
     G4S_ERR_FORMAT = -8,           /* weight store: not a VPK / manifest the engine would accept */
-    G4S_ERR_NOT_FOUND = -9         /* weight store: no such archive entry or tensor */
+    G4S_ERR_NOT_FOUND = -9,        /* weight store: no such archive entry or tensor */
+    G4S_ERR_ABORTED = -10          /* decode loop: the forward callback reported a failure */
 } g4s_status;
 
 /* TSamplingParams, src/Gemma4.Model.pas:70-76 (same fields, same meaning).
@@ -226,6 +227,57 @@ int g4s_lmhead_sample_q4_0(g4s_sampler* sampler, const void* d_tiles, int32_t co
                            const float* d_hidden, int32_t batch, float* d_logits,
                            int64_t logits_stride, const g4s_params* params, const double* u,
                            int32_t* ids, const g4s_outputs* outputs);
+
+/* ------------------------------------------------------------------------
+ * Batched decode loop: TModel.Generate (src/Gemma4.Model.pas:2829-2938) for
+ * `batch` sequences at once, around a forward pass the caller supplies.
+ * ---------------------------------------------------------------------- */
+
+/* IsEosToken, src/Gemma4.Types.pas:65-67,554-559 */
+#define G4S_EOS_TOKEN_1 1
+#define G4S_EOS_TOKEN_2 106
+#define G4S_EOS_TOKEN_3 50
+
+/* The caller's model step (Generate's Forward(LTokenId)): tokens[b] is the
+ * token sequence b feeds next, or -1 when sequence b takes no further step.
+ * On return the raw logits of every sequence with tokens[b] >= 0 must be in
+ * row b of the loop's logits buffer, written by work on the sampler's stream
+ * or already complete.  Return 0 to go on; anything else ends the loop with
+ * G4S_ERR_ABORTED. */
+typedef int (*g4s_forward_fn)(void* user, const int32_t* tokens, int32_t batch);
+
+/* System.Random for sequence `seq`: the uniform in [0,1) its next draw uses.
+ * Called only for rows with T > 0, once per sampled token, sequences in
+ * index order within a step (each sequence sees its own draws in the order
+ * Generate would make them). */
+typedef double (*g4s_random_fn)(void* user, int32_t seq);
+
+/* Generate's ACallback (TGenerateCallback, Model.pas:78-84), per sequence:
+ * return 0 to stop that sequence after `token`. */
+typedef int (*g4s_token_fn)(void* user, int32_t seq, int32_t token);
+
+/* DoEmbeddingLookup (src/Gemma4.Model.pas:2047-2080) for a Q4_0 table in the
+ * ROWS layout: d_hidden[b*cols ..] = dequantised row d_tokens[b] times
+ * `scale` (the engine passes fl32(sqrt(hidden_size))); a token outside
+ * [0, rows) gives zeros.  d_tokens device int32 [batch].  Stream-ordered. */
+int g4s_embed_q4_0(g4s_sampler* sampler, const void* d_weights, int32_t rows, int32_t cols,
+                   const int32_t* d_tokens, int32_t batch, float scale, float* d_hidden);
+
+/* Generate for `batch` sequences (params[b] each), every sequence following
+ * Model.pas:2887-2928: d_logits (dtype, row_stride as for g4s_sample) holds
+ * each sequence's logits after its prompt; the first token is sampled from
+ * them; then, while fewer than max_tokens tokens are out, the token is
+ * appended, an EOS token or a 0 from on_token (may be NULL) ends the
+ * sequence, and otherwise `forward` is called and the next token sampled.
+ * As in the reference, the sequence that appends its max_tokens-th token
+ * still takes that last forward and sample (their token is not returned),
+ * so a caller's random stream advances exactly as Generate's would.
+ * Sequences that end stop taking steps; the rest go on together.  Outputs:
+ * tokens[b*max_tokens + i] (host) and lengths[b] (host).  Synchronous. */
+int g4s_generate(g4s_sampler* sampler, int32_t batch, const g4s_params* params,
+                 int32_t max_tokens, const void* d_logits, int32_t dtype, int64_t row_stride,
+                 g4s_forward_fn forward, g4s_random_fn random, g4s_token_fn on_token, void* user,
+                 int32_t* tokens, int32_t* lengths);
 
 /* ------------------------------------------------------------------------
  * Weight store: the engine's VPK archive and the Q4_0 LM head weight.

@@ -196,3 +196,71 @@ def matvec_q4_batch(matrix, vecs, rows, cols, threads=8):
     dst = np.zeros((B, rows), np.float32)
     load().orc_matvec_q4_batch(_vp(m), _vp(v), _vp(dst), rows, cols, B, threads)
     return dst
+
+
+# --------------------------------------------------------------------------
+# Decode loop (TModel.Generate) and its embedding lookup
+
+EOS_TOKENS = (1, 106, 50)  # CEosTokenId1..3 / IsEosToken, src/Gemma4.Types.pas:65-67,554-559
+
+
+def embed_q4(matrix, token, cols, scale):
+    """DoEmbeddingLookup for a Q4_0 table (src/Gemma4.Model.pas:2047-2080):
+    Q4ToF32Buffer of row `token` (DequantQ4Block per block, Quant.pas:209-239)
+    then CpuScaleF32 by `scale` (Tensors.pas:626-636), in binary32."""
+    nblk = cols // 32
+    m = np.ascontiguousarray(matrix, np.uint8)
+    row = m[token * nblk * 18:(token + 1) * nblk * 18].reshape(nblk, 18)
+    out = np.concatenate([dequant_q4_block(row[k]) for k in range(nblk)])
+    return (out * np.float32(scale)).astype(np.float32)
+
+
+def generate(first_logits, params, max_tokens, forward, random, on_token=None, softcap=30.0):
+    """TModel.Generate (src/Gemma4.Model.pas:2887-2928) for each sequence b of
+    a batch, restated step by step: LTokenId := DoSample (:2889); while
+    LI < AMaxTokens (:2904): append (:2906), stop on IsEosToken (:2908-2909)
+    or a False callback (:2911-2916), Forward (:2919), DoSample (:2923),
+    Inc(LI) (:2926).  Sequences advance together; forward(tokens) gets -1 for
+    sequences that take no step and returns the next logits rows; random(b)
+    stands in for System.Random, called as DoSample would (only T > 0).
+    Returns the token lists."""
+    B = len(params)
+
+    def sample(rows, b):
+        t, k, p = params[b]
+        u = random(b) if t > 0 else 0.0
+        tok, _, _, _ = do_sample(rows[b], t, k, p, u, softcap=softcap, want_probs=False)
+        return tok
+
+    cur = [sample(first_logits, b) for b in range(B)]
+    out = [[] for _ in range(B)]
+    live = [True] * B
+    while True:
+        step = [-1] * B
+        for b in range(B):
+            if not live[b]:
+                continue
+            if len(out[b]) >= max_tokens:
+                live[b] = False
+                continue
+            out[b].append(cur[b])
+            if cur[b] in EOS_TOKENS or (on_token is not None and not on_token(b, cur[b])):
+                live[b] = False
+                continue
+            step[b] = cur[b]
+        if all(t < 0 for t in step):
+            return out
+        rows = forward(step)
+        for b in range(B):
+            if step[b] >= 0:
+                cur[b] = sample(rows, b)
+
+
+def lcg_uniforms(seed):
+    """A multiplicative-congruential stream of uniforms in [0, 1) with 2^-32
+    granularity (x := x * 134775813 + 1 mod 2^32, u = x / 2^32), the shape of
+    the engine's System.Random draws; test input only."""
+    x = seed & 0xFFFFFFFF
+    while True:
+        x = (x * 134775813 + 1) & 0xFFFFFFFF
+        yield x / 4294967296.0

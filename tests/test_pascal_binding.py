@@ -28,7 +28,8 @@ PAS2C = {
     "PG4SParams": "g4s_params*", "PG4SOutputs": "g4s_outputs*", "PDouble": "double*",
     "PInteger": "int32_t*", "PSingle": "float*", "PCardinal": "uint32_t*",
     "UInt64": "uint64_t", "PG4SStore": "g4s_store*", "PPG4SStore": "g4s_store**",
-    "PG4STensorInfo": "g4s_tensor_info*",
+    "PG4STensorInfo": "g4s_tensor_info*", "TG4SForwardFn": "g4s_forward_fn",
+    "TG4SRandomFn": "g4s_random_fn", "TG4STokenFn": "g4s_token_fn",
 }
 # canonical C type -> ctypes type
 C2CT = {
@@ -205,6 +206,9 @@ def test_call_every_export_with_the_declared_shapes(lib):
     assert f["g4s_store_upload_q4_0"](None, b"x", 0, None, 0, None) == -1
     assert f["g4s_q4_0_device_bytes"](64, 64, 0) == 64 * 2 * 18
     assert f["g4s_q4_0_repack"](None, 64, 64, None, None) == -1
+    assert f["g4s_embed_q4_0"](None, None, 64, 64, None, 1, 1.0, None) == -1
+    assert f["g4s_generate"](None, 1, None, 4, None, 0, 64, None, None, None, None, None,
+                             None) == -1
     if rc == 0:
         assert f["g4s_destroy"](h) == 0
     assert f["g4s_destroy"](None) == 0
