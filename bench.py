@@ -86,6 +86,8 @@ def harness():
     H.g4h_graph_chunks.argtypes = [vp, vp, vp, i32, i32, vp, vp, i32, vp, i32, vp]
     H.g4h_lmhead_sampler.argtypes = [vp, vp, vp, i32, i32, vp, i32, vp, vp, vp, i32, vp, i32, i32,
                                      vp, vp]
+    H.g4h_lmhead_tiled.argtypes = [vp, vp, vp, i32, i32, vp, i32, vp, i32, i32, vp]
+    H.g4h_lmhead_sample_fused.argtypes = [vp, vp, i32, i32, vp, i32, vp, vp, vp, vp, i32, i32, vp]
     return H
 
 
@@ -286,9 +288,15 @@ def probe(H, stream, name, steps):
 
 def lmhead_sampler(H, stream, threads, steps):
     """LM head + sampler: 32 hidden vectors ~ N(0,1), 262144 x 2560 Q4_0
-    weights (fp16 scales U(0.001, 0.02)), then T=0.7, K=64, P=0.95.  Every
-    id is checked against the CPU oracle's sampler on the same logits, and
-    the logits of 256 weight rows against the oracle's CpuMatVecQ4."""
+    weights (fp16 scales U(0.001, 0.02)), then T=0.7, K=64, P=0.95.
+
+    Three legs on the same weights: the row-layout LM head followed by the
+    sampler (stream-ordered, event-timed), the TILED64 LM head alone
+    (event-timed) and the fused g4s_lmhead_sample_q4_0 call (synchronous,
+    host-timed).  The logits of the two LM heads must be identical, 256
+    weight rows of them are checked against the oracle's CpuMatVecQ4, and
+    every id of both sampling legs against the oracle's sampler on the same
+    logits."""
     from gemma4_sampler import hip, native, workload as wl
     from oracle import oracle as orc
     B, rows, cols = 32, V, wl.HIDDEN_GEMMA4
@@ -314,6 +322,25 @@ def lmhead_sampler(H, stream, threads, steps):
         raise RuntimeError(f"g4h_lmhead_sampler failed: {rc} {s.last_error()}")
     logits = dl.download(np.float32).reshape(B, rows)
     ids = di.download(np.int32)
+    # TILED64 weights: the LM head alone, then LM head + sample fused
+    dt = hip.Buffer(native.q4_0_device_bytes(rows, cols, native.Q4_LAYOUT_TILED64))
+    native.q4_0_repack(dw, rows, cols, dt, stream=stream)
+    stream.synchronize()
+    tl = np.zeros(steps, np.float32)
+    rc = H.g4h_lmhead_tiled(s.h, stream.handle, dt.ptr, rows, cols, dh.ptr, B, dl.ptr, 2, steps,
+                            _vp(tl))
+    if rc != 0:
+        raise RuntimeError(f"g4h_lmhead_tiled failed: {rc} {s.last_error()}")
+    same_logits = bool(np.array_equal(dl.download(np.uint32).reshape(B, rows),
+                                      logits.view(np.uint32)))
+    fu = np.zeros(steps, np.float32)
+    fids = np.zeros(B, np.int32)
+    uarr = np.ascontiguousarray(u, np.float64)
+    rc = H.g4h_lmhead_sample_fused(s.h, dt.ptr, rows, cols, dh.ptr, B, dl.ptr,
+                                   ctypes.cast(parr, ctypes.c_void_p), _vp(uarr), _vp(fids), 2,
+                                   steps, _vp(fu))
+    if rc != 0:
+        raise RuntimeError(f"g4h_lmhead_sample_fused failed: {rc} {s.last_error()}")
     want = orc.sample_batch(logits, 0, V, V, (np.full(B, 0.7, np.float32), np.full(B, 64, np.int32),
                                               np.full(B, 0.95, np.float32)), u,
                             softcap=wl.SOFTCAP_GEMMA4, threads=threads)
@@ -321,17 +348,23 @@ def lmhead_sampler(H, stream, threads, steps):
     ref = orc.matvec_q4_batch(w_part, hidden, 256, cols, threads=threads)
     logit_bad = int(np.sum(logits[:, 123456:123456 + 256].view(np.uint32) != ref.view(np.uint32)))
     s.close()
-    for b in (dw, dh, dl, dp, du, di):
+    for b in (dw, dh, dl, dp, du, di, dt):
         b.free()
-    lm50, tot50 = float(np.median(lm)), float(np.median(tot))
+    lm50, tot50, tl50, fu50 = (float(np.median(x)) for x in (lm, tot, tl, fu))
     wbytes = rows * (cols // 32) * 18
     flops = 2.0 * B * rows * cols
-    return {"batch": B, "us_per_batch_p50": tot50, "lmhead_us_p50": lm50,
-            "sampler_us_p50": tot50 - lm50, "weights_bytes": wbytes,
-            "lmhead_hbm_gbps": wbytes / (lm50 * 1e-6) / 1e9,
-            "lmhead_tflops": flops / (lm50 * 1e-6) / 1e12,
-            "lmhead_frac_fp32_peak": flops / (lm50 * 1e-6) / 157.3e12,
-            "id_mismatches": int(np.sum(ids != want)),
+    return {"batch": B, "us_per_batch_p50": fu50,
+            "lmhead_us_p50": tl50,
+            "lmhead_tflops": flops / (tl50 * 1e-6) / 1e12,
+            "lmhead_frac_fp32_peak": flops / (tl50 * 1e-6) / 157.3e12,
+            "lmhead_frac_unpacked_fma_peak": flops / (tl50 * 1e-6) / 78.65e12,
+            "lmhead_hbm_gbps": wbytes / (tl50 * 1e-6) / 1e9,
+            "weights_bytes": wbytes,
+            "fused_call": "g4s_lmhead_sample_q4_0 (TILED64 weights; synchronous, host-timed)",
+            "row_layout": {"lmhead_us_p50": lm50, "lmhead_plus_sampler_us_p50": tot50,
+                           "sampler_us_p50": tot50 - lm50},
+            "logits_identical_across_layouts": same_logits,
+            "id_mismatches": int(np.sum(ids != want)) + int(np.sum(fids != want)),
             "logit_mismatches_in_256_checked_rows": logit_bad}
 
 
@@ -516,9 +549,10 @@ def main():
     c5 = {"batch": 32, "status": "not measured"}
     try:
         c5 = lmhead_sampler(H, stream, threads, max(10, args.batch_steps // 5))
-        log(f"LM head + sampler B=32: {c5['us_per_batch_p50']:.1f} us/batch (LM head "
-            f"{c5['lmhead_us_p50']:.1f} us, {c5['lmhead_tflops']:.1f} TFLOP/s), mismatches "
-            f"{c5['id_mismatches']}")
+        log(f"LM head + sampler B=32: fused {c5['us_per_batch_p50']:.1f} us/batch (tiled LM "
+            f"head {c5['lmhead_us_p50']:.1f} us, {c5['lmhead_tflops']:.1f} TFLOP/s; row-layout "
+            f"LM head {c5['row_layout']['lmhead_us_p50']:.1f} us + sampler "
+            f"{c5['row_layout']['sampler_us_p50']:.1f} us), mismatches {c5['id_mismatches']}")
     except (native.SamplerError, RuntimeError) as e:
         c5["status"] = f"not available: {e}"
         log(f"LM head + sampler: {e}")
