@@ -251,7 +251,7 @@ def check_full_rows(seed, batch, params, u, ids, threads):
 def probe(H, stream, name, steps):
     """One workload alone, `steps` launches, for hardware-counter runs:
     copy (128 MiB calibration copy), topk1 (top-k path B=1 fp32),
-    full256 (full path B=256 bf16)."""
+    full256 (full path B=256 bf16), lmhead (TILED64 Q4_0 LM head, B=32)."""
     from gemma4_sampler import hip, native, workload as wl
     if name == "copy":
         nbytes = 128 << 20
@@ -280,6 +280,25 @@ def probe(H, stream, name, steps):
         us, _, _, _ = batch_throughput(H, stream, d, native.DTYPE_BF16, B, par,
                                        wl.host_row_u(SEED + 4, 0, B), 0, 1, 2, steps)
         res = {"probe": name, "bytes_read": B * V * 2, "us_median": float(np.median(us))}
+    elif name == "lmhead":
+        B, cols = 32, wl.HIDDEN_GEMMA4
+        s = native.Sampler(V, max_batch=B, softcap=wl.SOFTCAP_GEMMA4, stream=stream)
+        dw = hip.Buffer(V * (cols // 32) * 18)
+        wl.dev_q4_weights(dw, SEED + 5, V, cols, stream=stream)
+        dt = hip.Buffer(native.q4_0_device_bytes(V, cols, native.Q4_LAYOUT_TILED64))
+        native.q4_0_repack(dw, V, cols, dt, stream=stream)
+        dh = hip.Buffer.from_array(wl.host_hidden(SEED + 6, B, cols))
+        dl = hip.Buffer(4 * B * V)
+        stream.synchronize()
+        dw.free()
+        us = np.zeros(steps, np.float32)
+        rc = H.g4h_lmhead_tiled(s.h, stream.handle, dt.ptr, V, cols, dh.ptr, B, dl.ptr, 1, steps,
+                                _vp(us))
+        if rc != 0:
+            raise RuntimeError(f"g4h_lmhead_tiled failed: {rc} {s.last_error()}")
+        res = {"probe": name, "bytes_read": V * (cols // 32) * 18,
+               "flops": 2.0 * B * V * cols, "us_median": float(np.median(us))}
+        s.close()
     else:
         raise ValueError(f"unknown probe {name}")
     print(json.dumps(res), flush=True)
@@ -420,7 +439,7 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=10000)
     ap.add_argument("--batch-steps", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="small run for profiling")
-    ap.add_argument("--probe", choices=["copy", "topk1", "full256"],
+    ap.add_argument("--probe", choices=["copy", "topk1", "full256", "lmhead"],
                     help="run one workload alone (for hardware-counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
