@@ -154,14 +154,31 @@ __device__ __forceinline__ bool elect_last(uint32_t* ticket, uint32_t count, int
     return *flag != 0;
 }
 
+/* Results a host reads as soon as a row's completion word is published (the
+ * id and flags in pinned host memory): system-scope stores, written through
+ * every cache. */
+__device__ __forceinline__ void st_sys(int32_t* p, int32_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void st_sys(uint32_t* p, uint32_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 /* Publish a row's completion for a host that spins on `done` instead of
- * synchronizing the stream: every store the calling wave made before this
- * point is visible to the host before done[row] reads `seq`.  Called by all
- * lanes of the wave that wrote the row's outputs (lane 0 stores the word). */
+ * synchronizing the stream.  The host then reads only the row's id and flags,
+ * which the calling wave wrote with st_sys: waiting for those stores to
+ * complete (they are written through to the system's point of coherence)
+ * orders them before the completion word, with no writeback of the L2 (a
+ * system-scope release fence would write back the whole XCD's L2).  The
+ * runtime uses `done` only for calls without device-memory outputs.  Called
+ * by all lanes of the wave that wrote the row's results (lane 0 stores the
+ * word). */
 __device__ __forceinline__ void publish_done(uint32_t* done, int row, uint32_t seq)
 {
     if (!done) return;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+    __builtin_amdgcn_s_waitcnt(0);
     if ((threadIdx.x & 63) == 0)
         __hip_atomic_store(done + row, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }

@@ -155,10 +155,10 @@ __global__ __launch_bounds__(kFullBlock) void wide_find_kernel(FullArgs a, int p
         }
         if (total == 0 && tid < 64) {
             if (tid == 0) {
-                a.ids[row] = -1;
+                st_sys(&a.ids[row], -1);
                 if (a.out.count) a.out.count[row] = 0;
                 if (a.out.flags)
-                    a.out.flags[row] = G4S_FLAG_TOPK_PATH | G4S_FLAG_WIDE_K | G4S_FLAG_EMPTY;
+                    st_sys(&a.out.flags[row], G4S_FLAG_TOPK_PATH | G4S_FLAG_WIDE_K | G4S_FLAG_EMPTY);
             }
             publish_done(a.done, row, a.seq);
         }

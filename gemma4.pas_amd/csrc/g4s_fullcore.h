@@ -1041,11 +1041,11 @@ __device__ void write_row_outputs(const FullArgs& a, int row, int32_t id, int32_
                                   int32_t count, uint32_t flags)
 {
     if ((threadIdx.x & 63) == 0) {
-        a.ids[row] = id;
+        st_sys(&a.ids[row], id);
         if (a.out.count) a.out.count[row] = count;
         if (a.out.argmax) a.out.argmax[row] = argmax;
         if (a.out.lsum) a.out.lsum[row] = lsum;
-        if (a.out.flags) a.out.flags[row] = flags;
+        if (a.out.flags) st_sys(&a.out.flags[row], flags);
     }
     publish_done(a.done, row, a.seq);
 }

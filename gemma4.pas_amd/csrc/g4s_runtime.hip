@@ -378,8 +378,12 @@ int sample_sync(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row
         s->h_ids[r] = -1;
         s->h_flags[r] = 0u;
     }
+    /* the completion words carry only the ids and flags: a call that also
+     * asks for device-memory outputs waits for the stream instead */
+    const bool dev_out = user_flags || out.count || out.indices || out.probs || out.argmax ||
+                         out.lsum;
     if (!user_flags) out.flags = s->h_flags;
-    uint32_t* done = !user_flags ? s->h_done : nullptr;
+    uint32_t* done = !dev_out ? s->h_done : nullptr;
 
     if (batch == 1) {
         rc = enqueue(s, d_logits, dtype, row_stride, 1, nullptr, nullptr, &params[0], u[0], kbound,

@@ -245,8 +245,8 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
          * stale id of an earlier call survives */
         if (!a.full_on && chunk == 0 && wid == 0 && a.mode != 1) {
             if (lane == 0) {
-                a.ids[row] = -1;
-                if (a.out.flags) a.out.flags[row] = G4S_FLAG_ERROR | G4S_FLAG_FULL_PATH;
+                st_sys(&a.ids[row], -1);
+                if (a.out.flags) st_sys(&a.out.flags[row], G4S_FLAG_ERROR | G4S_FLAG_FULL_PATH);
             }
             publish_done(a.done, row, a.seq);
         }
@@ -256,8 +256,8 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         if (a.wide_on && K > kMaxTopK) return; /* a wide row (g4s_full.hip) */
         if (chunk == 0 && wid == 0 && a.mode != 1) {
             if (lane == 0) {
-                a.ids[row] = -1;
-                if (a.out.flags) a.out.flags[row] = G4S_FLAG_ERROR | G4S_FLAG_TOPK_PATH;
+                st_sys(&a.ids[row], -1);
+                if (a.out.flags) st_sys(&a.out.flags[row], G4S_FLAG_ERROR | G4S_FLAG_TOPK_PATH);
             }
             publish_done(a.done, row, a.seq);
         }
@@ -757,8 +757,8 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     if (nsurv == 0) {
         if (wid == 0) {
             if (lane == 0) {
-                a.ids[row] = -1;
-                if (a.out.flags) a.out.flags[row] = flags | G4S_FLAG_EMPTY;
+                st_sys(&a.ids[row], -1);
+                if (a.out.flags) st_sys(&a.out.flags[row], flags | G4S_FLAG_EMPTY);
                 if (a.out.count) a.out.count[row] = 0;
             }
             publish_done(a.done, row, a.seq);
@@ -890,11 +890,11 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         }
     }
     if (lane == 0) {
-        a.ids[row] = (int32_t)cand_idx_of(sh.sorted[chosen]);           /* :2826 */
+        st_sys(&a.ids[row], (int32_t)cand_idx_of(sh.sorted[chosen]));   /* :2826 */
         if (a.out.count) a.out.count[row] = nsurv;
         if (a.out.argmax) a.out.argmax[row] = (int32_t)cand_idx_of(sh.sorted[jarg]);
         if (a.out.lsum) a.out.lsum[row] = lsum;
-        if (a.out.flags) a.out.flags[row] = flags;
+        if (a.out.flags) st_sys(&a.out.flags[row], flags);
     }
     if (a.out.indices || a.out.probs) {
         const int capn = a.out.capacity < nsurv ? a.out.capacity : nsurv;
