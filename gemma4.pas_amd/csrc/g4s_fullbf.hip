@@ -14,17 +14,17 @@
  *           by a cubic in x (hardware exp2): predictions only;
  *   row:    m = y(max x) from the handle's table of y per bf16 code; e for
  *           the 8192 codes of the 32 largest binades of |x|, correctly
- *           rounded, one per thread over 32 workgroups per row; the binades
- *           in which a table e is a half-unit tie; the smallest key whose e
- *           is 1.  Workgroup 0: the predicted binade of LSum entering every
- *           chunk and the chunks to stage (a binade crossing predicted within
- *           a relative margin);
+ *           rounded, eight per thread over four workgroups per row; the
+ *           binades in which a table e is a half-unit tie; the smallest key
+ *           whose e is 1.  Workgroup 0: the predicted binade of LSum entering
+ *           every chunk and the chunks to stage (a binade crossing predicted
+ *           within a relative margin).  One more workgroup: chunk 0's e and
+ *           LSum after it, exactly from 0;
  *   lsum:   per chunk the map of its terms in the predicted binade: a term
  *           adds rint(e / u) units, one fma into 1.5 * 2^23 and one integer
- *           add of the result's bits; chunk 0 evaluated exactly from 0;
- *           staged chunks store their lane maps in b and b + 1 and their
- *           terms; the argmax (the first e equal to 1) in the runs that can
- *           hold one;
+ *           add of the result's bits; staged chunks store their terms (the
+ *           chain builds their lane maps in b and b + 1); the argmax (the
+ *           first e equal to 1) in the runs that can hold one;
  *   lchain: one workgroup per row copies the staged chunks to LDS, then
  *           wave 0 walks the chunk maps from the state after chunk 0 and
  *           resolves each crossing from the staged lane maps; LSum, 1/LSum,
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(kFullBlock) void fb_max_kernel(FullArgs a)
 
 /* ------------------------------------------------------------ 2: row */
 
-constexpr int kRowWG = 8;                                   /* table workgroups per row */
+constexpr int kRowWG = 4;                                   /* table workgroups per row */
 constexpr int kRowEnt = kBfTab / (kRowWG * kFullBlock);    /* table entries per thread */
 static_assert(kRowEnt * kRowWG * kFullBlock == kBfTab, "whole workgroups of table entries");
 static_assert(kFullChunk == 4 * kFullBlock, "chunk 0: four terms per thread");
@@ -376,8 +376,9 @@ __device__ __forceinline__ float bf_e(const float* ytab, uint32_t code, int scal
 /* Workgroups 1 .. kRowWG of a row: table entries ((g-1)*kRowEnt + q)*256 +
  * tid, the binades where one is a half-unit tie, the smallest key whose e
  * is 1.  Workgroup 0: the row record, the predicted binade of LSum entering
- * every chunk and the staged chunks, and chunk 0 exactly from 0 (its e,
- * kept for the draw's chunk 0, its first e == 1, and LSum after it). */
+ * every chunk and the staged chunks.  Workgroup kRowWG + 1: chunk 0 exactly
+ * from 0 (its e, kept for the draw's chunk 0, its first e == 1, and LSum
+ * after it), beside workgroup 0's predictions. */
 __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
 {
     __shared__ Scratch sh;
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
     const float m = scale ? ym * inv_t : ym;                           /* Tensors.pas:648-654 */
     int win = (int)((am >> 23) & 0xFFu) - (kBfWin - 1);
     win = win < 0 ? 0 : (win > 223 ? 223 : win);
-    if (g > 0) {
+    if (g > 0 && g <= kRowWG) {
         uint64_t tb = 0ull;
         uint32_t k1 = 0xFFFFFFFFu;
         float ev[kRowEnt];
@@ -429,19 +430,8 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
         return;
     }
 
-    /* the terms of codes outside the table: e(-inf), e(+inf), and the codes
-     * below its binades -- e is monotone in x, so when the largest negative and
-     * the largest positive one give the same e, every code between does
-     * (threads 0-3, one evaluation each; combined after the barriers below) */
-    __shared__ float s_out[4];
-    if (tid < 4) {
-        const uint32_t top = win > 0 ? ((uint32_t)win << 7) - 1u : 0u;
-        const uint32_t code = tid == 0 ? 0xFF80u : (tid == 1 ? 0x7F80u : (tid == 2 ? 0x8000u | top : top));
-        s_out[tid] = bf_e(ytab, code, scale, inv_t, m);
-    }
-
-    /* chunk 0: e of terms 4*tid .. 4*tid+3, its first e == 1 */
-    {
+    if (g > kRowWG) {
+        /* chunk 0: e of terms 4*tid .. 4*tid+3, its first e == 1 */
         const uint2 w = reinterpret_cast<const uint2*>(row_ptr<1>(a, row))[tid];
         float4 e4;
         e4.x = bf_e(ytab, w.x & 0xFFFFu, scale, inv_t, m);
@@ -457,6 +447,37 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
         f1 = e4.x == 1.0f ? (uint32_t)(4 * tid) : f1;
         f1 = wave_min_u32(f1);
         if (lane == 0 && f1 != 0xFFFFFFFFu) atomicMin(&fr->amx, (int32_t)f1);
+        __syncthreads();
+        if (tid >= 64) return;
+        /* LSum through chunk 0 from 0 (Tensors.pas:657-663): the first
+         * kSeqLanes lanes term by term (the sum changes binade every few dozen
+         * terms there), then rounds of lane maps */
+        float t[kFullPer];
+        const float4* src = reinterpret_cast<const float4*>(hbuf + lane * kFullPer);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 v = src[k];
+            t[4 * k] = v.x;
+            t[4 * k + 1] = v.y;
+            t[4 * k + 2] = v.z;
+            t[4 * k + 3] = v.w;
+        }
+        int hit = -1, rounds = 0;
+        State st = seq_walk(hbuf, kSeqLanes * kFullPer, __builtin_inff(), &hit);
+        st = resolve_wave(t, kFullPer, st, __builtin_inff(), kSeqLanes, &hit, &rounds);
+        if (lane == 0) fr->s0 = ss::value_of(st);
+        return;
+    }
+
+    /* the terms of codes outside the table: e(-inf), e(+inf), and the codes
+     * below its binades -- e is monotone in x, so when the largest negative and
+     * the largest positive one give the same e, every code between does
+     * (threads 0-3, one evaluation each; combined after the barriers below) */
+    __shared__ float s_out[4];
+    if (tid < 4) {
+        const uint32_t top = win > 0 ? ((uint32_t)win << 7) - 1u : 0u;
+        const uint32_t code = tid == 0 ? 0xFF80u : (tid == 1 ? 0x7F80u : (tid == 2 ? 0x8000u | top : top));
+        s_out[tid] = bf_e(ytab, code, scale, inv_t, m);
     }
 
     /* predicted LSum entering every chunk: exclusive prefix of the estimates
@@ -491,7 +512,7 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
         }
     }
     int nstaged;
-    int pos = block_excl_scan_i(cnt, sh, nstaged); /* ends with a barrier: hbuf is complete */
+    int pos = block_excl_scan_i(cnt, sh, nstaged);
     int32_t* bl = a.ws.beta_l + rbase;
     BfStage* sg = a.ws.stage + (int64_t)row * kBfStage;
     {
@@ -547,25 +568,6 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
         r.l_reev = r.l_rounds = r.c_reev = r.c_rounds = 0;
         a.ws.rows[row] = r;
         fr->nsl = nstaged < kBfStage ? nstaged : kBfStage;
-    }
-    if (tid < 64) {
-        /* LSum through chunk 0 from 0 (Tensors.pas:657-663): the first
-         * kSeqLanes lanes term by term (the sum changes binade every few dozen
-         * terms there), then rounds of lane maps */
-        float t[kFullPer];
-        const float4* src = reinterpret_cast<const float4*>(hbuf + lane * kFullPer);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float4 v = src[k];
-            t[4 * k] = v.x;
-            t[4 * k + 1] = v.y;
-            t[4 * k + 2] = v.z;
-            t[4 * k + 3] = v.w;
-        }
-        int hit = -1, rounds = 0;
-        State st = seq_walk(hbuf, kSeqLanes * kFullPer, __builtin_inff(), &hit);
-        st = resolve_wave(t, kFullPer, st, __builtin_inff(), kSeqLanes, &hit, &rounds);
-        if (lane == 0) fr->s0 = ss::value_of(st);
     }
 }
 
@@ -785,15 +787,17 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(1, 6))
         w[0] = src[0];
         w[1] = src[1];
     };
-    uint4 w0[2], w1[2];
-    load(w0, cw);
-    if (1 < n) load(w1, cw + 1);
+    uint4 w[kRing][2];
+#pragma unroll
+    for (int r = 0; r < kRing; ++r)
+        if (r < n) load(w[r], cw + r);
     for (int q = 0; q < n; q += kRing) {
-        maps_chunk<P, ALL>(R, w0, q);
-        if (q + kRing < n) load(w0, cw + q + kRing);
-        if (q + 1 < n) {
-            maps_chunk<P, ALL>(R, w1, q + 1);
-            if (q + 1 + kRing < n) load(w1, cw + q + 1 + kRing);
+#pragma unroll
+        for (int r = 0; r < kRing; ++r) {
+            if (q + r < n) {
+                maps_chunk<P, ALL>(R, w[r], q + r);
+                if (q + r + kRing < n) load(w[r], cw + q + r + kRing);
+            }
         }
     }
 }
@@ -1409,7 +1413,7 @@ hipError_t fb_launch(const FullArgs& a0, hipStream_t s)
     }
     const unsigned B = (unsigned)a.batch;
     const dim3 gmax((unsigned)((a.nch + 4 * a.cpw - 1) / (4 * a.cpw)), B);
-    const dim3 grow((unsigned)(kRowWG + 1), B);
+    const dim3 grow((unsigned)(kRowWG + 2), B);
     const int cpw2 = bf_maps_cpw(a.cpw);
     const dim3 gmaps((unsigned)((a.nch + kBfWaves * cpw2 - 1) / (kBfWaves * cpw2)), B);
     const dim3 gchain(1u, B);
