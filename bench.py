@@ -251,7 +251,8 @@ def check_full_rows(seed, batch, params, u, ids, threads):
 def probe(H, stream, name, steps):
     """One workload alone, `steps` launches, for hardware-counter runs:
     copy (128 MiB calibration copy), topk1 (top-k path B=1 fp32),
-    full256 (full path B=256 bf16), lmhead (TILED64 Q4_0 LM head, B=32)."""
+    mixed64 (B=64 fp32 rows with mixed T/K/P), full256 (full path B=256
+    bf16), lmhead (TILED64 Q4_0 LM head, B=32)."""
     from gemma4_sampler import hip, native, workload as wl
     if name == "copy":
         nbytes = 128 << 20
@@ -270,6 +271,16 @@ def probe(H, stream, name, steps):
                                        [native.TSamplingParams.make(0.7, 64, 0.95)], [0.5], 64,
                                        0, 10, steps)
         res = {"probe": name, "bytes_read": V * 4, "us_median": float(np.median(us))}
+    elif name == "mixed64":
+        B = 64
+        d = hip.Buffer(B * V * 4)
+        wl.dev_peaky_rows(d, SEED + 3, 0, B, V, stream=stream)
+        stream.synchronize()
+        t, k, p = wl.host_mixed_params(SEED + 3, 0, B)
+        par = [native.TSamplingParams.make(a, b, c) for a, b, c in zip(t, k, p)]
+        us, _, _, _ = batch_throughput(H, stream, d, native.DTYPE_F32, B, par,
+                                       wl.host_row_u(SEED + 3, 0, B), int(k.max()), 0, 5, steps)
+        res = {"probe": name, "bytes_read": B * V * 4, "us_median": float(np.median(us))}
     elif name == "full256":
         B = 256
         d = hip.Buffer(B * V * 2)
@@ -439,7 +450,7 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=10000)
     ap.add_argument("--batch-steps", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="small run for profiling")
-    ap.add_argument("--probe", choices=["copy", "topk1", "full256", "lmhead"],
+    ap.add_argument("--probe", choices=["copy", "topk1", "mixed64", "full256", "lmhead"],
                     help="run one workload alone (for hardware-counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -484,8 +495,12 @@ def main():
                                     0 if args.no_cpu else args.cpu_rows)
     log(f"decode stream: {bad} mismatching ids of {len(ids)}")
     n_async = min(args.steps, 2000)
+    e_host, e_gpu, e_ids = decode_latency(H, stream, args.warmup, n_async, 2)
+    bad_async = int(np.sum(e_ids != ids[:n_async]))
+    log(f"decode stream (sync API between two hipEvents): host p50 {pct(e_host, 50):.2f} us, "
+        f"GPU events p50 {pct(e_gpu, 50):.2f} us, mismatches {bad_async}")
     a_host, a_gpu, a_ids = decode_latency(H, stream, args.warmup, n_async, 1)
-    bad_async = int(np.sum(a_ids != ids[:n_async]))
+    bad_async += int(np.sum(a_ids != ids[:n_async]))
     log(f"decode stream (async + readback): p50 {pct(a_host, 50):.2f} us, mismatches {bad_async}")
     n_graph = min(args.steps, 2000)
     g_host, g_gpu, g_ids = graph_decode(H, stream, args.warmup, n_graph)
@@ -611,7 +626,8 @@ def main():
                                "100th row greedy; synchronous g4s_sample per row",
                    "batch": 1, "vocab": V, "rows": args.steps},
         "p99_us": pct(host_us, 99),
-        "gpu_event_p50_us": pct(gpu_us, 50),
+        "with_events": {"rows": n_async, "host_p50_us": pct(e_host, 50),
+                        "gpu_event_p50_us": pct(e_gpu, 50)},
         "async_readback_p50_us": pct(a_host, 50),
         "graph_launched": {"rows": n_graph, "gpu_event_p50_us": pct(g_gpu, 50),
                            "gpu_event_p99_us": pct(g_gpu, 99), "host_p50_us": pct(g_host, 50),

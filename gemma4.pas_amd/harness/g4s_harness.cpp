@@ -124,10 +124,13 @@ G4H_API int g4h_graph_floor(void* stream, int32_t n, float* gpu_us)
  * the peaky workload (every `greedy_every`-th row greedy, TopK = 1, with the
  * maximum planted 2-4 more times) is generated into d_row, then sampled with
  * T, K, P and u of that row.
- *   mode 0: g4s_sample (synchronous; host params in, host id out)
+ *   mode 0: g4s_sample (synchronous; host params in, host id out), nothing
+ *           else inside the timed region (gpu_us[r] = 0)
  *   mode 1: g4s_sample_async (params and u already on the device) + a
- *           4-byte id readback and a stream sync
- * host_us[r]: wall clock of the sampler call, entry to id on the host.
+ *           4-byte id readback and a stream sync, between two hipEvents
+ *   mode 2: g4s_sample as in mode 0, between two hipEvents
+ * host_us[r]: wall clock of the sampler call, entry to id on the host
+ *             (modes 1 and 2: including the two event records).
  * gpu_us[r] : hipEvent time of the same work on the sampler's stream.
  * ids[r]    : the sampled token id.
  */
@@ -181,8 +184,17 @@ G4H_API int g4h_decode_latency(g4s_sampler* s, void* stream, void* d_row, uint64
         }
         int32_t id = -1;
         double t0 = now_us();
-        (void)hipEventRecord(e0, st);
         if (mode == 0) {
+            rc = g4s_sample(s, d_row, G4S_DTYPE_F32, vocab, 1, &p, &u, &id);
+            const double t1 = now_us();
+            if (rc != 0) break;
+            host_us[i] = t1 - t0;
+            gpu_us[i] = 0.0f;
+            ids[i] = id;
+            continue;
+        }
+        (void)hipEventRecord(e0, st);
+        if (mode == 2) {
             rc = g4s_sample(s, d_row, G4S_DTYPE_F32, vocab, 1, &p, &u, &id);
             (void)hipEventRecord(e1, st);
         } else {
