@@ -689,13 +689,34 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
     }
     if (cb == 0 || !maps) return;
     if (beta <= -2) {
-        /* a staged chunk: its terms (the chain builds its lane maps) */
+        /* a staged chunk, for the chain: its terms (pad[0]: a code outside the
+         * table) and, in the LSum pass, its lane maps in the predicted binade b
+         * and in b + 1 (ties per the row's mask), with their inclusive lane
+         * scans when both are constant (pad[1] = 1); the draw's chain builds
+         * its own beside its other prologue work */
         BfStage* sg = stg + (-2 - beta);
-        if (lane == 0) sg->pad[0] = outside ? 1 : 0; /* a code outside the table */
+        if (lane == 0) sg->pad[0] = outside ? 1 : 0;
         float4* dst = reinterpret_cast<float4*>(sg->t + lane * kFullPer);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             dst[k] = make_float4(t[4 * k], t[4 * k + 1], t[4 * k + 2], t[4 * k + 3]);
+        const int32_t b = __builtin_amdgcn_readfirstlane(sg->b);
+        if (!P && b >= 1) {
+            bool cst = true;
+            int32_t d[2];
+#pragma nounroll
+            for (int h = 0; h < 2; ++h) {
+                const PMap m = bf_map(t, b + h, outside || tie_possible(tm, tbase, b + h), tmax);
+                (h ? sg->hi : sg->lo)[lane] = m;
+                cst = cst && __ballot(m.d0 != m.d1) == 0;
+                d[h] = m.d0 > ss::kTop ? ss::kTop : m.d0;
+            }
+            if (cst) {
+                sg->xs[lane] = wave_inclusive_scan(d[0]);
+                sg->xs[64 + lane] = wave_inclusive_scan(d[1]);
+            }
+            if (lane == 0) sg->pad[1] = cst ? 1 : 0;
+        }
     } else if (beta >= 1) {
         const PMap cm =
             wave_chunk_map(bf_map(t, beta, outside || tie_possible(tm, tbase, beta), tmax));
@@ -713,7 +734,7 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
  * is left to the chain.  Every wave streams a run of bf_maps_cpw() chunks,
  * kRing of them in flight. */
 template <bool P, bool ALL>
-__global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(1, 6))) void fb_maps_kernel(FullArgs a)
+__global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))) void fb_maps_kernel(FullArgs a)
 {
     __shared__ __align__(16) float tab[kBfTab];
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -806,7 +827,7 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(1, 6))
 
 /* LDS of a chain workgroup: the chunk maps and predicted binades, the exact
  * LSum after every chunk, the wrapping prefix sums of the chunk increments,
- * the walk's stops, the staged chunks and their lane scans. */
+ * the walk's stops and the staged chunks (with their lane maps and scans). */
 struct BfChainLds {
     PMap* cm;
     int32_t* cb;
@@ -816,8 +837,6 @@ struct BfChainLds {
     int32_t* stops;  /* chunks the walk resolves one by one, ascending, then nch */
     int32_t* nstop;
     BfStage* st;
-    int32_t* xs;     /* per staged chunk: inclusive lane scans of its b maps [0..63]
-                        and b + 1 maps [64..127] (constant maps, capped at 2^24) */
 };
 
 __host__ __device__ __forceinline__ size_t bf_chain_lds(int nch, size_t* off)
@@ -839,14 +858,12 @@ __host__ __device__ __forceinline__ size_t bf_chain_lds(int nch, size_t* off)
     o = (o + 15) & ~(size_t)15;
     off[6] = o;
     o += (size_t)kBfStage * sizeof(BfStage);
-    off[7] = o;
-    o += (size_t)kBfStage * 128 * 4;
     return o;
 }
 
 __device__ __forceinline__ BfChainLds bf_chain_layout(char* base, int nch)
 {
-    size_t off[8];
+    size_t off[7];
     (void)bf_chain_lds(nch, off);
     BfChainLds L;
     L.cm = reinterpret_cast<PMap*>(base + off[0]);
@@ -856,7 +873,6 @@ __device__ __forceinline__ BfChainLds bf_chain_layout(char* base, int nch)
     L.stops = reinterpret_cast<int32_t*>(base + off[4]);
     L.nstop = reinterpret_cast<int32_t*>(base + off[5]);
     L.st = reinterpret_cast<BfStage*>(base + off[6]);
-    L.xs = reinterpret_cast<int32_t*>(base + off[7]);
     return L;
 }
 
@@ -874,22 +890,28 @@ __device__ __forceinline__ uint64_t bf_pre_inc(PMap f)
 
 /* Chain prologue (all threads; ends with a barrier): the maps and binades of
  * chunks 0 .. clast (a deferred map, or anything beyond clast, gets binade
- * -1) and the first `ns` staged chunks (every load of a thread issued before
- * its stores).  Then waves 1-3 build each staged chunk's lane maps in its b
- * and b + 1 (ties per the row's mask `tm` from `tbase`; no term exceeds
- * tmax) and, when both are constant, their inclusive lane scans (pad[1] = 1),
- * while wave 0 lists the stops and the prefix sums of the chunk increments. */
+ * -1) and the first `ns` staged chunks, every global load issued before the
+ * first LDS store; then wave 0 lists the stops and the prefix sums of the
+ * chunk increments while, with BUILD, waves 1-3 build each staged chunk's
+ * lane maps in its b and b + 1 (ties per the row's mask `tm` from `tbase`;
+ * no term exceeds tmax) and, when both are constant, their inclusive lane
+ * scans (pad[1] = 1).  Without BUILD the map pass left them in the stage. */
+template <bool BUILD>
 __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_t* gbeta,
                                                   const BfStage* gst, int ns, int nch, int clast,
                                                   const BfChainLds& L, uint64_t tm, int tbase,
                                                   float tmax)
 {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    for (int c = tid; c < nch; c += kFullBlock) {
-        const PMap f = c <= clast ? gmap[c] : ss::map_identity();
-        const int32_t b = c <= clast ? gbeta[c] : -1;
-        L.cm[c] = f;
-        L.cb[c] = (b >= 0 && f.d0 < 0) ? -1 : b;
+    constexpr int kPer = kBfMaxChunks / kFullBlock;
+    PMap f[kPer];
+    int32_t b[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int c = tid + q * kFullBlock;
+        const bool in = c < nch && c <= clast;
+        f[q] = in ? gmap[c] : ss::map_identity();
+        b[q] = in ? gbeta[c] : -1;
     }
     const uint4* src = reinterpret_cast<const uint4*>(gst);
     uint4* dst = reinterpret_cast<uint4*>(L.st);
@@ -897,6 +919,14 @@ __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_
     /* global and LDS never alias: the unrolled loads issue ahead of the stores */
 #pragma unroll 11
     for (int i = tid; i < nvec; i += kFullBlock) dst[i] = src[i];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int c = tid + q * kFullBlock;
+        if (c < nch) {
+            L.cm[c] = f[q];
+            L.cb[c] = (b[q] >= 0 && f[q].d0 < 0) ? -1 : b[q];
+        }
+    }
     __syncthreads();
     if (wid == 0) {
         /* prefix sums of the capped increments and the stops (lane l: chunks
@@ -907,9 +937,9 @@ __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_
         for (int q = 0; q < cpt; ++q) {
             const int c = lane * cpt + q;
             if (c < nch) {
-                const PMap f = L.cm[c];
-                sum += bf_pre_inc(f);
-                nst += bf_stop(f, L.cb[c]) ? 1 : 0;
+                const PMap m = L.cm[c];
+                sum += bf_pre_inc(m);
+                nst += bf_stop(m, L.cb[c]) ? 1 : 0;
             }
         }
         /* every total stays below 2^51 (at most 1024 chunks of 2^24 + 2^40); the
@@ -921,21 +951,20 @@ __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_
         for (int q = 0; q < cpt; ++q) {
             const int c = lane * cpt + q;
             if (c < nch) {
-                const PMap f = L.cm[c];
-                run += bf_pre_inc(f);
+                const PMap m = L.cm[c];
+                run += bf_pre_inc(m);
                 L.pre[c] = run;
-                if (bf_stop(f, L.cb[c])) L.stops[pos++] = c;
+                if (bf_stop(m, L.cb[c])) L.stops[pos++] = c;
             }
         }
         if (lane == 63) {
             L.stops[sincl] = nch;
             *L.nstop = sincl;
         }
-    } else {
+    } else if (BUILD) {
         for (int sl = wid - 1; sl < ns; sl += kFullBlock / 64 - 1) {
             BfStage* sg = L.st + sl;
             const int32_t b = sg->b;
-            sg->pad[1] = 0;
             if (b < 1) continue; /* deferred: the walk re-evaluates it */
             float t[kFullPer];
             const float4* src4 = reinterpret_cast<const float4*>(sg->t + lane * kFullPer);
@@ -947,17 +976,17 @@ __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_
                 t[4 * k + 2] = v.z;
                 t[4 * k + 3] = v.w;
             }
-            /* pad[0]: the chunk holds codes outside the table (not in the tie mask) */
             const bool out = sg->pad[0] != 0;
             const PMap lo = bf_map(t, b, out || tie_possible(tm, tbase, b), tmax);
             const PMap hi = bf_map(t, b + 1, out || tie_possible(tm, tbase, b + 1), tmax);
             sg->lo[lane] = lo;
             sg->hi[lane] = hi;
-            if (__ballot(lo.d0 != lo.d1 || hi.d0 != hi.d1) == 0) {
-                L.xs[sl * 128 + lane] = wave_inclusive_scan(lo.d0 > ss::kTop ? ss::kTop : lo.d0);
-                L.xs[sl * 128 + 64 + lane] = wave_inclusive_scan(hi.d0 > ss::kTop ? ss::kTop : hi.d0);
-                if (lane == 0) sg->pad[1] = 1;
+            const bool cst = __ballot(lo.d0 != lo.d1 || hi.d0 != hi.d1) == 0;
+            if (cst) {
+                sg->xs[lane] = wave_inclusive_scan(lo.d0 > ss::kTop ? ss::kTop : lo.d0);
+                sg->xs[64 + lane] = wave_inclusive_scan(hi.d0 > ss::kTop ? ss::kTop : hi.d0);
             }
+            if (lane == 0) sg->pad[1] = cst ? 1 : 0;
         }
     }
     __syncthreads();
@@ -997,7 +1026,7 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
         const int32_t b = sg->b;
         if (st.e == b && sg->pad[1] != 0) {
             ++*rounds;
-            const int32_t xl = L.xs[sl * 128 + lane];
+            const int32_t xl = sg->xs[lane];
             const int32_t mo = st.m + xl;
             const uint64_t bal = __ballot(mo >= ss::kTop || ss::value_of(State{b, mo}) >= thr);
             if (bal == 0) {
@@ -1005,7 +1034,7 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
                 return st;
             }
             const int ls = (int)__builtin_ctzll(bal);
-            const int32_t xl0 = lane > 0 ? L.xs[sl * 128 + lane - 1] : 0;
+            const int32_t xl0 = lane > 0 ? sg->xs[lane - 1] : 0;
             const int32_t mi = st.m + xl0;
             float sum = ss::value_of(State{b, mi < ss::kTop ? mi : 0});
             int below = 0;
@@ -1023,8 +1052,8 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
             }
             pos = ls + 1;
             if (st.e == b + 1) {
-                const int32_t xh = L.xs[sl * 128 + 64 + lane];
-                const int32_t m2 = st.m + (xh - L.xs[sl * 128 + 64 + ls]);
+                const int32_t xh = sg->xs[64 + lane];
+                const int32_t m2 = st.m + (xh - sg->xs[64 + ls]);
                 const uint64_t bad =
                     __ballot(lane >= pos && (m2 >= ss::kTop || ss::value_of(State{b + 1, m2}) >= thr));
                 if (bad == 0) {
@@ -1134,8 +1163,9 @@ __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
     const FullRow r = a.ws.rows[row];
     const FbRow fr = a.ws.fbrow[row];
     const BfChainLds L = bf_chain_layout(dsm, nch);
-    bf_chain_prologue(a.ws.lmap + rbase, a.ws.beta_l + rbase, a.ws.stage + (int64_t)row * kBfStage,
-                      fr.nsl, nch, nch - 1, L, a.ws.tmask[(int64_t)row * 2], kTieBaseE, 1.0f);
+    bf_chain_prologue<false>(a.ws.lmap + rbase, a.ws.beta_l + rbase,
+                             a.ws.stage + (int64_t)row * kBfStage, fr.nsl, nch, nch - 1, L,
+                             a.ws.tmask[(int64_t)row * 2], kTieBaseE, 1.0f);
     const float T = ri.p.temperature;
     const bool all = term_outputs(a, kRowFull);
     const bool nodraw = !(T > 0.0f);
@@ -1339,8 +1369,9 @@ __global__ __launch_bounds__(kFullBlock) void fb_cdf_chain_kernel(FullArgs a)
     const int nch = a.nch;
     const int64_t rbase = (int64_t)row * a.ws.cstride;
     const BfChainLds L = bf_chain_layout(dsm, nch);
-    bf_chain_prologue(a.ws.cmap + rbase, a.ws.beta_c + rbase, a.ws.stage + (int64_t)row * kBfStage,
-                      fr.nsc, nch, r.c_last, L, a.ws.tmask[(int64_t)row * 2 + 1], kTieBaseP, r.inv);
+    bf_chain_prologue<true>(a.ws.cmap + rbase, a.ws.beta_c + rbase,
+                            a.ws.stage + (int64_t)row * kBfStage, fr.nsc, nch, r.c_last, L,
+                            a.ws.tmask[(int64_t)row * 2 + 1], kTieBaseP, r.inv);
     if (tid >= 64) return;
 
     const float thr = r.thr;
@@ -1396,7 +1427,7 @@ hipError_t fb_launch(const FullArgs& a0, hipStream_t s)
 {
     FullArgs a = a0;
     a.cpw = bf_cpw(a.nch, a.batch);
-    size_t off[8];
+    size_t off[7];
     const size_t lds = bf_chain_lds(a.nch, off);
     /* the chains' dynamic LDS exceeds the default 64 KiB: raise the limit once
      * to what the largest supported vocabulary needs */
