@@ -1013,7 +1013,16 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
     *hit = -1;
     const int sl = beta <= -2 ? -2 - beta : -1;
     const BfStage* sg = sl >= 0 ? L.st + sl : nullptr;
-    if (sg && sg->b >= 1) {
+    /* every LDS read of a staged chunk issued together: its binade, its
+     * terms, and the lane scans of its b and b + 1 maps (the exclusive scan is
+     * the inclusive one less the lane's own capped increment) */
+    int32_t b = -1, cst = 0, xl = 0, xh = 0, own = 0;
+    if (sg) {
+        b = sg->b;
+        cst = sg->pad[1];
+        xl = sg->xs[lane];
+        xh = sg->xs[64 + lane];
+        own = sg->lo[lane].d0;
         const float4* src = reinterpret_cast<const float4*>(sg->t + lane * kFullPer);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -1023,10 +1032,10 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
             t[4 * k + 2] = v.z;
             t[4 * k + 3] = v.w;
         }
-        const int32_t b = sg->b;
-        if (st.e == b && sg->pad[1] != 0) {
+    }
+    if (sg && b >= 1) {
+        if (st.e == b && cst != 0) {
             ++*rounds;
-            const int32_t xl = sg->xs[lane];
             const int32_t mo = st.m + xl;
             const uint64_t bal = __ballot(mo >= ss::kTop || ss::value_of(State{b, mo}) >= thr);
             if (bal == 0) {
@@ -1034,7 +1043,7 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
                 return st;
             }
             const int ls = (int)__builtin_ctzll(bal);
-            const int32_t xl0 = lane > 0 ? sg->xs[lane - 1] : 0;
+            const int32_t xl0 = xl - (own > ss::kTop ? ss::kTop : own);
             const int32_t mi = st.m + xl0;
             float sum = ss::value_of(State{b, mi < ss::kTop ? mi : 0});
             int below = 0;
@@ -1052,8 +1061,7 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
             }
             pos = ls + 1;
             if (st.e == b + 1) {
-                const int32_t xh = sg->xs[64 + lane];
-                const int32_t m2 = st.m + (xh - sg->xs[64 + ls]);
+                const int32_t m2 = st.m + (xh - __builtin_amdgcn_readlane(xh, ls));
                 const uint64_t bad =
                     __ballot(lane >= pos && (m2 >= ss::kTop || ss::value_of(State{b + 1, m2}) >= thr));
                 if (bad == 0) {
