@@ -1096,10 +1096,19 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
  * each run of chunks between two stops applies at once (its increments are
  * a prefix-sum difference) when the sum enters it in the run's predicted
  * binade and stays there (and below thr); otherwise the run is walked
- * chunk map by chunk map.  Each stop is resolved by bf_chain_chunk.  Without
+ * chunk map by chunk map.  Each stop is resolved by bf_chain_chunk.  The
+ * stops and their runs' end values are read ahead, 64 at a time, one per
+ * lane, so that the walk's decisions take them from registers.  Without
  * THR, cpost[c] gets the exact sum after every chunk.  Returns the absolute
  * index of the first term reaching thr (-1: none); st becomes the final
  * state. */
+__device__ __forceinline__ uint64_t rl64(uint64_t v, int l)
+{
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 template <bool THR>
 __device__ int64_t bf_walk(const char* rowp, int c0, int nch, State& st, float thr,
                            const BfChainLds& L, uint32_t base2, const float* gtab, const Ctx& ctx,
@@ -1108,46 +1117,70 @@ __device__ int64_t bf_walk(const char* rowp, int c0, int nch, State& st, float t
     const int lane = threadIdx.x & 63;
     const int nstop = *L.nstop;
     int cur = c0;
-    for (int j = 0; j <= nstop && cur < nch; ++j) {
-        const int s = L.stops[j]; /* stops[nstop] == nch */
-        if (s < cur) continue;
-        if (s > cur) {
-            /* the run cur .. s-1 */
-            const int32_t b = L.cb[cur];
-            const uint64_t p0 = cur > 0 ? L.pre[cur - 1] : 0ull;
-            const uint64_t inc = L.pre[s - 1] - p0; /* >= kNonConst: a map with a tie */
-            const int32_t mend = st.m + (int32_t)(inc < (uint64_t)ss::kTop ? inc : (uint64_t)ss::kTop);
-            bool ok = b == st.e && L.cb[s - 1] == b && mend < ss::kTop;
-            if (THR) ok = ok && ss::value_of(State{b, mend}) < thr;
-            if (ok) {
-                if (!THR)
-                    for (int c = cur + lane; c < s; c += 64)
-                        L.cpost[c] = ss::value_of(State{b, st.m + (int32_t)(L.pre[c] - p0)}); /* constant maps */
-                st.m = mend;
-                cur = s;
-            } else {
-                /* chunk map by chunk map; a chunk whose map does not apply is
-                 * resolved on its own */
-                while (cur < s) {
-                    const int cc = walk_maps<THR>(L.cm, L.cb, cur, s, st, thr, THR ? nullptr : L.cpost);
-                    if (cc >= s) {
-                        cur = s;
-                        break;
+    for (int j0 = 0; j0 <= nstop && cur < nch; j0 += 64) {
+        /* lane q: stop j0 + q and the run before it, which starts after the
+         * previous stop (c0 for the first), read ahead in one batch */
+        const int jq = j0 + lane;
+        const int sq = jq <= nstop ? L.stops[jq] : nch; /* stops[nstop] == nch */
+        const int rq = jq == 0 ? c0 : (jq <= nstop ? L.stops[jq - 1] + 1 : nch);
+        const bool runq = rq < sq;
+        const int32_t bq = runq ? L.cb[rq] : -1;
+        const int32_t eq = runq ? L.cb[sq - 1] : -1;
+        const uint64_t p0q = (runq && rq > 0) ? L.pre[rq - 1] : 0ull;
+        const uint64_t peq = runq ? L.pre[sq - 1] : 0ull;
+        const int jn = nstop + 1 - j0 < 64 ? nstop + 1 - j0 : 64;
+        for (int q = 0; q < jn && cur < nch; ++q) {
+            const int s = __builtin_amdgcn_readlane(sq, q);
+            if (s < cur) continue;
+            if (s > cur) {
+                /* the run cur .. s-1 */
+                int32_t b, be;
+                uint64_t p0, pe;
+                if (cur == __builtin_amdgcn_readlane(rq, q)) {
+                    b = __builtin_amdgcn_readlane(bq, q);
+                    be = __builtin_amdgcn_readlane(eq, q);
+                    p0 = rl64(p0q, q);
+                    pe = rl64(peq, q);
+                } else {
+                    b = L.cb[cur];
+                    be = L.cb[s - 1];
+                    p0 = cur > 0 ? L.pre[cur - 1] : 0ull;
+                    pe = L.pre[s - 1];
+                }
+                const uint64_t inc = pe - p0; /* >= kNonConst: a map with a tie */
+                const int32_t mend = st.m + (int32_t)(inc < (uint64_t)ss::kTop ? inc : (uint64_t)ss::kTop);
+                bool ok = b == st.e && be == b && mend < ss::kTop;
+                if (THR) ok = ok && ss::value_of(State{b, mend}) < thr;
+                if (ok) {
+                    if (!THR) /* constant maps: the sum after each chunk of the run */
+                        for (int c = cur + lane; c < s; c += 64)
+                            L.cpost[c] = ss::value_of(State{b, st.m + (int32_t)(L.pre[c] - p0)});
+                    st.m = mend;
+                    cur = s;
+                } else {
+                    /* chunk map by chunk map; a chunk whose map does not apply is
+                     * resolved on its own */
+                    while (cur < s) {
+                        const int cc = walk_maps<THR>(L.cm, L.cb, cur, s, st, thr, THR ? nullptr : L.cpost);
+                        if (cc >= s) {
+                            cur = s;
+                            break;
+                        }
+                        int h;
+                        st = bf_chain_chunk<THR>(rowp, cc, st, thr, L, base2, gtab, ctx, &h, rounds, amx);
+                        if (h >= 0) return (int64_t)cc * kFullChunk + h;
+                        if (!THR && lane == 0) L.cpost[cc] = ss::value_of(st);
+                        cur = cc + 1;
                     }
-                    int h;
-                    st = bf_chain_chunk<THR>(rowp, cc, st, thr, L, base2, gtab, ctx, &h, rounds, amx);
-                    if (h >= 0) return (int64_t)cc * kFullChunk + h;
-                    if (!THR && lane == 0) L.cpost[cc] = ss::value_of(st);
-                    cur = cc + 1;
                 }
             }
+            if (s >= nch || cur != s) continue;
+            int h;
+            st = bf_chain_chunk<THR>(rowp, s, st, thr, L, base2, gtab, ctx, &h, rounds, amx);
+            if (h >= 0) return (int64_t)s * kFullChunk + h;
+            if (!THR && lane == 0) L.cpost[s] = ss::value_of(st);
+            cur = s + 1;
         }
-        if (s >= nch || cur != s) continue;
-        int h;
-        st = bf_chain_chunk<THR>(rowp, s, st, thr, L, base2, gtab, ctx, &h, rounds, amx);
-        if (h >= 0) return (int64_t)s * kFullChunk + h;
-        if (!THR && lane == 0) L.cpost[s] = ss::value_of(st);
-        cur = s + 1;
     }
     return -1;
 }
