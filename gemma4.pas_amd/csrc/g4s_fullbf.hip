@@ -18,13 +18,13 @@
  *           binades in which a table e is a half-unit tie; the smallest key
  *           whose e is 1.  Workgroup 0: the predicted binade of LSum entering
  *           every chunk and the chunks to stage (a binade crossing predicted
- *           within a relative margin).  One more workgroup: chunk 0's e and
- *           LSum after it, exactly from 0;
+ *           within a relative margin);
  *   lsum:   per chunk the map of its terms in the predicted binade: a term
  *           adds rint(e / u) units, one fma into 1.5 * 2^23 and one integer
- *           add of the result's bits; staged chunks store their terms (the
- *           chain builds their lane maps in b and b + 1); the argmax (the
- *           first e equal to 1) in the runs that can hold one;
+ *           add of the result's bits; staged chunks store their terms and
+ *           their lane maps in b and b + 1; the argmax (the first e equal to
+ *           1) in the runs that can hold one; and, on a wave the last chunks
+ *           leave idle, chunk 0's e and LSum after it, exactly from 0;
  *   lchain: one workgroup per row copies the staged chunks to LDS, then
  *           wave 0 walks the chunk maps from the state after chunk 0 and
  *           resolves each crossing from the staged lane maps; LSum, 1/LSum,
@@ -376,13 +376,11 @@ __device__ __forceinline__ float bf_e(const float* ytab, uint32_t code, int scal
 /* Workgroups 1 .. kRowWG of a row: table entries ((g-1)*kRowEnt + q)*256 +
  * tid, the binades where one is a half-unit tie, the smallest key whose e
  * is 1.  Workgroup 0: the row record, the predicted binade of LSum entering
- * every chunk and the staged chunks.  Workgroup kRowWG + 1: chunk 0 exactly
- * from 0 (its e, kept for the draw's chunk 0, its first e == 1, and LSum
- * after it), beside workgroup 0's predictions. */
+ * every chunk and the staged chunks.  (Chunk 0 is evaluated exactly by the
+ * LSum map pass, beside its chunk maps.) */
 __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
 {
     __shared__ Scratch sh;
-    __shared__ __align__(16) float hbuf[kFullChunk];
     const int tid = threadIdx.x, lane = tid & 63;
     const int row = blockIdx.y, g = blockIdx.x;
     const RowIn ri = row_in(a, row);
@@ -427,45 +425,6 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
             atomicOr((unsigned long long*)&a.ws.tmask[(int64_t)row * 2], (unsigned long long)tb);
         k1 = wave_min_u32(k1);
         if (lane == 0 && k1 != 0xFFFFFFFFu) atomicMin(&fr->key1, k1);
-        return;
-    }
-
-    if (g > kRowWG) {
-        /* chunk 0: e of terms 4*tid .. 4*tid+3, its first e == 1 */
-        const uint2 w = reinterpret_cast<const uint2*>(row_ptr<1>(a, row))[tid];
-        float4 e4;
-        e4.x = bf_e(ytab, w.x & 0xFFFFu, scale, inv_t, m);
-        e4.y = bf_e(ytab, w.x >> 16, scale, inv_t, m);
-        e4.z = bf_e(ytab, w.y & 0xFFFFu, scale, inv_t, m);
-        e4.w = bf_e(ytab, w.y >> 16, scale, inv_t, m);
-        reinterpret_cast<float4*>(hbuf)[tid] = e4;
-        reinterpret_cast<float4*>(a.ws.head + (int64_t)row * kFullChunk)[tid] = e4;
-        uint32_t f1 = 0xFFFFFFFFu;
-        f1 = e4.w == 1.0f ? (uint32_t)(4 * tid + 3) : f1;
-        f1 = e4.z == 1.0f ? (uint32_t)(4 * tid + 2) : f1;
-        f1 = e4.y == 1.0f ? (uint32_t)(4 * tid + 1) : f1;
-        f1 = e4.x == 1.0f ? (uint32_t)(4 * tid) : f1;
-        f1 = wave_min_u32(f1);
-        if (lane == 0 && f1 != 0xFFFFFFFFu) atomicMin(&fr->amx, (int32_t)f1);
-        __syncthreads();
-        if (tid >= 64) return;
-        /* LSum through chunk 0 from 0 (Tensors.pas:657-663): the first
-         * kSeqLanes lanes term by term (the sum changes binade every few dozen
-         * terms there), then rounds of lane maps */
-        float t[kFullPer];
-        const float4* src = reinterpret_cast<const float4*>(hbuf + lane * kFullPer);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float4 v = src[k];
-            t[4 * k] = v.x;
-            t[4 * k + 1] = v.y;
-            t[4 * k + 2] = v.z;
-            t[4 * k + 3] = v.w;
-        }
-        int hit = -1, rounds = 0;
-        State st = seq_walk(hbuf, kSeqLanes * kFullPer, __builtin_inff(), &hit);
-        st = resolve_wave(t, kFullPer, st, __builtin_inff(), kSeqLanes, &hit, &rounds);
-        if (lane == 0) fr->s0 = ss::value_of(st);
         return;
     }
 
@@ -569,6 +528,45 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
         a.ws.rows[row] = r;
         fr->nsl = nstaged < kBfStage ? nstaged : kBfStage;
     }
+}
+
+/* Chunk 0 exactly from 0 (one wave of the LSum map pass, which has the row's
+ * values in its record r): its e, kept for the draw's chunk 0, its first
+ * e == 1, and LSum after it (Tensors.pas:657-663): the first kSeqLanes lanes
+ * term by term (the sum changes binade every few dozen terms there), then
+ * rounds of lane maps. */
+__device__ void bf_head(const FullArgs& a, int row, float* hbuf)
+{
+    const int lane = threadIdx.x & 63;
+    const FullRow r = a.ws.rows[row];
+    FbRow* fr = a.ws.fbrow + row;
+    const uint4* src = reinterpret_cast<const uint4*>(row_ptr<1>(a, row) + (int64_t)lane * kFullPer * 2);
+    const uint4 w0 = src[0], w1 = src[1];
+    const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float t[kFullPer];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        t[2 * i] = bf_e(a.ws.ytab, ww[i] & 0xFFFFu, r.scale, r.inv_t, r.m);
+        t[2 * i + 1] = bf_e(a.ws.ytab, ww[i] >> 16, r.scale, r.inv_t, r.m);
+    }
+    float4* hd = reinterpret_cast<float4*>(a.ws.head + (int64_t)row * kFullChunk + lane * kFullPer);
+    float4* hb = reinterpret_cast<float4*>(hbuf + lane * kFullPer);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 e4 = make_float4(t[4 * k], t[4 * k + 1], t[4 * k + 2], t[4 * k + 3]);
+        hd[k] = e4;
+        hb[k] = e4;
+    }
+    uint32_t f1 = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = kFullPer - 1; j >= 0; --j) f1 = t[j] == 1.0f ? (uint32_t)(lane * kFullPer + j) : f1;
+    f1 = wave_min_u32(f1);
+    if (lane == 0 && f1 != 0xFFFFFFFFu) atomicMin(&fr->amx, (int32_t)f1);
+    wave_lds_sync();
+    int hit = -1, rounds = 0;
+    State st = seq_walk(hbuf, kSeqLanes * kFullPer, __builtin_inff(), &hit);
+    st = resolve_wave(t, kFullPer, st, __builtin_inff(), kSeqLanes, &hit, &rounds);
+    if (lane == 0) fr->s0 = ss::value_of(st);
 }
 
 /* ------------------------------------------ 3 and 5: chunk maps (e, then p) */
@@ -737,6 +735,7 @@ template <bool P, bool ALL>
 __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))) void fb_maps_kernel(FullArgs a)
 {
     __shared__ __align__(16) float tab[kBfTab];
+    __shared__ __align__(16) float hbuf[P ? 4 : kFullChunk];
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int row = blockIdx.y;
     const int nch = a.nch;
@@ -757,6 +756,9 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
             reinterpret_cast<float4*>(tab)[threadIdx.x + q * kBfBlock] = v[q];
     }
     __syncthreads();
+    /* without P, the last wave of the row's last workgroup (one the last
+     * chunks leave idle, or the one with fewest) also evaluates chunk 0 */
+    if (!P && blockIdx.x == gridDim.x - 1 && wid == kBfWaves - 1) bf_head(a, row, hbuf);
     const int cw = (blockIdx.x * kBfWaves + wid) * cpw;
     if (cw > clast) return;
     const int n = clast + 1 - cw < cpw ? clast + 1 - cw : cpw;
@@ -1485,7 +1487,7 @@ hipError_t fb_launch(const FullArgs& a0, hipStream_t s)
     }
     const unsigned B = (unsigned)a.batch;
     const dim3 gmax((unsigned)((a.nch + 4 * a.cpw - 1) / (4 * a.cpw)), B);
-    const dim3 grow((unsigned)(kRowWG + 2), B);
+    const dim3 grow((unsigned)(kRowWG + 1), B);
     const int cpw2 = bf_maps_cpw(a.cpw);
     const dim3 gmaps((unsigned)((a.nch + kBfWaves * cpw2 - 1) / (kBfWaves * cpw2)), B);
     const dim3 gchain(1u, B);

@@ -642,7 +642,7 @@ __device__ State resolve_wave(const float (&t)[kFullPer], int nvalid, State st, 
  * other with plain binary32 additions (the running sum changes binade every
  * few terms there). */
 constexpr int kHeadLanes = 8;
-__device__ State head_walk(const float (&t)[kFullPer], float thr, int* hit)
+[[maybe_unused]] __device__ State head_walk(const float (&t)[kFullPer], float thr, int* hit)
 {
     float s = 0.0f;
     for (int l = 0; l < kHeadLanes; ++l) {
