@@ -569,6 +569,36 @@ __device__ void bf_head(const FullArgs& a, int row, float* hbuf)
     if (lane == 0) fr->s0 = ss::value_of(st);
 }
 
+/* The draw through chunk 0 (Model.pas:2727-2735), one wave of the draw's
+ * map pass: p = fl32(e * inv) of its terms, staged in index order in hbuf,
+ * then as LSum's chunk 0 but against thr. */
+__device__ void bf_draw0(const FullArgs& a, int row, const FullRow& r, float* hbuf)
+{
+    const int lane = threadIdx.x & 63;
+    float t[kFullPer];
+    const float4* src =
+        reinterpret_cast<const float4*>(a.ws.head + (int64_t)row * kFullChunk + lane * kFullPer);
+    float4* hb = reinterpret_cast<float4*>(hbuf + lane * kFullPer);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 e = src[k];
+        t[4 * k] = e.x * r.inv;
+        t[4 * k + 1] = e.y * r.inv;
+        t[4 * k + 2] = e.z * r.inv;
+        t[4 * k + 3] = e.w * r.inv;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hb[k] = make_float4(t[4 * k], t[4 * k + 1], t[4 * k + 2], t[4 * k + 3]);
+    wave_lds_sync();
+    int hit = -1, rounds = 0;
+    State st = seq_walk(hbuf, kSeqLanes * kFullPer, r.thr, &hit);
+    if (hit < 0) st = resolve_wave(t, kFullPer, st, r.thr, kSeqLanes, &hit, &rounds);
+    if (lane == 0) {
+        a.ws.fbrow[row].hit0 = hit;
+        a.ws.fbrow[row].c0 = ss::value_of(st);
+    }
+}
+
 /* ------------------------------------------ 3 and 5: chunk maps (e, then p) */
 
 constexpr int kRing = 2; /* chunks a wave keeps in flight */
@@ -688,10 +718,9 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
     if (cb == 0 || !maps) return;
     if (beta <= -2) {
         /* a staged chunk, for the chain: its terms (pad[0]: a code outside the
-         * table) and, in the LSum pass, its lane maps in the predicted binade b
-         * and in b + 1 (ties per the row's mask), with their inclusive lane
-         * scans when both are constant (pad[1] = 1); the draw's chain builds
-         * its own beside its other prologue work */
+         * table) and its lane maps in the predicted binade b and in b + 1
+         * (ties per the row's mask), with their inclusive lane scans when both
+         * are constant (pad[1] = 1) */
         BfStage* sg = stg + (-2 - beta);
         if (lane == 0) sg->pad[0] = outside ? 1 : 0;
         float4* dst = reinterpret_cast<float4*>(sg->t + lane * kFullPer);
@@ -699,7 +728,7 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
         for (int k = 0; k < 4; ++k)
             dst[k] = make_float4(t[4 * k], t[4 * k + 1], t[4 * k + 2], t[4 * k + 3]);
         const int32_t b = __builtin_amdgcn_readfirstlane(sg->b);
-        if (!P && b >= 1) {
+        if (b >= 1) {
             bool cst = true;
             int32_t d[2];
 #pragma nounroll
@@ -735,7 +764,8 @@ template <bool P, bool ALL>
 __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))) void fb_maps_kernel(FullArgs a)
 {
     __shared__ __align__(16) float tab[kBfTab];
-    __shared__ __align__(16) float hbuf[P ? 4 : kFullChunk];
+    __shared__ __align__(16) float hbuf[kFullChunk];
+    __shared__ uint64_t s_tmw[kBfWaves];
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int row = blockIdx.y;
     const int nch = a.nch;
@@ -746,19 +776,47 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
     const int clast = P ? r.c_last : nch - 1;
     if ((int)blockIdx.x * kBfWaves * cpw > clast) return;
     {
-        const float4* src =
-            reinterpret_cast<const float4*>((P ? a.ws.ptab8 : a.ws.etab8) + (int64_t)row * kBfTab);
+        const float4* src = reinterpret_cast<const float4*>(a.ws.etab8 + (int64_t)row * kBfTab);
         float4 v[kBfTab / 4 / kBfBlock];
 #pragma unroll
         for (int q = 0; q < kBfTab / 4 / kBfBlock; ++q) v[q] = src[threadIdx.x + q * kBfBlock];
+        if (P) {
+            /* the p table (Tensors.pas:666-672) and the binades where one of
+             * its values is a half-unit tie; the first workgroup keeps the
+             * table for the draw's chain (its chunks evaluated anew) */
+            float4* dst = reinterpret_cast<float4*>(a.ws.ptab8 + (int64_t)row * kBfTab);
+            uint64_t tb = 0ull;
+#pragma unroll
+            for (int q = 0; q < kBfTab / 4 / kBfBlock; ++q) {
+                v[q] = make_float4(v[q].x * r.inv, v[q].y * r.inv, v[q].z * r.inv, v[q].w * r.inv);
+                tb |= tie_bits(v[q].x, kTieBaseP) | tie_bits(v[q].y, kTieBaseP) |
+                      tie_bits(v[q].z, kTieBaseP) | tie_bits(v[q].w, kTieBaseP);
+                if (blockIdx.x == 0) dst[threadIdx.x + q * kBfBlock] = v[q];
+            }
+            tb = wave_or64(tb);
+            if (lane == 0) s_tmw[wid] = tb;
+        }
 #pragma unroll
         for (int q = 0; q < kBfTab / 4 / kBfBlock; ++q)
             reinterpret_cast<float4*>(tab)[threadIdx.x + q * kBfBlock] = v[q];
     }
     __syncthreads();
-    /* without P, the last wave of the row's last workgroup (one the last
-     * chunks leave idle, or the one with fewest) also evaluates chunk 0 */
-    if (!P && blockIdx.x == gridDim.x - 1 && wid == kBfWaves - 1) bf_head(a, row, hbuf);
+    uint64_t tm = 0ull;
+    if (P) {
+#pragma unroll
+        for (int k = 0; k < kBfWaves; ++k) tm |= s_tmw[k];
+    } else {
+        tm = a.ws.tmask[(int64_t)row * 2];
+    }
+    /* the last wave of the row's last workgroup (one the last chunks leave
+     * idle, or the one with fewest) also evaluates chunk 0: for LSum, and
+     * for the draw against thr */
+    if (blockIdx.x == clast / (kBfWaves * cpw) && wid == kBfWaves - 1) {
+        if (!P)
+            bf_head(a, row, hbuf);
+        else if (r.nodraw == 0)
+            bf_draw0(a, row, r, hbuf);
+    }
     const int cw = (blockIdx.x * kBfWaves + wid) * cpw;
     if (cw > clast) return;
     const int n = clast + 1 - cw < cpw ? clast + 1 - cw : cpw;
@@ -766,7 +824,6 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
     const int64_t rbase = (int64_t)row * a.ws.cstride;
     const uint32_t base = (uint32_t)r.win_lo << 7;
     const uint32_t base2 = base | (base << 16);
-    const uint64_t tm = a.ws.tmask[(int64_t)row * 2 + (P ? 1 : 0)];
     const int tbase = P ? kTieBaseP : kTieBaseE;
     const int32_t betas = lane < n ? (P ? a.ws.beta_c : a.ws.beta_l)[rbase + cw + lane] : 0;
     PMap* gmap = (P ? a.ws.cmap : a.ws.lmap) + rbase;
@@ -892,17 +949,12 @@ __device__ __forceinline__ uint64_t bf_pre_inc(PMap f)
 
 /* Chain prologue (all threads; ends with a barrier): the maps and binades of
  * chunks 0 .. clast (a deferred map, or anything beyond clast, gets binade
- * -1) and the first `ns` staged chunks, every global load issued before the
- * first LDS store; then wave 0 lists the stops and the prefix sums of the
- * chunk increments while, with BUILD, waves 1-3 build each staged chunk's
- * lane maps in its b and b + 1 (ties per the row's mask `tm` from `tbase`;
- * no term exceeds tmax) and, when both are constant, their inclusive lane
- * scans (pad[1] = 1).  Without BUILD the map pass left them in the stage. */
-template <bool BUILD>
+ * -1) and the first `ns` staged chunks (with the lane maps and scans the map
+ * pass left in them), every global load issued before the first LDS store;
+ * then wave 0 lists the stops and the prefix sums of the chunk increments. */
 __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_t* gbeta,
                                                   const BfStage* gst, int ns, int nch, int clast,
-                                                  const BfChainLds& L, uint64_t tm, int tbase,
-                                                  float tmax)
+                                                  const BfChainLds& L)
 {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     constexpr int kPer = kBfMaxChunks / kFullBlock;
@@ -962,33 +1014,6 @@ __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_
         if (lane == 63) {
             L.stops[sincl] = nch;
             *L.nstop = sincl;
-        }
-    } else if (BUILD) {
-        for (int sl = wid - 1; sl < ns; sl += kFullBlock / 64 - 1) {
-            BfStage* sg = L.st + sl;
-            const int32_t b = sg->b;
-            if (b < 1) continue; /* deferred: the walk re-evaluates it */
-            float t[kFullPer];
-            const float4* src4 = reinterpret_cast<const float4*>(sg->t + lane * kFullPer);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float4 v = src4[k];
-                t[4 * k] = v.x;
-                t[4 * k + 1] = v.y;
-                t[4 * k + 2] = v.z;
-                t[4 * k + 3] = v.w;
-            }
-            const bool out = sg->pad[0] != 0;
-            const PMap lo = bf_map(t, b, out || tie_possible(tm, tbase, b), tmax);
-            const PMap hi = bf_map(t, b + 1, out || tie_possible(tm, tbase, b + 1), tmax);
-            sg->lo[lane] = lo;
-            sg->hi[lane] = hi;
-            const bool cst = __ballot(lo.d0 != lo.d1 || hi.d0 != hi.d1) == 0;
-            if (cst) {
-                sg->xs[lane] = wave_inclusive_scan(lo.d0 > ss::kTop ? ss::kTop : lo.d0);
-                sg->xs[64 + lane] = wave_inclusive_scan(hi.d0 > ss::kTop ? ss::kTop : hi.d0);
-            }
-            if (lane == 0) sg->pad[1] = cst ? 1 : 0;
         }
     }
     __syncthreads();
@@ -1195,8 +1220,6 @@ __device__ int64_t bf_walk(const char* rowp, int c0, int nch, State& st, float t
 __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
 {
     extern __shared__ __align__(16) char dsm[];
-    __shared__ float s_lsum, s_inv;
-    __shared__ int32_t s_amx, s_rounds;
     const int tid = threadIdx.x, lane = tid & 63;
     const int row = blockIdx.y;
     const RowIn ri = row_in(a, row);
@@ -1206,9 +1229,8 @@ __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
     const FullRow r = a.ws.rows[row];
     const FbRow fr = a.ws.fbrow[row];
     const BfChainLds L = bf_chain_layout(dsm, nch);
-    bf_chain_prologue<false>(a.ws.lmap + rbase, a.ws.beta_l + rbase,
-                             a.ws.stage + (int64_t)row * kBfStage, fr.nsl, nch, nch - 1, L,
-                             a.ws.tmask[(int64_t)row * 2], kTieBaseE, 1.0f);
+    bf_chain_prologue(a.ws.lmap + rbase, a.ws.beta_l + rbase,
+                      a.ws.stage + (int64_t)row * kBfStage, fr.nsl, nch, nch - 1, L);
     const float T = ri.p.temperature;
     const bool all = term_outputs(a, kRowFull);
     const bool nodraw = !(T > 0.0f);
@@ -1216,107 +1238,37 @@ __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
     /* fl32(u*TopP) <= 0: the first term's running sum already reaches it */
     const bool direct = !nodraw && !(thr > 0.0f);
     const bool early = (nodraw || direct) && !all;
-    if (tid >= 64 && early) return;
+    if (tid >= 64) return; /* the rest is wave 0's */
 
     const Ctx c0 = make_ctx(a, r, kRowFull);
     const uint32_t base = (uint32_t)r.win_lo << 7;
     const char* rowp = row_ptr<1>(a, row);
-    if (tid < 64) {
-        const float* gtab = a.ws.etab8 + (int64_t)row * kBfTab;
-        State st = ss::state_of(fr.s0);
-        if (lane == 0) L.cpost[0] = fr.s0;
-        int rounds = 0;
-        uint32_t amx = (uint32_t)fr.amx;
-        (void)bf_walk<false>(rowp, 1, nch, st, __builtin_inff(), L, base | (base << 16), gtab, c0,
-                             &rounds, &amx);
-        const float lsum = ss::value_of(st);
-        const float inv = div_cr32(1.0f, lsum);                        /* Tensors.pas:668 */
-        const int32_t argmax = (int32_t)amx;
-        if (early) {
-            uint32_t f = G4S_FLAG_FULL_PATH;
-            if (direct) f |= G4S_FLAG_DREW | G4S_FLAG_REACHED;
-            write_row_outputs(a, row, direct ? 0 : argmax, argmax, lsum, a.vocab, f);
-            return;
-        }
-        if (lane == 0) {
-            s_lsum = lsum;
-            s_inv = inv;
-            s_amx = argmax;
-            s_rounds = rounds;
-            a.ws.fbrow[row].p_ninf = fr.e_ninf * inv;
-            a.ws.fbrow[row].p_pinf = fr.e_pinf * inv;
-            a.ws.fbrow[row].p_tiny = fr.e_tiny * inv; /* NaN stays NaN */
-        }
-    }
-    __syncthreads();
-    const float lsum = s_lsum, inv = s_inv;
-    const int wid = tid >> 6;
-    if (wid == 0) {
-        if (!nodraw && !direct) {
-            /* the draw through chunk 0 (Model.pas:2727-2735): p = fl32(e * inv)
-             * of its terms, staged in index order in the (no longer needed)
-             * first staging slot, then as LSum's chunk 0 but against thr */
-            float t[kFullPer];
-            const float4* src = reinterpret_cast<const float4*>(a.ws.head + (int64_t)row * kFullChunk +
-                                                                lane * kFullPer);
-            float4* hb = reinterpret_cast<float4*>(L.st[0].t + lane * kFullPer);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float4 e = src[k];
-                t[4 * k] = e.x * inv;
-                t[4 * k + 1] = e.y * inv;
-                t[4 * k + 2] = e.z * inv;
-                t[4 * k + 3] = e.w * inv;
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                hb[k] = make_float4(t[4 * k], t[4 * k + 1], t[4 * k + 2], t[4 * k + 3]);
-            wave_lds_sync();
-            int hit = -1, rounds = 0;
-            State st = seq_walk(L.st[0].t, kSeqLanes * kFullPer, thr, &hit);
-            if (hit < 0) st = resolve_wave(t, kFullPer, st, thr, kSeqLanes, &hit, &rounds);
-            if (lane == 0) {
-                a.ws.fbrow[row].hit0 = hit;
-                a.ws.fbrow[row].c0 = ss::value_of(st);
-            }
-        }
+    const float* gtab = a.ws.etab8 + (int64_t)row * kBfTab;
+    State st = ss::state_of(fr.s0);
+    if (lane == 0) L.cpost[0] = fr.s0;
+    int rounds = 0;
+    uint32_t amx = (uint32_t)fr.amx;
+    (void)bf_walk<false>(rowp, 1, nch, st, __builtin_inff(), L, base | (base << 16), gtab, c0,
+                         &rounds, &amx);
+    const float lsum = ss::value_of(st);
+    const float inv = div_cr32(1.0f, lsum);                        /* Tensors.pas:668 */
+    const int32_t argmax = (int32_t)amx;
+    if (early) {
+        uint32_t f = G4S_FLAG_FULL_PATH;
+        if (direct) f |= G4S_FLAG_DREW | G4S_FLAG_REACHED;
+        write_row_outputs(a, row, direct ? 0 : argmax, argmax, lsum, a.vocab, f);
         return;
     }
-    /* waves 1-3: the p table (Tensors.pas:666-672) and the binades where one
-     * of its values is a half-unit tie */
-    {
-        constexpr int kThreads = kFullBlock - 64;
-        constexpr int kPer = (kBfTab / 4 + kThreads - 1) / kThreads;
-        const int t3 = tid - 64;
-        const float4* src = reinterpret_cast<const float4*>(a.ws.etab8 + (int64_t)row * kBfTab);
-        float4* dst = reinterpret_cast<float4*>(a.ws.ptab8 + (int64_t)row * kBfTab);
-        float4 e4[kPer];
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int i = t3 + q * kThreads;
-            if (i < kBfTab / 4) e4[q] = src[i];
-        }
-        uint64_t tb = 0ull;
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int i = t3 + q * kThreads;
-            if (i < kBfTab / 4) {
-                const float4 p4 =
-                    make_float4(e4[q].x * inv, e4[q].y * inv, e4[q].z * inv, e4[q].w * inv);
-                dst[i] = p4;
-                tb |= tie_bits(p4.x, kTieBaseP) | tie_bits(p4.y, kTieBaseP) |
-                      tie_bits(p4.z, kTieBaseP) | tie_bits(p4.w, kTieBaseP);
-            }
-        }
-        tb = wave_or64(tb);
-        if (lane == 0 && tb != 0ull)
-            atomicOr((unsigned long long*)&a.ws.tmask[(int64_t)row * 2 + 1], (unsigned long long)tb);
+    if (lane == 0) {
+        a.ws.fbrow[row].p_ninf = fr.e_ninf * inv;
+        a.ws.fbrow[row].p_pinf = fr.e_pinf * inv;
+        a.ws.fbrow[row].p_tiny = fr.e_tiny * inv; /* NaN stays NaN */
     }
-    if (wid != 1) return;
-    /* wave 1: the last chunk the draw needs (the first whose running sum,
-     * LSum prefix times 1/LSum, surely reaches thr), the draw's predicted
-     * binades and its staged chunks up to there (where the running sum is
-     * predicted to change binade or reach thr); lane l: chunks l*cpt .. */
+    wave_lds_sync(); /* the walk's LSum after every chunk, from every lane */
+    /* the last chunk the draw needs (the first whose running sum, LSum
+     * prefix times 1/LSum, surely reaches thr), the draw's predicted binades
+     * and its staged chunks up to there (where the running sum is predicted
+     * to change binade or reach thr); lane l: chunks l*cpt .. */
     const int cpt = (nch + 63) / 64;
     uint32_t last = (uint32_t)(nch - 1);
     for (int q = 0; q < cpt; ++q) {
@@ -1349,9 +1301,9 @@ __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
         int32_t beta = -1;
         if (cb > 0 && cb <= clast) {
             double pre;
-            const bool st = staged(cb, pre);
+            const bool stg = staged(cb, pre);
             beta = binade_of(pre);
-            if (st) {
+            if (stg) {
                 if (pos < kBfStage) {
                     beta = -2 - pos;
                     sg[pos].b = binade_of(pre * (1.0 - kMargin));
@@ -1368,10 +1320,10 @@ __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
         w.lsum = lsum;
         w.inv = inv;
         w.thr = thr;
-        w.argmax = s_amx;
+        w.argmax = argmax;
         w.c_last = clast;
         w.nodraw = nodraw ? 1 : (direct ? 2 : 0);
-        w.l_rounds = s_rounds;
+        w.l_rounds = rounds;
         a.ws.rows[row] = w;
         a.ws.fbrow[row].nsc = nstaged < kBfStage ? nstaged : kBfStage;
     }
@@ -1394,7 +1346,7 @@ __global__ __launch_bounds__(kFullBlock) void fb_cdf_chain_kernel(FullArgs a)
     }
     if (row_class(a, ri.p.top_k) != kRowFull) return;
     const FbRow fr = a.ws.fbrow[row];
-    __syncthreads();
+    __syncthreads(); /* every thread has read the row's words before they are reset */
     if (tid == 0) fb_reset_row(a, row);
     const FullRow r = a.ws.rows[row];
     if (r.c_last < 0) return;
@@ -1412,9 +1364,8 @@ __global__ __launch_bounds__(kFullBlock) void fb_cdf_chain_kernel(FullArgs a)
     const int nch = a.nch;
     const int64_t rbase = (int64_t)row * a.ws.cstride;
     const BfChainLds L = bf_chain_layout(dsm, nch);
-    bf_chain_prologue<true>(a.ws.cmap + rbase, a.ws.beta_c + rbase,
-                            a.ws.stage + (int64_t)row * kBfStage, fr.nsc, nch, r.c_last, L,
-                            a.ws.tmask[(int64_t)row * 2 + 1], kTieBaseP, r.inv);
+    bf_chain_prologue(a.ws.cmap + rbase, a.ws.beta_c + rbase,
+                      a.ws.stage + (int64_t)row * kBfStage, fr.nsc, nch, r.c_last, L);
     if (tid >= 64) return;
 
     const float thr = r.thr;
