@@ -565,6 +565,16 @@ __device__ void bf_head(const FullArgs& a, int row, float* hbuf)
     wave_lds_sync();
     int hit = -1, rounds = 0;
     State st = seq_walk(hbuf, kSeqLanes * kFullPer, __builtin_inff(), &hit);
+    /* the lane's terms again from LDS: not held in registers across the walk */
+    const float4* hr = reinterpret_cast<const float4*>(hbuf + lane * kFullPer);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 e4 = hr[k];
+        t[4 * k] = e4.x;
+        t[4 * k + 1] = e4.y;
+        t[4 * k + 2] = e4.z;
+        t[4 * k + 3] = e4.w;
+    }
     st = resolve_wave(t, kFullPer, st, __builtin_inff(), kSeqLanes, &hit, &rounds);
     if (lane == 0) fr->s0 = ss::value_of(st);
 }
@@ -592,7 +602,18 @@ __device__ void bf_draw0(const FullArgs& a, int row, const FullRow& r, float* hb
     wave_lds_sync();
     int hit = -1, rounds = 0;
     State st = seq_walk(hbuf, kSeqLanes * kFullPer, r.thr, &hit);
-    if (hit < 0) st = resolve_wave(t, kFullPer, st, r.thr, kSeqLanes, &hit, &rounds);
+    if (hit < 0) {
+        const float4* hr = reinterpret_cast<const float4*>(hbuf + lane * kFullPer);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 p4 = hr[k];
+            t[4 * k] = p4.x;
+            t[4 * k + 1] = p4.y;
+            t[4 * k + 2] = p4.z;
+            t[4 * k + 3] = p4.w;
+        }
+        st = resolve_wave(t, kFullPer, st, r.thr, kSeqLanes, &hit, &rounds);
+    }
     if (lane == 0) {
         a.ws.fbrow[row].hit0 = hit;
         a.ws.fbrow[row].c0 = ss::value_of(st);
