@@ -133,3 +133,86 @@ def test_below_table_codes_that_differ(orc):
     codes[:, 12345] = _b16(np.float32(-1e6))
     t, k, p, u = _settings(rng, B)
     _run(orc, codes, t, k, p, u, CAP, probs=False)
+
+
+def _rn32(fr):
+    """The binary32 nearest to a positive rational (ties to even), exactly."""
+    from fractions import Fraction
+    f = np.float32(float(fr))
+    lo = f if Fraction(float(f)) <= fr else np.nextafter(f, F32(0))
+    hi = np.nextafter(lo, F32(np.inf))
+    dl, dh = fr - Fraction(float(lo)), Fraction(float(hi)) - fr
+    if dl != dh:
+        return lo if dl < dh else hi
+    return lo if (int(lo.view(np.uint32)) & 1) == 0 else hi
+
+
+def _u_for(thr, top_p):
+    """A double u with RN32(u * TopP) == thr (the draw's threshold,
+    Model.pas:2726, the product correctly rounded)."""
+    from fractions import Fraction
+    u = float(Fraction(float(thr)) / Fraction(float(top_p)))
+    for _ in range(64):
+        got = _rn32(Fraction(u) * Fraction(float(top_p)))
+        if got == thr:
+            return u
+        u = float(np.nextafter(u, np.inf if got < thr else -np.inf))
+    raise AssertionError(f"no u gives thr {thr!r}")
+
+
+def _half_unit_ties(p):
+    """Indices i whose step S = RN32(S + p[i]) of the left-to-right binary32
+    running sum is a tie (S + p[i] exactly halfway between two binary32
+    values), and the running sums.  The exact S + p[i] fits a double here."""
+    s = np.add.accumulate(p, dtype=F32)
+    prev = np.concatenate([[0.0], s[:-1].astype(np.float64)])
+    a = prev + p.astype(np.float64)
+    m, e = np.frexp(a)                    # a = m * 2^e, 0.5 <= m < 1
+    q = np.ldexp(a, 25 - e.astype(np.int64))  # units of half the binary32 spacing there
+    tie = (q == np.floor(q)) & (np.mod(q, 2.0) == 1.0) & (p > 0)
+    return np.nonzero(tie)[0], s
+
+
+def test_draw_targets_after_half_unit_ties(orc):
+    """Draws whose threshold is the exact running sum a few lanes after a step
+    that rounds a half-unit tie (Model.pas:2727-2735).  Past chunk 0 the
+    chunk holding the target is staged for the draw chain and the tie sits in
+    a lane before the target's, so it enters through that chunk's lane maps;
+    in chunk 0 it enters through the draw's walk of chunk 0.  A lane map that
+    rounded the tie as if the sum's parity did not matter would leave the
+    running sum one unit off at the target, and the first index that reaches
+    thr would move.  Rows of N(0, 0.5^2) logits are drawn until 12 have such
+    a tie past chunk 0 (they are rare there: a few rows in ten) and 4 more in
+    chunk 0; the expected ids come from the oracle's p and the binary32
+    running sum, and must also be the oracle's own."""
+    rng = np.random.default_rng(61)
+    B = 16
+    picked, targets = [], []
+    for _ in range(400):
+        if len(picked) == B:
+            break
+        need_past0 = len(picked) < 12
+        c = _b16(rng.normal(0, 0.5, V))
+        _, det, idx, pr = orc.do_sample(_widen(c), 1.0, 0, 0.99, 0.5, softcap=CAP, want_probs=True)
+        assert det["count"] == V and np.array_equal(idx, np.arange(V))
+        ties, s = _half_unit_ties(pr)
+        ok = ties[(ties % 1024 < 1024 - 48) & ((ties >= 1024) if need_past0 else (ties < 1024))]
+        if ok.size == 0:
+            continue
+        i = int(ok[0])
+        thr = s[i + 40]
+        if not 0 < thr < F32(0.99):
+            continue
+        picked.append(c)
+        targets.append((i, thr, int(np.argmax(s >= thr))))
+    assert len(picked) == B, f"only {len(picked)} rows with a usable tie"
+    codes = np.stack(picked)
+    rows = _widen(codes)
+    t = np.full(B, 1.0, F32)
+    k = np.zeros(B, np.int32)
+    p = np.full(B, 0.99, F32)
+    u = np.array([_u_for(thr, p[r]) for r, (_, thr, _) in enumerate(targets)])
+    for r, (i, thr, first) in enumerate(targets):
+        tok, _, _, _ = orc.do_sample(rows[r], 1.0, 0, 0.99, u[r], softcap=CAP, want_probs=False)
+        assert tok == first, f"row {r}: oracle {tok}, running sum says {first} (tie at {i})"
+    _run(orc, codes, t, k, p, u, CAP, probs=False)
