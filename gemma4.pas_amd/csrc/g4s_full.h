@@ -140,7 +140,8 @@ struct FullWorkspace {
     float* etab = nullptr;       /* [max_batch][kFullTab] e of the tabulated bf16 codes */
     float* ptab = nullptr;       /* [max_batch][kFullTab] p of the same codes */
     uint64_t* tmask = nullptr;   /* [max_batch][2] binades where a table e ([0]) or p
-                                    ([1]) is a half-unit tie (64-binade windows) */
+                                    ([1]) is a half-unit tie (64-binade windows); the
+                                    bf16 rows' draw pass keeps its p mask in LDS */
     /* wide rows */
     WideSel* sel = nullptr;      /* [max_batch] */
     uint32_t* hist = nullptr;    /* [max_batch][kWideBins], zero between launches */

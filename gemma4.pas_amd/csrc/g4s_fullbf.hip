@@ -28,11 +28,11 @@
  *   lchain: one workgroup per row copies the staged chunks to LDS, then
  *           wave 0 walks the chunk maps from the state after chunk 0 and
  *           resolves each crossing from the staged lane maps; LSum, 1/LSum,
- *           the p table, the draw's predicted binades, staged chunks and
- *           last chunk;
- *   cdf:    the same maps for p up to the draw's predicted last chunk (every
- *           chunk when all probabilities are requested), chunk 0 exactly
- *           against thr = fl32(u * TopP);
+ *           the draw's predicted binades, staged chunks and last chunk;
+ *   cdf:    the p table from the e table, the same maps for p up to the
+ *           draw's predicted last chunk (every chunk when all probabilities
+ *           are requested), and on an idle wave chunk 0 exactly against
+ *           thr = fl32(u * TopP);
  *   dchain: the walk against thr: the exact first index, and the token.
  *
  * Chunks are 1024 terms, one wave's (16 consecutive terms per lane), as in
@@ -362,7 +362,6 @@ __global__ __launch_bounds__(kFullBlock) void fb_max_kernel(FullArgs a)
 constexpr int kRowWG = 4;                                   /* table workgroups per row */
 constexpr int kRowEnt = kBfTab / (kRowWG * kFullBlock);    /* table entries per thread */
 static_assert(kRowEnt * kRowWG * kFullBlock == kBfTab, "whole workgroups of table entries");
-static_assert(kFullChunk == 4 * kFullBlock, "chunk 0: four terms per thread");
 
 /* e of one bf16 code: RN32(exp(y - m)), y from the handle's table scaled by
  * 1/T when the row scales (the same value e_direct computes). */
@@ -773,10 +772,11 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
 }
 
 /* One pass over the chunks 1 .. clast of every full row (chunk 0 is
- * evaluated exactly by the row kernel and the LSum chain): the terms from
- * the LDS table (e, or p when P), per chunk its map in the predicted binade
- * (or, for a staged chunk, its lane maps in b and b + 1 and its terms).
- * Without P: the argmax in the chunks whose run can hold an e == 1.  With
+ * evaluated exactly, on the last wave of the row's last workgroup): the
+ * terms from the LDS table (e, or p when P, made from the e table as it is
+ * copied), per chunk its map in the predicted binade (or, for a staged
+ * chunk, its lane maps in b and b + 1 and its terms).  Without P: the
+ * argmax in the chunks whose run can hold an e == 1.  With
  * ALL (P and every probability requested): the probabilities, including
  * those of codes outside the table; otherwise a chunk holding such a code
  * is left to the chain.  Every wave streams a run of bf_maps_cpw() chunks,
@@ -1234,10 +1234,10 @@ __device__ int64_t bf_walk(const char* rowp, int c0, int nch, State& st, float t
 }
 
 /* One workgroup per row: LSum by chaining the chunk maps left to right from
- * the exact state after chunk 0 (Tensors.pas:657-663), 1/LSum and the p
- * table (Tensors.pas:666-672), the argmax, the draw's predictions (the last
- * chunk it needs, the predicted binade of its running sum entering every
- * chunk, the chunks to stage), and the draw through chunk 0. */
+ * the exact state after chunk 0 (Tensors.pas:657-663), 1/LSum
+ * (Tensors.pas:668), the argmax, and the draw's predictions (the last chunk
+ * it needs, the predicted binade of its running sum entering every chunk,
+ * the chunks to stage). */
 __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
 {
     extern __shared__ __align__(16) char dsm[];
