@@ -602,6 +602,7 @@ __device__ void bf_draw0(const FullArgs& a, int row, const FullRow& r, float* hb
     int hit = -1, rounds = 0;
     State st = seq_walk(hbuf, kSeqLanes * kFullPer, r.thr, &hit);
     if (hit < 0) {
+        /* the lane's terms again from LDS, as in bf_head */
         const float4* hr = reinterpret_cast<const float4*>(hbuf + lane * kFullPer);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
