@@ -776,6 +776,35 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     uint32_t kv = 0u;
     float vv = 0.0f;
     int pos = 0;
+    /* p's storage holds the rank counters until the tail writes p */
+    uint32_t* rk = reinterpret_cast<uint32_t*>(sh.prob);
+    if (!ordered) {
+        /* rank by count over the whole workgroup: thread (i, s) counts the
+         * survivors of slice s with an index below survivor i's into i's
+         * counter */
+        for (int i = tid; i < nsurv; i += BLOCK) rk[i] = 0u;
+        __syncthreads();
+        const int npad = (nsurv + 63) & ~63; /* <= KCAP <= BLOCK */
+        const int SL = BLOCK / npad;
+        const int i = tid % npad, sl = tid / npad;
+        if (sl < SL && i < nsurv) {
+            const int per = (nsurv + SL - 1) / SL;
+            const int j0 = sl * per, j1 = j0 + per < nsurv ? j0 + per : nsurv;
+            const uint32_t mi = cand_idx_of(sh.surv[i]);
+            uint32_t c = 0u;
+            int j = j0;
+            for (; j + 8 <= j1; j += 8) {
+                uint32_t xx[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) xx[t] = cand_idx_of(sh.surv[j + t]);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) c += xx[t] < mi ? 1u : 0u;
+            }
+            for (; j < j1; ++j) c += cand_idx_of(sh.surv[j]) < mi ? 1u : 0u;
+            if (c != 0u) atomicAdd(&rk[i], c);
+        }
+        __syncthreads();
+    }
     if (tid < nsurv) {
         uint64_t my;
         if (ordered) {
@@ -783,16 +812,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
             my = sh.sorted[tid];
         } else {
             my = sh.surv[tid];
-            const uint32_t mi = cand_idx_of(my);
-            int j = 0;
-            for (; j + 8 <= nsurv; j += 8) {
-                uint32_t xx[8];
-#pragma unroll
-                for (int t = 0; t < 8; ++t) xx[t] = cand_idx_of(sh.surv[j + t]);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) pos += xx[t] < mi;
-            }
-            for (; j < nsurv; ++j) pos += cand_idx_of(sh.surv[j]) < mi;
+            pos = (int)rk[tid];
             sh.sorted[pos] = my;
         }
         const float x = key2f(cand_key_of(my));                         /* :2774 */
