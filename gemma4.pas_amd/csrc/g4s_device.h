@@ -178,7 +178,12 @@ __device__ __forceinline__ void st_sys(uint32_t* p, uint32_t v)
 __device__ __forceinline__ void publish_done(uint32_t* done, int row, uint32_t seq)
 {
     if (!done) return;
+    /* the compiler may not move memory operations across the wait: the
+     * signal fences are compiler-only barriers (no cache maintenance), the
+     * wait itself is the hardware ordering */
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if ((threadIdx.x & 63) == 0)
         __hip_atomic_store(done + row, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }

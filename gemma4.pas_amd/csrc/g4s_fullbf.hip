@@ -41,6 +41,8 @@
  */
 #include "g4s_fullcore.h"
 
+#include <mutex>
+
 namespace g4s {
 
 namespace {
@@ -1446,18 +1448,21 @@ hipError_t fb_launch(const FullArgs& a0, hipStream_t s)
     size_t off[7];
     const size_t lds = bf_chain_lds(a.nch, off);
     /* the chains' dynamic LDS exceeds the default 64 KiB: raise the limit once
-     * to what the largest supported vocabulary needs */
-    static bool raised = false;
-    if (!raised) {
-        const int most = (int)bf_chain_lds(kBfMaxChunks, off);
+     * per process to what the largest supported vocabulary needs (handles on
+     * several threads may make their first call together) */
+    static std::once_flag raised;
+    static hipError_t raise_err = hipSuccess;
+    std::call_once(raised, [] {
+        size_t o[7];
+        const int most = (int)bf_chain_lds(kBfMaxChunks, o);
         hipError_t e = hipFuncSetAttribute((const void*)fb_lsum_chain_kernel,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, most);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)fb_cdf_chain_kernel,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, most);
-        if (e != hipSuccess) return e;
-        raised = true;
-    }
+        raise_err = e;
+    });
+    if (raise_err != hipSuccess) return raise_err;
     const unsigned B = (unsigned)a.batch;
     const dim3 gmax((unsigned)((a.nch + 4 * a.cpw - 1) / (4 * a.cpw)), B);
     const dim3 grow((unsigned)(kRowWG + 1), B);

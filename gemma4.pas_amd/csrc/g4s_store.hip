@@ -794,6 +794,10 @@ G4S_API int g4s_store_upload_q4_0(g4s_store* st, const char* name, int32_t layou
     if (e == hipSuccess) {
         what = "stream synchronize";
         e = hipStreamSynchronize(s);
+    } else {
+        /* copies and repacks enqueued before the failure may still read the
+         * staging buffers freed below */
+        (void)hipStreamSynchronize(s);
     }
     for (int i = 0; i < 2; ++i) {
         if (ev[i]) (void)hipEventDestroy(ev[i]);

@@ -221,12 +221,17 @@ type
     procedure Close();
 
     // DoSample on one GPU-resident logits row: u is the engine's Random, as
-    // at Model.pas:2726,2813.  False (and ATokenId = -1) on failure.
+    // at Model.pas:2726,2813, drawn only when AParams^.Temperature > 0 (a
+    // greedy row consumes no Random, as in the reference).  False (and
+    // ATokenId = -1) on failure.
     function Sample(const ADevLogits: Pointer; const ADType: Integer;
       const AParams: PG4SParams; out ATokenId: Integer): Boolean;
 
     // ABatch rows at ADevLogits + i*ARowStride elements; AParams, AU and
-    // AIds point at ABatch host entries each
+    // AIds point at ABatch host entries each.  AU[i] is read only for rows
+    // with Temperature > 0: a caller reproducing the reference fills it
+    // with Random for those rows alone, in row order, and leaves the greedy
+    // rows' entries unread (any value in [0, 1)).
     function SampleBatch(const ADevLogits: Pointer; const ADType: Integer;
       const ARowStride: Int64; const ABatch: Integer; const AParams: PG4SParams;
       const AU: PDouble; const AIds: PInteger): Boolean;
@@ -332,7 +337,13 @@ var
   LStatus: Integer;
 begin
   ATokenId := -1;
-  LU := Random;
+  // System.Random is drawn only when the row draws, as DoSample does on
+  // both of its paths (Model.pas:2723-2726, 2811-2813): a greedy call
+  // (Temperature <= 0) leaves RandSeed where the reference leaves it.
+  if AParams^.Temperature > 0.0 then
+    LU := Random
+  else
+    LU := 0.0;
   LId := -1;
   LStatus := g4s_sample(FHandle, ADevLogits, ADType, FVocab, 1, AParams, @LU, @LId);
   if LStatus <> G4S_OK then

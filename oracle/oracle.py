@@ -166,6 +166,10 @@ def f16_from_f32(x):
     return load().orc_f16_from_f32(float(x))
 
 
+def f32_to_bf16(x):
+    return load().orc_f32_to_bf16(float(x))
+
+
 def dequant_q4_block(block18):
     b = np.ascontiguousarray(block18, np.uint8)
     out = np.empty(32, np.float32)

@@ -329,3 +329,60 @@ def test_matvec_q4_hand_values(orc):
     h = np.zeros(cols, F32)
     h[:4] = [2.0 ** 24, 1.0, 1.0, 2.0 ** 24]
     assert orc.matvec_q4(w, h, 2, cols)[1] == F32(0.0)
+
+
+def _f32_from_bits(b):
+    return np.array([b], np.uint32).view(F32)[0]
+
+
+def test_bf16_from_single_truncates(orc):
+    """TBFloat16.FromSingle (Types.pas:426-434) truncates.  Values chosen so
+    that round-to-nearest(-even) gives another code: 0x3F80FFFF lies just
+    below 0x3F81 and 0x3F818000 is a tie whose even neighbour is 0x3F82."""
+    for bits, want in ((0x3F80FFFF, 0x3F80), (0xBF80FFFF, 0xBF80), (0x3F818000, 0x3F81),
+                       (0x7F7FFFFF, 0x7F7F), (0x00000001, 0x0000), (0x80000000, 0x8000)):
+        assert orc.f32_to_bf16(_f32_from_bits(bits)) == want, hex(bits)
+    # every non-NaN bf16 value converts back to its own code
+    codes = np.arange(65536, dtype=np.uint32)
+    ok = (((codes >> 7) & 0xFF) != 0xFF) | ((codes & 0x7F) == 0)
+    for c in codes[ok][::7]:
+        assert orc.f32_to_bf16(orc.bf16_to_f32(int(c))) == c
+    # truncation toward zero: the code's value has x's sign, is no larger in
+    # magnitude than x, and the next code up in magnitude is larger than x
+    rng = np.random.default_rng(31)
+    xs = rng.normal(0, 1, 2000).astype(F32) * F32(2.0) ** rng.integers(-60, 60, 2000).astype(F32)
+    for x in xs:
+        b = orc.f32_to_bf16(x)
+        w = orc.bf16_to_f32(b)
+        up = orc.bf16_to_f32(b + 1)
+        assert np.signbit(w) == np.signbit(x) and abs(w) <= abs(x) < abs(up), (x, hex(b))
+
+
+def test_f16_from_single_truncates(orc):
+    """TFloat16.FromSingle (Types.pas:483-501): truncation, results below the
+    smallest normal flushed to a signed zero, overflow to infinity.  Each
+    value below rounds to a different code under round-to-nearest."""
+    h = F32(2.0) ** -11  # half a unit of f16 at 1.0
+    for x, want in ((F32(1) + h + F32(2.0) ** -23, 0x3C00),  # just above a half-unit
+                    (F32(1) + 2 * h - F32(2.0) ** -23, 0x3C00),  # just below the next code
+                    (F32(-1) - h - F32(2.0) ** -23, 0xBC00),
+                    (F32(65535.0), 0x7BFF),  # round-to-nearest would overflow
+                    (F32(65536.0), 0x7C00),
+                    (F32(2.0) ** -14, 0x0400),  # smallest normal
+                    (F32(2.0) ** -14 * F32(1 - 2.0 ** -24), 0x0000),  # just below: flushed
+                    (-F32(2.0) ** -15, 0x8000)):
+        assert orc.f16_from_f32(x) == want, (x, want)
+    # every normal f16 code converts back to itself (the decode is pinned to
+    # IEEE half for normals above)
+    for c in list(range(0x0400, 0x7C00, 13)) + list(range(0x8400, 0xFC00, 29)):
+        assert orc.f16_from_f32(orc.f16_to_f32(c)) == c, hex(c)
+    # truncation toward zero against numpy's IEEE half decode
+    rng = np.random.default_rng(32)
+    xs = (rng.uniform(-1, 1, 2000) * 2.0 ** rng.integers(-13, 15, 2000)).astype(F32)
+    for x in xs:
+        c = orc.f16_from_f32(x)
+        if (c & 0x7C00) == 0:
+            continue
+        dec = np.array([c], np.uint16).view(np.float16).astype(F32)[0]
+        nxt = np.array([c + 1], np.uint16).view(np.float16).astype(F32)[0]
+        assert np.signbit(dec) == np.signbit(x) and abs(dec) <= abs(x) < abs(nxt), (x, hex(c))

@@ -212,3 +212,94 @@ def test_call_every_export_with_the_declared_shapes(lib):
     if rc == 0:
         assert f["g4s_destroy"](h) == 0
     assert f["g4s_destroy"](None) == 0
+
+
+# --------------------------------------------------------------------------
+# TGpuSampler.Sample and the engine-side integration (model_integration.py)
+# --------------------------------------------------------------------------
+
+def _method_body(src, header_regex):
+    """Text between `begin` and the matching final `end;` of one method."""
+    m = re.search(header_regex + r".*?\bbegin\b(.*?)\nend;", src, re.S)
+    assert m, header_regex
+    return m.group(1)
+
+
+def test_sample_draws_random_only_when_the_row_draws():
+    """DoSample calls Random only when Temperature > 0 (Model.pas:2723-2726 on
+    the full path, :2811-2813 on the top-k path): the shim that takes its
+    place must consume the RTL stream the same way, or every later T > 0
+    token of the process is drawn from a shifted stream."""
+    src = _strip_pascal_comments(open(UNIT).read())
+    body = _method_body(src, r"function TGpuSampler\.Sample\(")
+    flat = re.sub(r"\s+", " ", body)
+    assert len(re.findall(r"\bRandom\b", flat)) == 1, flat
+    assert re.search(r"if AParams\^\.Temperature > 0\.0 then LU := Random else LU := 0\.0;",
+                     flat), flat
+    # the only use of u is the library call, after the guard
+    assert flat.index("Random") < flat.index("g4s_sample(")
+
+
+def _integration():
+    import importlib.util
+    p = os.path.join(ROOT, "gemma4.pas_amd", "pascal", "model_integration.py")
+    spec = importlib.util.spec_from_file_location("model_integration", p)
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    return m
+
+
+def test_integration_do_sample_calls_only_the_gpu_sampler():
+    mi = _integration()
+    body = mi.DO_SAMPLE.split("procedure TModel.SetDeviceLogits")[0]
+    code = _strip_pascal_comments(body)
+    calls = re.findall(r"\b([A-Za-z_][\w\.]*)\s*\(", code)
+    # GetErrors().Add reports missing logits; PG4SParams is a type cast
+    assert [c for c in calls if c not in ("TModel.DoSample", "GetErrors", "Add",
+                                          "PG4SParams")] == ["FSampler.Sample"], calls
+    for banned in ("Random", "FLogits", "DoSelectTopKIndices", "DoSampleTopP", "CpuSoftmaxF32",
+                   "CpuLogitSoftcap", "Exp", "Tanh"):
+        assert not re.search(r"\b%s\b" % banned, code), banned
+
+
+REF_MODEL = "/root/reference/src/Gemma4.Model.pas"
+
+
+@pytest.mark.skipif(not os.path.exists(REF_MODEL), reason="the engine's Model.pas is not here")
+def test_integration_applies_to_the_engine_model():
+    mi = _integration()
+    src = open(REF_MODEL, encoding="utf-8-sig").read().replace("\r\n", "\n")
+    out = mi.apply(src)
+    code = _strip_pascal_comments(out)
+    # the logits never come back to the host
+    assert "DownloadFromBuffer(FGpuLogits" not in code
+    assert "Exit(Copy(FLogits))" not in code
+    # DoSample: one call into the GPU sampler, no CPU sampling left in it
+    body = _method_body(code, r"function TModel\.DoSample\(const AParams: TSamplingParams\)")
+    assert "FSampler.Sample(FDevLogits, G4S_DTYPE_F32, PG4SParams(@AParams), Result)" in body
+    for banned in ("Random", "FLogits", "DoSelectTopKIndices", "DoSampleTopP", "Exp("):
+        assert banned not in body, banned
+    # Generate: a failed sample ends the loop before its id is added
+    gen = _method_body(code, r"function TModel\.Generate\(")
+    flat = re.sub(r"\s+", " ", gen)
+    assert flat.count("LResult.Add(LTokenId);") == 1
+    assert "while LI < AMaxTokens do begin if LTokenId < 0 then Break; LResult.Add(LTokenId);" \
+        in flat, flat[:400]
+    # the sampler lives with the GPU buffers
+    alloc = _method_body(code, r"function TModel\.DoAllocateResidentGpuBuffers\(\)")
+    assert re.search(r"FSampler := TGpuSampler\.Create\(\);\s*FSampler\.SetErrors\(GetErrors\(\)\);"
+                     r"\s*if not FSampler\.Open\(FConfig\.VocabSize, 1, "
+                     r"FConfig\.FinalLogitSoftcapping\) then\s*Exit;", alloc)
+    free = _method_body(code, r"procedure TModel\.DoFreeGpuBuffers\(\)")
+    assert re.match(r"\s*FreeAndNil\(FSampler\);", free)
+    assert re.search(r"\bGemma4\.Compute,\s*Gemma4\.Sampler;", code)
+    assert re.search(r"FSampler: TGpuSampler;\s*FDevLogits: Pointer;", code)
+    # every anchor is consumed: a second application finds nothing to edit
+    with pytest.raises(mi.IntegrationError):
+        mi.apply(out)
+
+
+def test_integration_refuses_a_file_it_does_not_know():
+    mi = _integration()
+    with pytest.raises(mi.IntegrationError, match="uses"):
+        mi.apply("unit Gemma4.Model;\ninterface\nimplementation\nend.\n")
