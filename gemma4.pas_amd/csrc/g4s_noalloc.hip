@@ -12,9 +12,10 @@
  * is handed to kernels.  Nothing here calls hipMalloc, hipFree or an
  * allocating library routine.
  *
- * What must start at zero: the election tickets.  The kernel returns each
- * ticket to zero in the workgroup it elects, so they are zero between
- * launches; they are also cleared once, with a fill kernel on the caller's
+ * What must start at zero: the election tickets (the one-word tickets of
+ * the chunked launch and the counters of the decode-sized launch).  The
+ * kernels return each to zero in the workgroup it elects, so they are zero
+ * between launches; they are also cleared once, with a fill kernel on the caller's
  * stream, at the first call on each device.  Calls that overlap on one GPU
  * share the array and race: a caller runs one call at a time per device
  * (e.g. one stream).
@@ -39,16 +40,20 @@ constexpr size_t kCandOff = 256;
 constexpr size_t kMergeOff = kCandOff + (size_t)kRows * kCandRow * sizeof(uint64_t);
 constexpr size_t kRecsOff = kMergeOff + (size_t)kRows * kCandRow * sizeof(uint64_t);
 constexpr size_t kWbOff = kRecsOff + (size_t)kRows * kMaxSplits * sizeof(ChunkRec);
-constexpr size_t kBytes = kWbOff + (size_t)kRows * kWaveBounds * sizeof(uint32_t);
+constexpr size_t kDecTicketsOff = kWbOff + (size_t)kRows * kWaveBounds * sizeof(uint32_t);
+constexpr int kDecWords = kDecMaxRows * kDecTicketWords;
+constexpr size_t kBytes = kDecTicketsOff + (size_t)kDecWords * sizeof(uint32_t);
 static_assert(kRows * sizeof(uint32_t) <= kCandOff, "tickets before the candidates");
+static_assert(kDecTicketsOff % 256 == 0, "aligned sections");
 static_assert(kBytes == G4S_NOALLOC_SCRATCH_BYTES, "header states the scratch size");
 static_assert(kRecsOff % 256 == 0 && kWbOff % 256 == 0, "aligned sections");
 
 static __device__ __align__(256) uint8_t scratch[kBytes];
 
-__global__ void noalloc_clear_tickets(uint32_t* tickets)
+__global__ void noalloc_clear_tickets(uint32_t* tickets, uint32_t* dec_tickets)
 {
     if (threadIdx.x < (unsigned)kRows) tickets[threadIdx.x] = 0u;
+    for (int i = threadIdx.x; i < kDecWords; i += blockDim.x) dec_tickets[i] = 0u;
 }
 
 constexpr int kMaxDevices = 64;
@@ -146,8 +151,9 @@ G4S_API int g4s_sample_topk_noalloc(const void* d_logits, int32_t dtype, int32_t
     uint8_t* base = ds.ptr;
     if (first) {
         /* a kernel, not hipMemsetAsync: the call may be under graph capture */
-        hipLaunchKernelGGL(noalloc_clear_tickets, dim3(1), dim3(64), 0, stream,
-                           reinterpret_cast<uint32_t*>(base + kTicketsOff));
+        hipLaunchKernelGGL(noalloc_clear_tickets, dim3(1), dim3(256), 0, stream,
+                           reinterpret_cast<uint32_t*>(base + kTicketsOff),
+                           reinterpret_cast<uint32_t*>(base + kDecTicketsOff));
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess)
             return set_null_handle_error(G4S_ERR_HIP, "scratch set-up: %s", hipGetErrorString(e));
@@ -171,6 +177,7 @@ G4S_API int g4s_sample_topk_noalloc(const void* d_logits, int32_t dtype, int32_t
     a.recs = reinterpret_cast<ChunkRec*>(base + kRecsOff);
     a.wbounds = reinterpret_cast<uint32_t*>(base + kWbOff);
     a.tickets = reinterpret_cast<uint32_t*>(base + kTicketsOff);
+    a.dec_tickets = reinterpret_cast<uint32_t*>(base + kDecTicketsOff);
     a.ids = d_ids;
     a.done = nullptr;
     a.seq = 0;

@@ -62,6 +62,7 @@ struct g4s_sampler {
     g4s::ChunkRec* recs = nullptr;
     uint32_t* wbounds = nullptr;
     uint32_t* tickets = nullptr;
+    uint32_t* dec_tickets = nullptr; /* [min(max_batch, kDecMaxRows)][kDecTicketWords] */
     uint32_t* gmax = nullptr;     /* [max_batch][ceil(vocab/64)] LM-head group maxima */
     /* full path workspace */
     g4s::FullWorkspace full{};
@@ -110,6 +111,7 @@ void release(g4s_sampler* s)
     f(s->recs);
     f(s->wbounds);
     f(s->tickets);
+    f(s->dec_tickets);
     f(s->gmax);
     g4s::full_free(s->full);
     f(s->d_params);
@@ -178,6 +180,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         a.recs = s->recs;
         a.wbounds = s->wbounds;
         a.tickets = s->tickets;
+        a.dec_tickets = s->dec_tickets;
         a.ids = d_ids;
         a.done = done;
         a.seq = seq;
@@ -290,6 +293,8 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
     dm((void**)&s->recs, mb * g4s::kMaxSplits * sizeof(g4s::ChunkRec));
     dm((void**)&s->wbounds, mb * g4s::kWaveBounds * sizeof(uint32_t));
     dm((void**)&s->tickets, mb * sizeof(uint32_t));
+    const size_t dec_rows = mb < (size_t)g4s::kDecMaxRows ? mb : (size_t)g4s::kDecMaxRows;
+    dm((void**)&s->dec_tickets, dec_rows * g4s::kDecTicketWords * sizeof(uint32_t));
     dm((void**)&s->gmax, mb * (size_t)((vocab + 63) / 64) * sizeof(uint32_t));
     dm((void**)&s->d_params, mb * sizeof(g4s_params));
     dm((void**)&s->d_u, mb * sizeof(double));
@@ -311,6 +316,9 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
      * start below the first sequence value */
     std::memset(s->h_done, 0, mb * sizeof(uint32_t));
     hipError_t e = hipMemsetAsync(s->tickets, 0, mb * sizeof(uint32_t), s->stream);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(s->dec_tickets, 0, dec_rows * g4s::kDecTicketWords * sizeof(uint32_t),
+                           s->stream);
     if (e == hipSuccess) e = g4s::full_init(s->full, max_batch, softcap, s->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) {

@@ -10,6 +10,21 @@ namespace g4s {
 
 constexpr int kWaveBounds = 512; /* per-wave bounds kept per row (splits * waves) */
 
+/* The decode-sized launch (g4s_decode.hip): batches of up to kDecMaxRows rows
+ * whose TopK bound is at most kDecMaxK, on vocabularies of at most
+ * kDecMaxChunks 16-byte-per-thread workgroup chunks (262144 binary32 logits,
+ * 524288 bf16). */
+constexpr int kDecMaxRows = 8;
+constexpr int kDecMaxK = 64;
+constexpr int kDecBlock = 256;                 /* threads per workgroup */
+constexpr int kDecMaxChunks = 256;             /* workgroups per row */
+constexpr int kDecListLen = 4;                 /* entries per wave list */
+constexpr int kDecCounterStride = 32;          /* words between election counters (128 B) */
+constexpr int kDecGroups = 16;                 /* first-level election counters per row */
+constexpr int kDecTicketWords = kDecCounterStride * (kDecGroups + 1);
+constexpr int kDecSlotsPerRow = kDecMaxChunks * (kDecBlock / 64) * kDecListLen;
+static_assert(kDecSlotsPerRow <= 16384, "the wave lists fit a row's candidate slots");
+
 /* Per-chunk record written by phase 1 (16 bytes). */
 struct ChunkRec {
     uint32_t count;  /* candidates emitted */
@@ -53,6 +68,8 @@ struct TopkArgs {
     uint32_t* done;    /* [batch] host-pinned completion words, or NULL */
     uint32_t seq;      /* value written to done[row] once the row's outputs are visible */
     g4s_outputs out;
+    uint32_t* dec_tickets; /* [batch][kDecTicketWords] election counters of the decode
+                              launch, zero between launches; NULL: no decode launch */
 };
 
 struct TopkConfig {
@@ -67,6 +84,13 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound);
  * that a later chunk is waiting for. */
 hipError_t topk_launch(const TopkConfig& c, const TopkArgs& a, int dtype, hipStream_t s,
                        int32_t ncu = 0);
+
+/* Whether topk_launch takes the decode-sized launch for these rows. */
+bool decode_eligible(const TopkArgs& a, int dtype);
+/* The decode-sized launch (g4s_decode.hip): per-wave candidate lists written
+ * by every workgroup, a two-level election, and the merge + tail in the last
+ * workgroup of each row.  The lists use the rows' candidate slots (a.cand). */
+hipError_t decode_launch(const TopkArgs& a, int dtype, hipStream_t s);
 
 /* Rows whose f32 logits come from the tiled LM head with its 64-logit group
  * maxima (gmax [batch][ngroups], candidate keys): candidates from the groups

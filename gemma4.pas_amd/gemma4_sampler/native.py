@@ -174,7 +174,7 @@ def load():
 
 
 NOALLOC_MAX_ROWS = 32
-NOALLOC_SCRATCH_BYTES = 8585472
+NOALLOC_SCRATCH_BYTES = 8602880
 
 
 def sample_topk_noalloc(d_logits, batch, d_params, d_u, k_bound, d_ids, vocab,

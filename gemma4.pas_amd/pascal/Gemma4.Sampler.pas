@@ -85,7 +85,7 @@ const
 
   // g4s_sample_topk_noalloc: rows per call and bytes of its device array
   G4S_NOALLOC_MAX_ROWS = 32;
-  G4S_NOALLOC_SCRATCH_BYTES = 8585472;
+  G4S_NOALLOC_SCRATCH_BYTES = 8602880;
 
 type
   { PG4SSampler }

@@ -166,7 +166,7 @@ int g4s_sample_async(g4s_sampler* sampler, const void* d_logits, int32_t dtype,
 /* Rows and bytes of the device scratch array behind g4s_sample_topk_noalloc
  * (held by every GPU the library runs on until the process ends). */
 #define G4S_NOALLOC_MAX_ROWS 32
-#define G4S_NOALLOC_SCRATCH_BYTES 8585472
+#define G4S_NOALLOC_SCRATCH_BYTES 8602880
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
