@@ -75,6 +75,27 @@ struct g4s_sampler {
     uint32_t* h_flags = nullptr;    /* pinned */
     uint32_t* h_done = nullptr;     /* pinned, coherent: per-row completion words */
     uint32_t seq = 0;               /* last completion value handed to a launch */
+
+    /* g4s_sample_graph: captured stream-ordered samples, one per argument set */
+    struct GraphEntry {
+        bool used = false;
+        uint64_t last = 0; /* least recently launched entry is replaced first */
+        const void* logits = nullptr;
+        int32_t dtype = 0;
+        int64_t row_stride = 0;
+        int32_t batch = 0;
+        const g4s_params* params = nullptr;
+        const double* u = nullptr;
+        int32_t k_bound = 0;
+        int32_t full_rows = 0;
+        int32_t* ids = nullptr;
+        g4s_outputs out{};
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+    };
+    static constexpr int kGraphs = 8;
+    GraphEntry graphs[kGraphs];
+    uint64_t graph_clock = 0;
 };
 
 namespace {
@@ -121,6 +142,11 @@ void release(g4s_sampler* s)
     fh(s->h_ids);
     fh(s->h_flags);
     fh(s->h_done);
+    for (auto& g : s->graphs) {
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        if (g.graph) (void)hipGraphDestroy(g.graph);
+        g = g4s_sampler::GraphEntry{};
+    }
 }
 
 bool is_topk_row(const g4s_params& p, int32_t vocab) { return p.top_k >= 1 && p.top_k < vocab; }
@@ -461,13 +487,12 @@ G4S_API int g4s_sample(g4s_sampler* s, const void* d_logits, int32_t dtype, int6
     return g4s_sample_ex(s, d_logits, dtype, row_stride, batch, params, u, ids, nullptr);
 }
 
-G4S_API int g4s_sample_async(g4s_sampler* s, const void* d_logits, int32_t dtype,
-                             int64_t row_stride, int32_t batch, const g4s_params* d_params,
-                             const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,
-                             const g4s_outputs* outputs)
+namespace {
+
+int check_async(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
+                int32_t batch, const g4s_params* d_params, const double* d_u, int32_t k_bound,
+                int32_t full_rows, int32_t* d_ids)
 {
-    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
-    s->err.clear();
     int rc = check_logits(s, d_logits, dtype, row_stride, batch);
     if (rc) return rc;
     if (!d_params || !d_u || !d_ids)
@@ -476,9 +501,112 @@ G4S_API int g4s_sample_async(g4s_sampler* s, const void* d_logits, int32_t dtype
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "k_bound %d outside [0, %d)", k_bound, s->vocab);
     if (k_bound == 0 && !full_rows)
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "k_bound == 0 and full_rows == 0: nothing to do");
+    return G4S_OK;
+}
+
+int enqueue_async(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
+                  int32_t batch, const g4s_params* d_params, const double* d_u, int32_t k_bound,
+                  int32_t full_rows, int32_t* d_ids, const g4s_outputs* outputs)
+{
     const bool wide = k_bound > g4s::kMaxTopK;
     return enqueue(s, d_logits, dtype, row_stride, batch, d_params, d_u, nullptr, 0.0,
                    wide ? g4s::kMaxTopK : k_bound, full_rows != 0, wide, d_ids, outputs);
+}
+
+bool same_outputs(const g4s_outputs& a, const g4s_outputs& b)
+{
+    return a.count == b.count && a.indices == b.indices && a.probs == b.probs &&
+           a.capacity == b.capacity && a.argmax == b.argmax && a.lsum == b.lsum &&
+           a.flags == b.flags;
+}
+
+}  // namespace
+
+G4S_API int g4s_sample_async(g4s_sampler* s, const void* d_logits, int32_t dtype,
+                             int64_t row_stride, int32_t batch, const g4s_params* d_params,
+                             const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,
+                             const g4s_outputs* outputs)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    const int rc = check_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound,
+                               full_rows, d_ids);
+    if (rc) return rc;
+    return enqueue_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound, full_rows,
+                         d_ids, outputs);
+}
+
+G4S_API int g4s_sample_graph(g4s_sampler* s, const void* d_logits, int32_t dtype,
+                             int64_t row_stride, int32_t batch, const g4s_params* d_params,
+                             const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,
+                             const g4s_outputs* outputs)
+{
+    if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
+    s->err.clear();
+    int rc = check_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound,
+                         full_rows, d_ids);
+    if (rc) return rc;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s->stream, &cs);
+    if (e != hipSuccess) return hip_fail(s, e, "hipStreamIsCapturing");
+    if (cs == hipStreamCaptureStatusActive) /* the caller's own capture records the launches */
+        return enqueue_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound,
+                             full_rows, d_ids, outputs);
+    if (!s->stream)
+        return fail(s, G4S_ERR_UNSUPPORTED,
+                    "g4s_sample_graph needs a handle created on a stream (not the null stream)");
+    g4s_outputs out{};
+    if (outputs) out = *outputs;
+    g4s_sampler::GraphEntry* hit = nullptr;
+    g4s_sampler::GraphEntry* victim = &s->graphs[0];
+    for (auto& g : s->graphs) {
+        if (g.used && g.logits == d_logits && g.dtype == dtype && g.row_stride == row_stride &&
+            g.batch == batch && g.params == d_params && g.u == d_u && g.k_bound == k_bound &&
+            g.full_rows == full_rows && g.ids == d_ids && same_outputs(g.out, out)) {
+            hit = &g;
+            break;
+        }
+        if (!g.used || (victim->used && g.last < victim->last)) victim = &g;
+    }
+    if (!hit) {
+        if (victim->exec) (void)hipGraphExecDestroy(victim->exec);
+        if (victim->graph) (void)hipGraphDestroy(victim->graph);
+        *victim = g4s_sampler::GraphEntry{};
+        e = hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return hip_fail(s, e, "hipStreamBeginCapture");
+        rc = enqueue_async(s, d_logits, dtype, row_stride, batch, d_params, d_u, k_bound,
+                           full_rows, d_ids, outputs);
+        hipGraph_t g = nullptr;
+        e = hipStreamEndCapture(s->stream, &g);
+        if (rc || e != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc ? rc : hip_fail(s, e, "hipStreamEndCapture");
+        }
+        hipGraphExec_t x = nullptr;
+        e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            return hip_fail(s, e, "hipGraphInstantiate");
+        }
+        victim->used = true;
+        victim->logits = d_logits;
+        victim->dtype = dtype;
+        victim->row_stride = row_stride;
+        victim->batch = batch;
+        victim->params = d_params;
+        victim->u = d_u;
+        victim->k_bound = k_bound;
+        victim->full_rows = full_rows;
+        victim->ids = d_ids;
+        victim->out = out;
+        victim->graph = g;
+        victim->exec = x;
+        hit = victim;
+    }
+    hit->last = ++s->graph_clock;
+    e = hipGraphLaunch(hit->exec, s->stream);
+    if (e != hipSuccess) return hip_fail(s, e, "hipGraphLaunch");
+    return G4S_OK;
 }
 
 G4S_API int g4s_lmhead_q4_0(g4s_sampler* s, const void* d_weights, int32_t rows, int32_t cols,

@@ -54,6 +54,7 @@ FLAG_ERROR = 0x80000000
 
 EXPORTS = ("g4s_version", "g4s_params_set_defaults", "g4s_max_top_k", "g4s_create",
            "g4s_destroy", "g4s_last_error", "g4s_sample", "g4s_sample_ex", "g4s_sample_async",
+           "g4s_sample_graph",
            "g4s_sample_topk_noalloc", "g4s_lmhead_q4_0", "g4s_lmhead_q4_0_tiled",
            "g4s_lmhead_sample_q4_0", "g4s_store_open", "g4s_store_close", "g4s_store_last_error",
            "g4s_store_tensor_count", "g4s_store_tensor_info", "g4s_store_find_tensor",
@@ -129,6 +130,7 @@ def load():
                                        ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                        ctypes.c_void_p, ctypes.c_void_p]
+        L.g4s_sample_graph.argtypes = L.g4s_sample_async.argtypes
         L.g4s_lmhead_q4_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
                                       ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                       ctypes.c_void_p, ctypes.c_int64]
@@ -285,6 +287,16 @@ class Sampler:
         L = load()
         stride = self.vocab if row_stride is None else int(row_stride)
         rc = L.g4s_sample_async(self.h, _ptr(d_logits), int(dtype), stride, int(batch),
+                                _ptr(d_params), _ptr(d_u), int(k_bound), int(full_rows),
+                                _ptr(d_ids), ctypes.byref(outputs) if outputs is not None else None)
+        self._check(rc)
+
+    def sample_graph(self, d_logits, batch, d_params, d_u, k_bound, full_rows, d_ids,
+                     dtype=DTYPE_F32, row_stride=None, outputs=None):
+        """g4s_sample_graph: sample_async replayed from a graph this handle owns."""
+        L = load()
+        stride = self.vocab if row_stride is None else int(row_stride)
+        rc = L.g4s_sample_graph(self.h, _ptr(d_logits), int(dtype), stride, int(batch),
                                 _ptr(d_params), _ptr(d_u), int(k_bound), int(full_rows),
                                 _ptr(d_ids), ctypes.byref(outputs) if outputs is not None else None)
         self._check(rc)

@@ -84,9 +84,10 @@ G4H_API int g4h_null_roundtrip(void* stream, int32_t n, int32_t mode, double* us
  * graph leg of the decode stream measures the sampler (g4h_graph_decode): a
  * graph holding one launch of a null kernel, captured once, launched `n`
  * times from an idle stream, each launch between two events; gpu_us[i] =
- * event time of launch i.
+ * event time of launch i, call_us[i] = host time spent inside the
+ * hipGraphLaunch call itself.
  */
-G4H_API int g4h_graph_floor(void* stream, int32_t n, float* gpu_us)
+G4H_API int g4h_graph_floor(void* stream, int32_t n, float* gpu_us, double* call_us)
 {
     hipStream_t st = (hipStream_t)stream;
     hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -104,7 +105,9 @@ G4H_API int g4h_graph_floor(void* stream, int32_t n, float* gpu_us)
     for (int32_t i = 0; rc == 0 && i < n; ++i) {
         if (hipStreamSynchronize(st) != hipSuccess) rc = -105;
         (void)hipEventRecord(e0, st);
+        const double t0 = now_us();
         if (rc == 0 && hipGraphLaunch(gx, st) != hipSuccess) rc = -106;
+        call_us[i] = now_us() - t0;
         (void)hipEventRecord(e1, st);
         if (rc == 0 && hipEventSynchronize(e1) != hipSuccess) rc = -107;
         float ms = 0.0f;
@@ -313,19 +316,21 @@ G4H_API int g4h_batch_throughput(g4s_sampler* s, void* stream, const void* d_log
 }
 
 /*
- * The decode stream launched from a hipGraph, as a device-resident decode
- * loop runs it: g4s_sample_async for one row is captured once, on fixed
- * device buffers (logits, parameters, uniform, id; the id stays on the
- * device for the next step).  For each row i of d_rows (fp32, row i at
+ * The decode stream launched from the sampler's own hipGraph
+ * (g4s_sample_graph), as a device-resident decode loop runs it: one row on
+ * fixed device buffers (logits, parameters, uniform, id; the id stays on the
+ * device for the next step), so every call after the first replays the graph
+ * the handle captured.  For each row i of d_rows (fp32, row i at
  * d_rows + i*vocab, parameters and uniforms in device arrays) the row is
- * copied into those buffers untimed, then the graph is launched:
- * gpu_us[i] = event time around the launch on the stream, host_us[i] =
- * launch until the host sees the closing event complete, ids[i] = the id
- * (read back untimed).
+ * copied into those buffers untimed, then g4s_sample_graph is called:
+ * gpu_us[i] = event time around the call on the stream, host_us[i] = call
+ * until the host sees the closing event complete, call_us[i] = host time
+ * inside g4s_sample_graph, ids[i] = the id (read back untimed).
  */
 G4H_API int g4h_graph_decode(g4s_sampler* s, void* stream, const float* d_rows, int32_t vocab,
                              int32_t nrows, const g4s_params* d_params, const double* d_u,
-                             int32_t k_bound, double* host_us, float* gpu_us, int32_t* ids)
+                             int32_t k_bound, double* host_us, float* gpu_us, double* call_us,
+                             int32_t* ids)
 {
     hipStream_t st = (hipStream_t)stream;
     if (nrows < 1) return -100;
@@ -335,8 +340,6 @@ G4H_API int g4h_graph_decode(g4s_sampler* s, void* stream, const float* d_rows, 
     int32_t* did = nullptr;
     int32_t* hid = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    hipGraph_t g = nullptr;
-    hipGraphExec_t gx = nullptr;
     int rc = 0;
     if (hipMalloc((void**)&row, (size_t)vocab * sizeof(float)) != hipSuccess ||
         hipMalloc((void**)&par, sizeof(g4s_params)) != hipSuccess ||
@@ -345,16 +348,18 @@ G4H_API int g4h_graph_decode(g4s_sampler* s, void* stream, const float* d_rows, 
         hipHostMalloc((void**)&hid, sizeof(int32_t), hipHostMallocDefault) != hipSuccess ||
         hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
         rc = -101;
-    if (rc == 0 && hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    /* the first call captures; it is not timed */
+    if (rc == 0 && (hipMemcpyAsync(row, d_rows, (size_t)vocab * sizeof(float),
+                                   hipMemcpyDeviceToDevice, st) != hipSuccess ||
+                    hipMemcpyAsync(par, d_params, sizeof(g4s_params), hipMemcpyDeviceToDevice,
+                                   st) != hipSuccess ||
+                    hipMemcpyAsync(u, d_u, sizeof(double), hipMemcpyDeviceToDevice, st) !=
+                        hipSuccess ||
+                    hipStreamSynchronize(st) != hipSuccess))
         rc = -102;
-    if (rc == 0) {
-        const int src = g4s_sample_async(s, row, G4S_DTYPE_F32, vocab, 1, par, u, k_bound, 0, did,
-                                         nullptr);
-        const hipError_t ec = hipStreamEndCapture(st, &g);
-        if (src != 0) rc = src;
-        if (rc == 0 && ec != hipSuccess) rc = -104;
-    }
-    if (rc == 0 && hipGraphInstantiate(&gx, g, nullptr, nullptr, 0) != hipSuccess) rc = -105;
+    if (rc == 0) rc = g4s_sample_graph(s, row, G4S_DTYPE_F32, vocab, 1, par, u, k_bound, 0, did,
+                                       nullptr);
+    if (rc == 0 && hipStreamSynchronize(st) != hipSuccess) rc = -103;
     for (int32_t i = 0; rc == 0 && i < nrows; ++i) {
         if (hipMemcpyAsync(row, d_rows + (int64_t)i * vocab, (size_t)vocab * sizeof(float),
                            hipMemcpyDeviceToDevice, st) != hipSuccess ||
@@ -367,7 +372,9 @@ G4H_API int g4h_graph_decode(g4s_sampler* s, void* stream, const float* d_rows, 
         }
         const double t0 = now_us();
         (void)hipEventRecord(e0, st);
-        if (hipGraphLaunch(gx, st) != hipSuccess) rc = -107;
+        const double c0 = now_us();
+        rc = g4s_sample_graph(s, row, G4S_DTYPE_F32, vocab, 1, par, u, k_bound, 0, did, nullptr);
+        const double c1 = now_us();
         (void)hipEventRecord(e1, st);
         while (rc == 0 && hipEventQuery(e1) == hipErrorNotReady) {
         }
@@ -380,11 +387,10 @@ G4H_API int g4h_graph_decode(g4s_sampler* s, void* stream, const float* d_rows, 
         (void)hipEventElapsedTime(&ms, e0, e1);
         host_us[i] = t1 - t0;
         gpu_us[i] = ms * 1000.0f;
+        call_us[i] = c1 - c0;
         ids[i] = *hid;
     }
     (void)hipStreamSynchronize(st);
-    if (gx) (void)hipGraphExecDestroy(gx);
-    if (g) (void)hipGraphDestroy(g);
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     if (row) (void)hipFree(row);

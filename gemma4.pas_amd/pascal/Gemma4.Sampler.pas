@@ -160,6 +160,10 @@ function g4s_sample_async(ASampler: PG4SSampler; ADevLogits: Pointer; ADType: In
   ARowStride: Int64; ABatch: Integer; ADevParams: PG4SParams; ADevU: PDouble;
   AKBound: Integer; AFullRows: Integer; ADevIds: PInteger;
   AOutputs: PG4SOutputs): Integer; cdecl; external CG4SLib;
+function g4s_sample_graph(ASampler: PG4SSampler; ADevLogits: Pointer; ADType: Integer;
+  ARowStride: Int64; ABatch: Integer; ADevParams: PG4SParams; ADevU: PDouble;
+  AKBound: Integer; AFullRows: Integer; ADevIds: PInteger;
+  AOutputs: PG4SOutputs): Integer; cdecl; external CG4SLib;
 // no counterpart in the engine: for callers that cannot allocate GPU memory
 // (graph capture, serving loops); no handle, errors via g4s_last_error(nil)
 function g4s_sample_topk_noalloc(ADevLogits: Pointer; ADType: Integer; AVocab: Integer;

@@ -163,6 +163,24 @@ int g4s_sample_async(g4s_sampler* sampler, const void* d_logits, int32_t dtype,
                      const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,
                      const g4s_outputs* outputs);
 
+/* g4s_sample_async launched from a hipGraph the handle owns: the first call
+ * with a given set of arguments (the pointers, dtype, row_stride, batch,
+ * k_bound, full_rows and the outputs' pointers) captures the launches on the
+ * handle's stream and instantiates them; later calls with the same arguments
+ * replay that graph (up to 8 argument sets are kept, the least recently used
+ * replaced first).  The graph reads the logits, parameters and uniforms when
+ * it runs, so a decode loop rewrites the same buffers and calls again.  Under
+ * a capture of the caller's own on the handle's stream the launches are
+ * recorded into that capture instead.  Same arguments, results and errors
+ * as g4s_sample_async; the handle needs a stream other than the null stream.
+ * Replaces the engine's per-token record + submit of its sampling work
+ * (src/Gemma4.Model.pas:1331-1375; src/Gemma4.Vulkan.pas:1449-1461) for
+ * the sampling step. */
+int g4s_sample_graph(g4s_sampler* sampler, const void* d_logits, int32_t dtype,
+                     int64_t row_stride, int32_t batch, const g4s_params* d_params,
+                     const double* d_u, int32_t k_bound, int32_t full_rows, int32_t* d_ids,
+                     const g4s_outputs* outputs);
+
 /* Rows and bytes of the device scratch array behind g4s_sample_topk_noalloc
  * (held by every GPU the library runs on until the process ends). */
 #define G4S_NOALLOC_MAX_ROWS 32
