@@ -216,3 +216,105 @@ def test_draw_targets_after_half_unit_ties(orc):
         tok, _, _, _ = orc.do_sample(rows[r], 1.0, 0, 0.99, u[r], softcap=CAP, want_probs=False)
         assert tok == first, f"row {r}: oracle {tok}, running sum says {first} (tie at {i})"
     _run(orc, codes, t, k, p, u, CAP, probs=False)
+
+
+def _target_u(orc, row, t, p, pos):
+    """u that makes the draw of a full row land exactly on index `pos` (the
+    threshold is the exact running sum there) and that index."""
+    _, _, _, pr = orc.do_sample(row, t, 0, p, 0.5, softcap=CAP, want_probs=True)
+    s = np.add.accumulate(pr, dtype=F32)
+    thr = s[pos]
+    u = _u_for(thr, F32(p))
+    return u, int(np.argmax(s >= thr))
+
+
+def test_row_state_between_calls(orc):
+    """The pipeline's per-row words are accumulated (row maxima, the
+    smallest key with e == 1 and the argmax by atomics) or handed from
+    kernel to kernel (the draw's exact sum and hit in chunk 0, the staged
+    chunk counts), and the draw chain resets them for the next call after
+    reading its own.  One handle samples four calls in a row through the
+    same row slots, each slot chosen so that a word left over from the
+    previous call, or read after its reset, changes the result:
+      slot 0: maximum 12 early (greedy) -> maximum 2.5 late (draw; a stale
+              row maximum or argmax) -> maximum 6 late behind early 3.0s
+              (greedy; a stale smallest key with e == 1 picks a 3.0);
+      slot 1: draw inside chunk 0 -> draw in a late chunk (a stale hit)
+              -> inside chunk 0 -> late chunk;
+      slot 2: top-k row -> full draw -> (not in the call) -> greedy with the
+              argmax early;
+      slot 3: draw late with |x| up to 40 -> P = 0 (the chains' early exit)
+              -> (not in the call) -> draw inside chunk 0 (the running sum of
+              chunk 0 read before its reset).
+    Ids, LSum and the greedy id of every full row equal the oracle's."""
+    rng = np.random.default_rng(73)
+    s = native.Sampler(V, max_batch=4, softcap=CAP)
+
+    def base():
+        return rng.normal(0, 0.5, V).astype(F32)
+
+    calls = []
+    # call 1
+    r0 = base(); r0[3] = 12.0; r0[rng.integers(1000, V)] = -40.0
+    r1 = base()
+    r2 = base()
+    r3 = base(); r3[rng.choice(V, 8, replace=False)] = -40.0
+    calls.append([(r0, 0.0, 0, 0.95, None), (r1, 1.0, 0, 0.99, 300),
+                  (r2, 0.7, 64, 0.95, "u"), (r3, 1.0, 0, 0.99, 200000)])
+    # call 2
+    r0 = base(); r0[250000] = 2.5
+    r1 = base()
+    r2 = base()
+    r3 = base()
+    calls.append([(r0, 1.0, 0, 0.99, 150000), (r1, 1.0, 0, 0.99, 180000),
+                  (r2, 1.0, 0, 0.99, 90000), (r3, 1.0, 0, 0.0, None)])
+    # call 3 (two rows)
+    r0 = base(); r0[rng.choice(1000, 10, replace=False)] = 3.0; r0[200000] = 6.0
+    r1 = base()
+    calls.append([(r0, 0.0, 0, 0.95, None), (r1, 1.0, 0, 0.99, 700)])
+    # call 4
+    r0 = base()
+    r1 = base()
+    r2 = base(); r2[10] = 4.0
+    r3 = base()
+    calls.append([(r0, 1.0, 0, 0.99, 100000), (r1, 1.0, 0, 0.99, 240000),
+                  (r2, 0.0, 0, 0.95, None), (r3, 1.0, 0, 0.99, 500)])
+
+    for ci, call in enumerate(calls):
+        B = len(call)
+        codes = np.stack([_b16(c[0]) for c in call])
+        rows = _widen(codes)
+        t = np.array([c[1] for c in call], F32)
+        k = np.array([c[2] for c in call], np.int32)
+        p = np.array([c[3] for c in call], F32)
+        u = np.empty(B)
+        for r, c in enumerate(call):
+            if c[4] is None:
+                u[r] = 0.5
+            elif c[4] == "u":
+                u[r] = 0.375
+            else:
+                u[r], _ = _target_u(orc, rows[r], float(t[r]), float(p[r]), c[4])
+        d = hip.Buffer.from_array(np.ascontiguousarray(codes))
+        params = [native.TSamplingParams.make(float(a), int(b), float(q))
+                  for a, b, q in zip(t, k, p)]
+        outs = native.DeviceOutputs(B, 1)
+        rc, ids = s.sample(d, B, params, u, outputs=outs.struct, dtype=native.DTYPE_BF16)
+        assert rc == 0, s.last_error()
+        o = outs.read()
+        for r in range(B):
+            tok, det, _, _ = orc.do_sample(rows[r], t[r], k[r], p[r], u[r], softcap=CAP,
+                                           want_probs=False)
+            ctx = f"call {ci + 1} slot {r} (T={t[r]}, K={k[r]}, P={p[r]}, u={u[r]!r})"
+            assert ids[r] == tok, f"{ctx}: gpu id {ids[r]} != oracle {tok}"
+            if k[r] <= 0:
+                assert o["flags"][r] & native.FLAG_FULL_PATH, ctx
+                assert o["lsum"][r].view(np.uint32) == np.float32(det["lsum"]).view(np.uint32), \
+                    f"{ctx}: lsum {o['lsum'][r]!r} != {det['lsum']!r}"
+                assert o["argmax"][r] == det["argmax_pos"], \
+                    f"{ctx}: argmax {o['argmax'][r]} != {det['argmax_pos']}"
+            c = call[r]
+            if isinstance(c[4], int) and p[r] > 0:  # the draw lands in the chunk aimed at
+                assert ids[r] // 1024 == c[4] // 1024, f"{ctx}: id {ids[r]}, aimed at {c[4]}"
+        d.free()
+    s.close()
