@@ -259,7 +259,8 @@ def probe(H, stream, name, steps):
     """One workload alone, `steps` launches, for hardware-counter runs:
     copy (128 MiB calibration copy), topk1 (top-k path B=1 fp32),
     mixed64 (B=64 fp32 rows with mixed T/K/P), full256 (full path B=256
-    bf16), lmhead (TILED64 Q4_0 LM head, B=32)."""
+    bf16), lmhead (TILED64 Q4_0 LM head, B=32), lmhead_nolog (the fused LM
+    head + sample writing no logits, B=32, K=64)."""
     from gemma4_sampler import hip, native, workload as wl
     if name == "copy":
         nbytes = 128 << 20
@@ -298,7 +299,7 @@ def probe(H, stream, name, steps):
         us, _, _, _ = batch_throughput(H, stream, d, native.DTYPE_BF16, B, par,
                                        wl.host_row_u(SEED + 4, 0, B), 0, 1, 2, steps)
         res = {"probe": name, "bytes_read": B * V * 2, "us_median": float(np.median(us))}
-    elif name == "lmhead":
+    elif name in ("lmhead", "lmhead_nolog"):
         B, cols = 32, wl.HIDDEN_GEMMA4
         s = native.Sampler(V, max_batch=B, softcap=wl.SOFTCAP_GEMMA4, stream=stream)
         dw = hip.Buffer(V * (cols // 32) * 18)
@@ -310,10 +311,18 @@ def probe(H, stream, name, steps):
         stream.synchronize()
         dw.free()
         us = np.zeros(steps, np.float32)
-        rc = H.g4h_lmhead_tiled(s.h, stream.handle, dt.ptr, V, cols, dh.ptr, B, dl.ptr, 1, steps,
-                                _vp(us))
+        if name == "lmhead":
+            rc = H.g4h_lmhead_tiled(s.h, stream.handle, dt.ptr, V, cols, dh.ptr, B, dl.ptr, 1,
+                                    steps, _vp(us))
+        else:
+            parr = native.params_array([native.TSamplingParams.make(0.7, 64, 0.95)] * B)
+            uarr = np.ascontiguousarray(wl.host_row_u(SEED + 7, 0, B), np.float64)
+            ids = np.zeros(B, np.int32)
+            rc = H.g4h_lmhead_sample_fused(s.h, dt.ptr, V, cols, dh.ptr, B, None,
+                                           ctypes.cast(parr, ctypes.c_void_p), _vp(uarr),
+                                           _vp(ids), 1, steps, _vp(us))
         if rc != 0:
-            raise RuntimeError(f"g4h_lmhead_tiled failed: {rc} {s.last_error()}")
+            raise RuntimeError(f"{name} probe failed: {rc} {s.last_error()}")
         res = {"probe": name, "bytes_read": V * (cols // 32) * 18,
                "flops": 2.0 * B * V * cols, "us_median": float(np.median(us))}
         s.close()
@@ -378,6 +387,14 @@ def lmhead_sampler(H, stream, threads, steps):
                                    steps, _vp(fu))
     if rc != 0:
         raise RuntimeError(f"g4h_lmhead_sample_fused failed: {rc} {s.last_error()}")
+    # the same call writing no logits (group maxima, recomputed groups)
+    nu = np.zeros(steps, np.float32)
+    nids = np.zeros(B, np.int32)
+    rc = H.g4h_lmhead_sample_fused(s.h, dt.ptr, rows, cols, dh.ptr, B, None,
+                                   ctypes.cast(parr, ctypes.c_void_p), _vp(uarr), _vp(nids), 2,
+                                   steps, _vp(nu))
+    if rc != 0:
+        raise RuntimeError(f"g4h_lmhead_sample_fused (no logits) failed: {rc} {s.last_error()}")
     want = orc.sample_batch(logits, 0, V, V, (np.full(B, 0.7, np.float32), np.full(B, 64, np.int32),
                                               np.full(B, 0.95, np.float32)), u,
                             softcap=wl.SOFTCAP_GEMMA4, threads=threads)
@@ -387,7 +404,7 @@ def lmhead_sampler(H, stream, threads, steps):
     s.close()
     for b in (dw, dh, dl, dp, du, di, dt):
         b.free()
-    lm50, tot50, tl50, fu50 = (float(np.median(x)) for x in (lm, tot, tl, fu))
+    lm50, tot50, tl50, fu50, nu50 = (float(np.median(x)) for x in (lm, tot, tl, fu, nu))
     wbytes = rows * (cols // 32) * 18
     flops = 2.0 * B * rows * cols
     return {"batch": B, "us_per_batch_p50": fu50,
@@ -398,10 +415,14 @@ def lmhead_sampler(H, stream, threads, steps):
             "lmhead_hbm_gbps": wbytes / (tl50 * 1e-6) / 1e9,
             "weights_bytes": wbytes,
             "fused_call": "g4s_lmhead_sample_q4_0 (TILED64 weights; synchronous, host-timed)",
+            "fused_no_logits": {"us_per_batch_p50": nu50, "logits_written_bytes": 0,
+                                "group_summary_bytes": B * ((rows + 63) // 64) * 8,
+                                "id_mismatches": int(np.sum(nids != want))},
             "row_layout": {"lmhead_us_p50": lm50, "lmhead_plus_sampler_us_p50": tot50,
                            "sampler_us_p50": tot50 - lm50},
             "logits_identical_across_layouts": same_logits,
-            "id_mismatches": int(np.sum(ids != want)) + int(np.sum(fids != want)),
+            "id_mismatches": int(np.sum(ids != want)) + int(np.sum(fids != want)) +
+                             int(np.sum(nids != want)),
             "logit_mismatches_in_256_checked_rows": logit_bad}
 
 
@@ -457,7 +478,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=10000)
     ap.add_argument("--batch-steps", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="small run for profiling")
-    ap.add_argument("--probe", choices=["copy", "topk1", "mixed64", "full256", "lmhead"],
+    ap.add_argument("--probe", choices=["copy", "topk1", "mixed64", "full256", "lmhead",
+                                        "lmhead_nolog"],
                     help="run one workload alone (for hardware-counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:

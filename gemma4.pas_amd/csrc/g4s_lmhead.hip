@@ -253,31 +253,9 @@ __device__ __forceinline__ void fma_pair(float& S0, float& S1, const float4 x, c
 }
 #undef G4S_FMAC_BCAST
 
-/* Weight j of the block: term (Single(q) * LScale) of CpuMatVecQ4
- * (Tensors.pas:586,590) with q = nibble - 8; fma(nibble, s, -8s) is exact
- * and equal to it (both are (nibble - 8) * s, at most 15 significant bits). */
-__device__ __forceinline__ void dequant(const uint4 w, float sc, float (&q)[32])
-{
-    const float m8 = -8.0f * sc;
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        /* the nibble masks stay opaque so that each nibble converts with one
-         * v_cvt_f32_ubyteN (instead of a field extract and a convert) */
-        uint32_t lo, hi;
-        asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(ws[d]));
-        asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi) : "v"(ws[d] >> 4));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            q[8 * d + 2 * i] = __builtin_fmaf((float)((lo >> (8 * i)) & 0xFFu), sc, m8);
-            q[8 * d + 2 * i + 1] = __builtin_fmaf((float)((hi >> (8 * i)) & 0xFFu), sc, m8);
-        }
-    }
-}
-
 __global__ __launch_bounds__(64 * kTileWaves) void lmhead_tiled_kernel(
     const uint8_t* __restrict__ tiles, int32_t rows, int32_t nblk, const float* __restrict__ h,
-    int32_t cols, int32_t batch, float* __restrict__ out, int64_t stride, uint32_t* __restrict__ gmax,
+    int32_t cols, int32_t batch, float* __restrict__ out, int64_t stride, uint64_t* __restrict__ gsum,
     int32_t ngroups)
 {
     const int lane = threadIdx.x & 63;
@@ -315,7 +293,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void lmhead_tiled_kernel(
         for (int p = 0; p < kXAhead; ++p) xr[p] = xload(p, 0);
         for (int32_t k = 0; k < nblk; ++k) {
             float q[32];
-            dequant(w, sc, q);
+            q4_dequant32(w, sc, q);
             const int32_t kn = k + 1 < nblk ? k + 1 : k;
             sc = tsc[(uint32_t)(kn * kTileF) + ul];
             w = tq[(uint32_t)(kn * kTileQ) + ul];
@@ -338,10 +316,15 @@ __global__ __launch_bounds__(64 * kTileWaves) void lmhead_tiled_kernel(
 #pragma unroll
         for (int b = 0; b < kTileB; ++b) {
             if (b0 + b < batch) {
-                if (live) out[(int64_t)(b0 + b) * stride + r] = S[b];
-                if (gmax) {
-                    const uint32_t key = wave_max_u32(live ? cand_key(S[b]) : 0u);
-                    if (lane == 0) gmax[(int64_t)(b0 + b) * ngroups + g] = key;
+                if (out && live) out[(int64_t)(b0 + b) * stride + r] = S[b];
+                if (gsum) {
+                    /* the group's summary: its largest key, the lowest row
+                     * holding it, and the largest key of the other rows */
+                    const uint32_t key = live ? cand_key(S[b]) : 0u;
+                    const uint32_t kmax = wave_max_u32(key);
+                    const uint32_t r6 = (uint32_t)__builtin_ctzll(__ballot(key == kmax));
+                    const uint32_t k2 = wave_max_u32(ul == r6 ? 0u : key);
+                    if (lane == 0) gsum[(int64_t)(b0 + b) * ngroups + g] = gsum_pack(kmax, r6, k2);
                 }
             }
         }
@@ -395,13 +378,13 @@ hipError_t q4_tile_launch(const uint8_t* src, int32_t rows, int32_t nblk, uint8_
 }
 
 hipError_t lmhead_tiled_launch(const uint8_t* tiles, int32_t rows, int32_t cols, const float* h,
-                               int32_t batch, float* logits, int64_t stride, uint32_t* gmax,
+                               int32_t batch, float* logits, int64_t stride, uint64_t* gsum,
                                hipStream_t s)
 {
     const int32_t ngroups = (rows + kQ4TileRows - 1) / kQ4TileRows;
     const unsigned grid = (unsigned)((ngroups + kTileWaves - 1) / kTileWaves);
     hipLaunchKernelGGL(lmhead_tiled_kernel, dim3(grid), dim3(64 * kTileWaves), 0, s, tiles, rows,
-                       cols / 32, h, cols, batch, logits, stride, gmax, ngroups);
+                       cols / 32, h, cols, batch, logits, stride, gsum, ngroups);
     return hipGetLastError();
 }
 

@@ -28,6 +28,14 @@ namespace {
 
 thread_local std::string g_create_error;
 
+/* The fused LM head's weights and hidden vectors, for the rows whose
+ * logits were not written (recomputed groups). */
+struct LmSource {
+    const uint8_t* tiles;
+    const float* hidden;
+    int32_t cols;
+};
+
 }  // namespace
 
 namespace g4s {
@@ -63,7 +71,10 @@ struct g4s_sampler {
     uint32_t* wbounds = nullptr;
     uint32_t* tickets = nullptr;
     uint32_t* dec_tickets = nullptr; /* [min(max_batch, kDecMaxRows)][kDecTicketWords] */
-    uint32_t* gmax = nullptr;     /* [max_batch][ceil(vocab/64)] LM-head group maxima */
+    uint64_t* gsum = nullptr;     /* [max_batch][ceil(vocab/64)] LM-head group summaries */
+    int32_t* gc_jobs = nullptr;   /* [max_batch][kGcJobStride] group recompute jobs */
+    float* row_logits = nullptr;  /* one row of logits for a recomputed row (allocated by
+                                     the first fused call without d_logits that needs it) */
     /* full path workspace */
     g4s::FullWorkspace full{};
     /* per-call staging */
@@ -133,7 +144,9 @@ void release(g4s_sampler* s)
     f(s->wbounds);
     f(s->tickets);
     f(s->dec_tickets);
-    f(s->gmax);
+    f(s->gsum);
+    f(s->gc_jobs);
+    f(s->row_logits);
     g4s::full_free(s->full);
     f(s->d_params);
     f(s->d_u);
@@ -177,7 +190,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
             const g4s_params* d_params, const double* d_u, const g4s_params* p0, double u0,
             int32_t kbound, bool full_rows, bool wide, int32_t* d_ids,
             const g4s_outputs* outputs, uint32_t* done = nullptr, uint32_t seq = 0,
-            const uint32_t* gmax = nullptr)
+            const uint64_t* gsum = nullptr, const LmSource* lm = nullptr)
 {
     g4s_outputs out{};
     if (outputs) out = *outputs;
@@ -207,15 +220,22 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         a.wbounds = s->wbounds;
         a.tickets = s->tickets;
         a.dec_tickets = s->dec_tickets;
+        if (lm) {
+            a.lm_tiles = lm->tiles;
+            a.lm_hidden = lm->hidden;
+            a.lm_cols = lm->cols;
+            a.gc_jobs = s->gc_jobs;
+        }
         a.ids = d_ids;
         a.done = done;
         a.seq = seq;
         a.out = out;
         hipError_t e = hipErrorNotSupported;
-        if (gmax && dtype == G4S_DTYPE_F32)
-            e = g4s::topk_groups_launch(cfg, a, gmax, (s->vocab + 63) / 64, s->stream);
+        if (gsum && dtype == G4S_DTYPE_F32)
+            e = g4s::topk_groups_launch(cfg, a, gsum, (s->vocab + 63) / 64, s->stream);
         if (e == hipErrorNotSupported) {
             (void)hipGetLastError();
+            if (!d_logits) return fail(s, G4S_ERR_UNSUPPORTED, "top-k rows without logits");
             e = g4s::topk_launch(cfg, a, dtype, s->stream, s->ncu);
         }
         if (e != hipSuccess) return hip_fail(s, e, "top-k kernel launch");
@@ -321,7 +341,8 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
     dm((void**)&s->tickets, mb * sizeof(uint32_t));
     const size_t dec_rows = mb < (size_t)g4s::kDecMaxRows ? mb : (size_t)g4s::kDecMaxRows;
     dm((void**)&s->dec_tickets, dec_rows * g4s::kDecTicketWords * sizeof(uint32_t));
-    dm((void**)&s->gmax, mb * (size_t)((vocab + 63) / 64) * sizeof(uint32_t));
+    dm((void**)&s->gsum, mb * (size_t)((vocab + 63) / 64) * sizeof(uint64_t));
+    dm((void**)&s->gc_jobs, mb * g4s::kGcJobStride * sizeof(int32_t));
     dm((void**)&s->d_params, mb * sizeof(g4s_params));
     dm((void**)&s->d_u, mb * sizeof(double));
     hm((void**)&s->h_params, mb * sizeof(g4s_params));
@@ -383,7 +404,8 @@ int check_params(g4s_sampler* s, int32_t batch, const g4s_params* params, const 
  * logits from the tiled LM head with their group maxima. */
 int sample_sync(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_stride,
                 int32_t batch, const g4s_params* params, const double* u, int32_t* ids,
-                const g4s_outputs* outputs, const uint32_t* gmax)
+                const g4s_outputs* outputs, const uint64_t* gsum = nullptr,
+                const LmSource* lm = nullptr)
 {
     int rc;
     int32_t kbound = 0;
@@ -421,7 +443,7 @@ int sample_sync(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row
 
     if (batch == 1) {
         rc = enqueue(s, d_logits, dtype, row_stride, 1, nullptr, nullptr, &params[0], u[0], kbound,
-                     full_rows, wide, s->h_ids, &out, done, seq, gmax);
+                     full_rows, wide, s->h_ids, &out, done, seq, gsum, lm);
     } else {
         std::memcpy(s->h_params, params, sizeof(g4s_params) * batch);
         std::memcpy(s->h_u, u, sizeof(double) * batch);
@@ -432,7 +454,7 @@ int sample_sync(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row
                                s->stream);
         if (e != hipSuccess) return hip_fail(s, e, "parameter upload");
         rc = enqueue(s, d_logits, dtype, row_stride, batch, s->d_params, s->d_u, nullptr, 0.0,
-                     kbound, full_rows, wide, s->h_ids, &out, done, seq, gmax);
+                     kbound, full_rows, wide, s->h_ids, &out, done, seq, gsum, lm);
     }
     if (rc) return rc;
     hipError_t e = hipSuccess;
@@ -634,13 +656,15 @@ G4S_API int g4s_lmhead_q4_0(g4s_sampler* s, const void* d_weights, int32_t rows,
 namespace {
 
 int check_tiled(g4s_sampler* s, const void* d_tiles, int32_t rows, int32_t cols,
-                const float* d_hidden, int32_t batch, float* d_logits, int64_t logits_stride)
+                const float* d_hidden, int32_t batch, float* d_logits, int64_t logits_stride,
+                bool logits_optional = false)
 {
-    if (!d_tiles || !d_hidden || !d_logits)
+    if (!d_tiles || !d_hidden || (!d_logits && !logits_optional))
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "NULL device pointer");
     if (rows < 1 || cols < 32 || (cols % 32) != 0)
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "rows %d / cols %d (cols must be a multiple of 32)",
                     rows, cols);
+    if (!d_logits) logits_stride = rows;
     if (batch < 1 || logits_stride < rows)
         return fail(s, G4S_ERR_INVALID_ARGUMENT, "batch %d / logits_stride %lld", batch,
                     (long long)logits_stride);
@@ -773,6 +797,72 @@ G4S_API int g4s_generate(g4s_sampler* s, int32_t batch, const g4s_params* params
     return G4S_OK;
 }
 
+namespace {
+
+/* The fused call without logits accepts top-k rows only (0 < TopK <=
+ * kMaxTopK, TopK < vocab), at most 8192 64-row groups, and a hidden vector
+ * that fits the recompute launch's LDS. */
+int check_no_logits(g4s_sampler* s, int32_t cols, int32_t batch, const g4s_params* params)
+{
+    if ((s->vocab + 63) / 64 > 8192)
+        return fail(s, G4S_ERR_UNSUPPORTED, "vocab %d above 524288 without d_logits", s->vocab);
+    if ((int64_t)cols * 4 > 65536)
+        return fail(s, G4S_ERR_UNSUPPORTED, "cols %d above 16384 without d_logits", cols);
+    for (int32_t r = 0; r < batch; ++r)
+        if (!is_topk_row(params[r], s->vocab) || params[r].top_k > g4s::kMaxTopK)
+            return fail(s, G4S_ERR_INVALID_ARGUMENT,
+                        "row %d: TopK %d needs d_logits (only 0 < TopK <= %d without them)", r,
+                        params[r].top_k, g4s::kMaxTopK);
+    return G4S_OK;
+}
+
+/* Row r of a fused call without logits whose ties needed every logit: its
+ * logits recomputed into the handle's row buffer, then sampled as
+ * g4s_sample_ex would, into row r of the caller's outputs. */
+int resample_row(g4s_sampler* s, const void* d_tiles, int32_t cols, const float* d_hidden,
+                 int32_t r, const g4s_params* params, const double* u, int32_t* ids,
+                 const g4s_outputs* outputs)
+{
+    const int64_t stride = ((int64_t)s->vocab + 3) & ~(int64_t)3;
+    if (!s->row_logits) {
+        if (hipMalloc((void**)&s->row_logits, (size_t)stride * sizeof(float)) != hipSuccess) {
+            s->row_logits = nullptr;
+            return fail(s, G4S_ERR_OUT_OF_MEMORY, "row buffer of %lld floats",
+                        (long long)stride);
+        }
+    }
+    hipError_t e = g4s::lmhead_tiled_launch((const uint8_t*)d_tiles, s->vocab, cols,
+                                            d_hidden + (int64_t)r * cols, 1, s->row_logits,
+                                            stride, nullptr, s->stream);
+    if (e != hipSuccess) return hip_fail(s, e, "LM-head kernel launch");
+    g4s_outputs o{};
+    if (outputs) {
+        o = *outputs;
+        const int64_t cap = o.capacity > 0 ? o.capacity : 0;
+        if (o.count) o.count += r;
+        if (o.indices) o.indices += (int64_t)r * cap;
+        if (o.probs) o.probs += (int64_t)r * cap;
+        if (o.argmax) o.argmax += r;
+        if (o.lsum) o.lsum += r;
+        if (o.flags) o.flags += r;
+    }
+    int32_t id = -1;
+    const int rc = sample_sync(s, s->row_logits, G4S_DTYPE_F32, stride, 1, &params[r], &u[r], &id,
+                               outputs ? &o : nullptr);
+    ids[r] = id;
+    if (rc) return rc;
+    if (o.flags) {
+        uint32_t f = 0u;
+        e = hipMemcpy(&f, o.flags, sizeof(f), hipMemcpyDeviceToHost);
+        f |= G4S_FLAG_ROW_RECOMPUTED;
+        if (e == hipSuccess) e = hipMemcpy(o.flags, &f, sizeof(f), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(s, e, "flags of a recomputed row");
+    }
+    return G4S_OK;
+}
+
+}  // namespace
+
 G4S_API int g4s_lmhead_sample_q4_0(g4s_sampler* s, const void* d_tiles, int32_t cols,
                                    const float* d_hidden, int32_t batch, float* d_logits,
                                    int64_t logits_stride, const g4s_params* params,
@@ -780,15 +870,35 @@ G4S_API int g4s_lmhead_sample_q4_0(g4s_sampler* s, const void* d_tiles, int32_t 
 {
     if (!s) return fail(nullptr, G4S_ERR_INVALID_ARGUMENT, "sampler is NULL");
     s->err.clear();
-    int rc = check_tiled(s, d_tiles, s->vocab, cols, d_hidden, batch, d_logits, logits_stride);
+    int rc = check_tiled(s, d_tiles, s->vocab, cols, d_hidden, batch, d_logits, logits_stride,
+                         true);
     if (rc) return rc;
-    rc = check_logits(s, d_logits, G4S_DTYPE_F32, logits_stride, batch);
-    if (rc) return rc;
+    if (d_logits) {
+        rc = check_logits(s, d_logits, G4S_DTYPE_F32, logits_stride, batch);
+        if (rc) return rc;
+    }
     rc = check_params(s, batch, params, u, ids);
     if (rc) return rc;
+    if (!d_logits) {
+        rc = check_no_logits(s, cols, batch, params);
+        if (rc) return rc;
+    }
     hipError_t e = g4s::lmhead_tiled_launch((const uint8_t*)d_tiles, s->vocab, cols, d_hidden,
-                                            batch, d_logits, logits_stride, s->gmax, s->stream);
+                                            batch, d_logits, logits_stride, s->gsum, s->stream);
     if (e != hipSuccess) return hip_fail(s, e, "LM-head kernel launch");
-    return sample_sync(s, d_logits, G4S_DTYPE_F32, logits_stride, batch, params, u, ids, outputs,
-                       s->gmax);
+    if (d_logits)
+        return sample_sync(s, d_logits, G4S_DTYPE_F32, logits_stride, batch, params, u, ids,
+                           outputs, s->gsum);
+    const LmSource lm{(const uint8_t*)d_tiles, d_hidden, cols};
+    rc = sample_sync(s, nullptr, G4S_DTYPE_F32, s->vocab, batch, params, u, ids, outputs, s->gsum,
+                     &lm);
+    if (rc && rc != G4S_ERR_EMPTY_ROW) return rc;
+    const int rc_rows = rc;
+    std::vector<uint32_t> fl(s->h_flags, s->h_flags + batch);
+    for (int32_t r = 0; r < batch; ++r) {
+        if (!(fl[r] & G4S_FLAG_ROW_RECOMPUTED)) continue;
+        rc = resample_row(s, d_tiles, cols, d_hidden, r, params, u, ids, outputs);
+        if (rc) return rc;
+    }
+    return rc_rows;
 }

@@ -29,9 +29,21 @@ static_assert(kDecSlotsPerRow <= 16384, "the wave lists fit a row's candidate sl
 struct ChunkRec {
     uint32_t count;  /* candidates emitted */
     uint32_t bound;  /* lower bound of the chunk's K-th largest key (exact when mode bit set) */
-    uint32_t rsv;    /* reserved (0) */
+    uint32_t rsv;    /* 0, or kRecNeedRow in the row's first record */
     uint32_t mode_e; /* bit 31: exact select; bits 0-30: copies of the K-th key in the chunk */
 };
+
+/* rsv of a row's first record: the candidates cannot decide the row without
+ * logits that were never written (the fused LM head without d_logits); the
+ * merge gives the row id -1 and G4S_FLAG_ROW_RECOMPUTED, and the host
+ * samples it again from recomputed logits. */
+constexpr uint32_t kRecNeedRow = 1u;
+
+/* Fused LM head without logits: per row, the 64-row groups whose logits the
+ * recompute launch produces: [0] count, [1] first candidate slot of the
+ * recomputed logits (64 slots per group), [2 ..] the groups. */
+constexpr int kGcMaxJobs = 32;
+constexpr int kGcJobStride = kGcMaxJobs + 2;
 
 /* A candidate: order-preserving key in the high word, vocab index in the low word. */
 __host__ __device__ inline uint64_t cand_pack(uint32_t key, uint32_t idx)
@@ -70,6 +82,13 @@ struct TopkArgs {
     g4s_outputs out;
     uint32_t* dec_tickets; /* [batch][kDecTicketWords] election counters of the decode
                               launch, zero between launches; NULL: no decode launch */
+    /* the fused LM head without logits (logits == NULL): its TILED64
+     * weights, hidden vectors [batch][lm_cols] and the recompute jobs
+     * [batch][kGcJobStride] */
+    const uint8_t* lm_tiles;
+    const float* lm_hidden;
+    int32_t lm_cols;
+    int32_t* gc_jobs;
 };
 
 struct TopkConfig {
@@ -93,10 +112,12 @@ bool decode_eligible(const TopkArgs& a, int dtype);
 hipError_t decode_launch(const TopkArgs& a, int dtype, hipStream_t s);
 
 /* Rows whose f32 logits come from the tiled LM head with its 64-logit group
- * maxima (gmax [batch][ngroups], candidate keys): candidates from the groups
+ * summaries (gsum [batch][ngroups], gsum_pack): candidates from the groups
  * whose maximum reaches the K-th largest group maximum, then the merge launch
- * (mode 2).  hipErrorNotSupported above 8192 groups. */
-hipError_t topk_groups_launch(const TopkConfig& c, const TopkArgs& a, const uint32_t* gmax,
+ * (mode 2).  With a.logits == NULL a candidate group gives its maximum, or,
+ * when its second largest key may reach the bound, its 64 logits recomputed
+ * by a launch in between.  hipErrorNotSupported above 8192 groups. */
+hipError_t topk_groups_launch(const TopkConfig& c, const TopkArgs& a, const uint64_t* gsum,
                               int32_t ngroups, hipStream_t s);
 
 }  // namespace g4s

@@ -43,6 +43,7 @@
  */
 #include "g4s_select.h"
 #include "g4s_topk.h"
+#include "g4s_lmhead.h"
 
 #include <type_traits>
 
@@ -397,7 +398,7 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         ChunkRec r;
         r.count = (uint32_t)w0;
         r.bound = (uint32_t)(w0 >> 32);
-        r.rsv = 0u;
+        r.rsv = (uint32_t)w1;
         r.mode_e = (uint32_t)(w1 >> 32);
         sh.rec[tid] = r;
     }
@@ -409,6 +410,19 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
     }
     if (use_wb && tid < nwave) sh.wb[tid] = wbv;
     __syncthreads();
+    /* a row the candidates cannot decide without its logits (none written) */
+    bool need_row = sh.rec[0].rsv == kRecNeedRow;
+    if (need_row) {
+        if (wid == 0) {
+            if (lane == 0) {
+                st_sys(&a.ids[row], -1);
+                if (a.out.flags) st_sys(&a.out.flags[row], flags | G4S_FLAG_ROW_RECOMPUTED);
+                if (a.out.count) a.out.count[row] = 0;
+            }
+            publish_done(a.done, row, a.seq);
+        }
+        return;
+    }
     uint32_t lb, l1 = 0u;
     bool any_exact;
     {
@@ -693,6 +707,8 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
                 for (int i = tid; i < M; i += BLOCK)
                     if (surv_ok(i)) sh.surv[soff++] = ent(i);
                 nsurv = sv;
+            } else if (!a.logits) {
+                need_row = true; /* the replay needs every logit */
             } else {
                 float* hv = reinterpret_cast<float*>(sh.surv);
                 int32_t* hi = reinterpret_cast<int32_t*>(sh.surv) + KCAP;
@@ -713,7 +729,9 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         if (wid == 0) {
             if (lane == 0) {
                 st_sys(&a.ids[row], -1);
-                if (a.out.flags) st_sys(&a.out.flags[row], flags | G4S_FLAG_EMPTY);
+                if (a.out.flags)
+                    st_sys(&a.out.flags[row],
+                           flags | (need_row ? G4S_FLAG_ROW_RECOMPUTED : G4S_FLAG_EMPTY));
                 if (a.out.count) a.out.count[row] = 0;
             }
             publish_done(a.done, row, a.seq);
@@ -927,45 +945,61 @@ __device__ uint32_t regs_radix_kth_agg(const uint32_t (&keys)[ITEMS], int k, uin
 }
 
 /* The top-k candidates of rows whose logits come from the tiled LM head,
- * which also leaves each 64-logit group's largest candidate key.  tau0 is
- * the K-th largest group maximum with its low 16 bits cleared (1 when at
- * most K groups hold a key): K groups hold a key >= tau0, so tau0 is at most
- * the row's K-th largest key, and every key >= tau0 lies in a group whose
- * maximum is >= tau0.  Those groups (about K of them) are read back and
- * their keys >= tau0 become the merge's candidates, laid out as the chunk
- * launch would leave them: slot i
- * of the row belongs to chunk i >> cap_log2, every chunk's record carries
- * tau0 as its bound, and the per-wave bounds are 0 (no information).  When
- * the keys >= tau0 outnumber the row's slots (heavy ties), the row is
- * written as one exact chunk record instead: the keys above the row's K-th
- * largest key tau and the first min(copies, K) copies of tau in index order,
- * as the chunk launch's exact select does.  The merge launch (mode 2) then
- * runs unchanged on the materialized logits. */
+ * which also leaves each 64-logit group's summary (gsum_pack: its largest
+ * candidate key, that key's row, a bound of the others).  tau0 is the K-th
+ * largest group maximum with its low 16 bits cleared (1 when at most K
+ * groups hold a key): K groups hold a key >= tau0, so tau0 is at most the
+ * row's K-th largest key, and every key >= tau0 lies in a group whose
+ * maximum is >= tau0.  Those groups (about K of them) give the merge's
+ * candidates, laid out as the chunk launch would leave them: slot i of the
+ * row belongs to chunk i >> cap_log2, every chunk's record carries tau0 as
+ * its bound, and the per-wave bounds are 0 (no information).
+ *  - with the logits written, a candidate group's keys >= tau0 are read back;
+ *    when they outnumber the row's slots (heavy ties), the row is written
+ *    as one exact chunk record instead: the keys above the row's K-th largest
+ *    key tau and the first min(copies, K) copies of tau in index order, as
+ *    the chunk launch's exact select does;
+ *  - without them, a candidate group whose other keys are all below tau0
+ *    (by the summary's bound) gives its maximum; any other candidate group
+ *    becomes a recompute job: its 64 logits are recomputed for this row
+ *    (group_logits_kernel) into 64 slots after the maxima.  Too many jobs,
+ *    or candidates beyond the slots, mark the row kRecNeedRow.
+ * The merge launch (mode 2) then runs unchanged. */
 constexpr int kGcBlock = 1024;
 constexpr int kGcItems = 8; /* group maxima per thread: up to 8192 groups */
 constexpr int kGcLoads = 8; /* candidate groups per wave whose logits are loaded together */
 
-__global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const uint32_t* gmax,
+__global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const uint64_t* gsum,
                                                               int32_t ngroups, int32_t nwave)
 {
     __shared__ uint32_t s_hist[256];
     __shared__ int s_misc[8];
     __shared__ int s_scan[kGcBlock / 64];
     __shared__ int s_list[kGcBlock * kGcItems];
-    __shared__ int s_cnt;
+    __shared__ int s_cnt, s_njob;
+    __shared__ int s_jobs[kGcMaxJobs];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     constexpr int NW = kGcBlock / 64;
     const int row = blockIdx.x;
     const g4s_params rp = a.params ? a.params[row] : a.p0;
     const int K = rp.top_k;
-    if (!(K >= 1 && K < a.vocab) || K > a.kbound) return; /* the merge launch flags the row */
-    const float* lg = reinterpret_cast<const float*>(a.logits) + (int64_t)row * a.row_stride;
-    const uint32_t* gm = gmax + (int64_t)row * ngroups;
+    int32_t* jobs = a.gc_jobs ? a.gc_jobs + (int64_t)row * kGcJobStride : nullptr;
+    if (!(K >= 1 && K < a.vocab) || K > a.kbound) {
+        if (tid == 0 && jobs) jobs[0] = 0;
+        return; /* the merge launch flags the row */
+    }
+    const float* lg = a.logits ? reinterpret_cast<const float*>(a.logits) + (int64_t)row * a.row_stride
+                               : nullptr;
+    const uint64_t* gs = gsum + (int64_t)row * ngroups;
     const int S = a.splits;
     const int cap = 1 << a.cap_log2;
     const int slots = S << a.cap_log2;
     uint64_t* rc = a.cand + (int64_t)row * kCandRow;
-    if (tid == 0) s_cnt = 0;
+    ChunkRec* recs = a.recs + (int64_t)row * kMaxSplits;
+    if (tid == 0) {
+        s_cnt = 0;
+        s_njob = 0;
+    }
 
     /* thread t holds groups kGcItems*t .. +kGcItems-1 */
     uint32_t keys[kGcItems];
@@ -973,7 +1007,7 @@ __global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const 
 #pragma unroll
     for (int q = 0; q < kGcItems; ++q) {
         const int g = tid * kGcItems + q;
-        keys[q] = g < ngroups ? gm[g] : 0u;
+        keys[q] = g < ngroups ? gsum_key(gs[g]) : 0u;
         nz += keys[q] != 0u;
     }
     nz = block_sum_i32<kGcBlock>(nz, s_scan);
@@ -996,6 +1030,40 @@ __global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const 
             if (keys[q] >= tau0) s_list[pos++] = tid * kGcItems + q;
     }
     __syncthreads();
+    if (!lg) {
+        /* no logits: a candidate group's maximum, or a recompute job */
+        for (int t = tid; t < ng; t += kGcBlock) {
+            const int g = s_list[t];
+            const uint64_t sm = gs[g];
+            if (gsum_bound2(sm) >= tau0) {
+                const int j = atomicAdd(&s_njob, 1);
+                if (j < kGcMaxJobs) s_jobs[j] = g;
+            } else {
+                const int pos = atomicAdd(&s_cnt, 1);
+                if (pos < slots)
+                    rc[pos] = cand_pack(gsum_key(sm), (uint32_t)(g * 64) + gsum_row(sm));
+            }
+        }
+        __syncthreads();
+        const int nmax = s_cnt, njob = s_njob;
+        const int M0 = nmax + 64 * njob;
+        const bool need_row = njob > kGcMaxJobs || M0 > slots;
+        if (tid == 0) {
+            jobs[0] = need_row ? 0 : njob;
+            jobs[1] = nmax;
+        }
+        if (!need_row)
+            for (int j = tid; j < njob; j += kGcBlock) jobs[2 + j] = s_jobs[j];
+        for (int i = tid; i < nwave && i < kWaveBounds; i += kGcBlock)
+            a.wbounds[(int64_t)row * kWaveBounds + i] = 0u;
+        for (int c = tid; c < S; c += kGcBlock) {
+            const int n = M0 - c * cap;
+            const int cnt = need_row ? 0 : (n < 0 ? 0 : (n > cap ? cap : n));
+            recs[c] = ChunkRec{(uint32_t)cnt, cnt > 0 ? tau0 : 1u,
+                               (need_row && c == 0) ? kRecNeedRow : 0u, 0u};
+        }
+        return;
+    }
     /* their keys >= tau0, one group per wave at a time (lane = logit) */
     const auto gkey = [&](int g) -> uint32_t {
         const int64_t i = (int64_t)g * 64 + lane;
@@ -1027,7 +1095,6 @@ __global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const 
     const int M0 = s_cnt;
     for (int i = tid; i < nwave && i < kWaveBounds; i += kGcBlock)
         a.wbounds[(int64_t)row * kWaveBounds + i] = 0u;
-    ChunkRec* recs = a.recs + (int64_t)row * kMaxSplits;
     if (M0 <= slots) {
         for (int c = tid; c < S; c += kGcBlock) {
             const int n = M0 - c * cap;
@@ -1084,6 +1151,32 @@ __global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const 
     for (int c = tid; c < S; c += kGcBlock)
         recs[c] = c == 0 ? ChunkRec{(uint32_t)(gt + want), tau, 0u, 0x80000000u | (uint32_t)eq}
                          : ChunkRec{0u, 1u, 0u, 0u};
+}
+
+/* The recompute jobs of group_cand_kernel (fused LM head without logits):
+ * one wave per job, the row's hidden vector staged in LDS, the group's 64
+ * logits in the LM head's term order (bit-exact with the logits it did not
+ * write) as candidates in the job's 64 slots; a row past the vocabulary
+ * gets key 0, which the merge drops with every key below tau0. */
+constexpr int kGcWeightsAhead = 16; /* weight blocks in flight per recompute wave */
+
+__global__ __launch_bounds__(64) void group_logits_kernel(TopkArgs a)
+{
+    extern __shared__ __align__(16) float s_x[];
+    const int row = blockIdx.y, j = blockIdx.x;
+    const int32_t* jobs = a.gc_jobs + (int64_t)row * kGcJobStride;
+    const int njob = jobs[0];
+    if (j >= njob) return;
+    const int g = jobs[2 + j];
+    const int base = jobs[1] + 64 * j;
+    const int cols = a.lm_cols;
+    const float4* h = reinterpret_cast<const float4*>(a.lm_hidden + (int64_t)row * cols);
+    for (int i = threadIdx.x; i < cols / 4; i += 64) reinterpret_cast<float4*>(s_x)[i] = h[i];
+    __syncthreads();
+    const float S = lm_group_logit<kGcWeightsAhead>(a.lm_tiles, g, cols / 32, s_x);
+    const int64_t idx = (int64_t)g * 64 + threadIdx.x;
+    const uint32_t key = idx < a.vocab ? cand_key(S) : 0u;
+    a.cand[(int64_t)row * kCandRow + base + threadIdx.x] = cand_pack(key, (uint32_t)idx);
 }
 
 /* ---------------------------------------------------------------- launch */
@@ -1154,19 +1247,27 @@ TopkConfig topk_plan(int32_t vocab, int32_t kbound)
     return c;
 }
 
-hipError_t topk_groups_launch(const TopkConfig& c, const TopkArgs& a, const uint32_t* gmax,
+hipError_t topk_groups_launch(const TopkConfig& c, const TopkArgs& a, const uint64_t* gsum,
                               int32_t ngroups, hipStream_t s)
 {
     if (ngroups > kGcBlock * kGcItems) return hipErrorNotSupported;
     /* two chunks' slots (>= 8 x kbound) hold the candidates of all but
      * heavily tied rows, which take the exact record; the merge then loads
-     * only those slots */
+     * only those slots.  Without logits, four chunks' slots: the groups'
+     * maxima and 64 slots per recompute job. */
     TopkArgs b = a;
-    b.splits = c.splits < 2 ? c.splits : 2;
-    hipLaunchKernelGGL(group_cand_kernel, dim3((unsigned)a.batch), dim3(kGcBlock), 0, s, b, gmax,
+    const int smax = a.logits ? 2 : 4;
+    b.splits = c.splits < smax ? c.splits : smax;
+    hipLaunchKernelGGL(group_cand_kernel, dim3((unsigned)a.batch), dim3(kGcBlock), 0, s, b, gsum,
                        ngroups, (int32_t)(b.splits * (c.block / 64)));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (!a.logits) {
+        hipLaunchKernelGGL(group_logits_kernel, dim3((unsigned)kGcMaxJobs, (unsigned)a.batch),
+                           dim3(64), (size_t)a.lm_cols * sizeof(float), s, b);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     b.mode = 2;
     if (c.block == 512 && c.items == 16) return launch_one<512, 16, 0>(b, a.kbound, s);
     if (c.block == 1024 && c.items == 32) return launch_one<1024, 32, 0>(b, a.kbound, s);

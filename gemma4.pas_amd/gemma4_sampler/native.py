@@ -49,6 +49,7 @@ FLAG_HEAP_REPLAY = 0x20
 FLAG_CHUNK_EXACT = 0x40
 FLAG_WIDE_MERGE = 0x80
 FLAG_WIDE_K = 0x100
+FLAG_ROW_RECOMPUTED = 0x200
 FLAG_EMPTY = 0x40000000
 FLAG_ERROR = 0x80000000
 
@@ -318,7 +319,8 @@ class Sampler:
 
     def lmhead_sample_q4_0(self, d_tiles, cols, d_hidden, batch, d_logits, params, u,
                            logits_stride=None, outputs=None, check=True):
-        """g4s_lmhead_sample_q4_0: LM head + sample; returns (status, ids)."""
+        """g4s_lmhead_sample_q4_0: LM head + sample; returns (status, ids).
+        d_logits None: no logits are written (top-k rows only)."""
         L = load()
         if isinstance(params, TSamplingParams):
             params = [params] * batch

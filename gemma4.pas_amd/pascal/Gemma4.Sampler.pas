@@ -68,6 +68,7 @@ const
   G4S_FLAG_CHUNK_EXACT = $40;
   G4S_FLAG_WIDE_MERGE = $80;
   G4S_FLAG_WIDE_K = $100;
+  G4S_FLAG_ROW_RECOMPUTED = $200;
   G4S_FLAG_EMPTY = $40000000;
   G4S_FLAG_ERROR = $80000000;
 
@@ -247,7 +248,8 @@ type
 
     // The tied LM head (TILED64 weights from TGpuWeightStore.UploadQ4_0)
     // fused with the sampler: Forward's last projection + DoSample for
-    // ABatch hidden vectors (Model.pas:1285-1300,2739-2827)
+    // ABatch hidden vectors (Model.pas:1285-1300,2739-2827); ADevLogits = nil
+    // writes no logits (top-k rows with 0 < TopK <= g4s_max_top_k only)
     function LmHeadSampleQ4_0(const ADevTiles: Pointer; const ACols: Integer;
       const ADevHidden: PSingle; const ABatch: Integer; const ADevLogits: PSingle;
       const AParams: PG4SParams; const AU: PDouble; const AIds: PInteger): Boolean;

@@ -77,6 +77,9 @@ typedef struct g4s_params {
 #define G4S_FLAG_CHUNK_EXACT 0x40u  /* a vocabulary chunk needed the exact per-chunk select */
 #define G4S_FLAG_WIDE_MERGE 0x80u   /* the merge candidate set exceeded on-chip memory */
 #define G4S_FLAG_WIDE_K 0x100u      /* TopK above g4s_max_top_k(): radix select over the whole row */
+#define G4S_FLAG_ROW_RECOMPUTED 0x200u /* g4s_lmhead_sample_q4_0 without d_logits: the row's ties
+                                          needed every logit, so the call recomputed the row and
+                                          sampled it again (same result, slower) */
 #define G4S_FLAG_EMPTY 0x40000000u  /* no logit above -1e30 on the top-k path */
 #define G4S_FLAG_ERROR 0x80000000u  /* row rejected (e.g. TopK above the launch bound) */
 
@@ -233,13 +236,25 @@ int g4s_lmhead_q4_0_tiled(g4s_sampler* sampler, const void* d_tiles, int32_t row
 
 /* The LM head fused with the sampler: logits of `batch` hidden vectors over
  * the handle's `vocab` rows of TILED64 weights, then g4s_sample_ex on them
- * (same params / u / ids / outputs, same results).  While it writes the
- * logits (d_logits, f32, logits_stride >= vocab, a multiple of 4) the LM
- * head keeps each 64-row group's largest logit; top-k rows then read back
- * only the groups that can hold their top K (the K-th largest group maximum
- * bounds the K-th largest logit from below) instead of the whole row.
- * Other rows take the usual paths on the written logits.  Synchronous.
- * Replaces: Forward's LM head + readback + DoSample
+ * (same params / u / ids / outputs, same results).  The LM head keeps, per
+ * hidden vector and 64-row group, the group's largest logit (as a candidate
+ * key), its row and a bound of the group's second largest; top-k rows then
+ * take only the groups that can hold their top K (the K-th largest group
+ * maximum bounds the K-th largest logit from below).
+ *   d_logits != NULL: the logits are also written (f32, logits_stride >=
+ *     vocab, a multiple of 4); candidate groups are read back from them and
+ *     rows with TopK <= 0, >= V or above g4s_max_top_k() take the usual
+ *     paths on them.
+ *   d_logits == NULL: no logits are written (logits_stride is ignored).  A
+ *     candidate group contributes its largest logit, unless its second
+ *     largest may also be a candidate: then its 64 logits for that vector
+ *     are recomputed in the LM head's term order (bit-exact).  A row whose
+ *     ties at the K-th value need every logit is recomputed whole and
+ *     sampled again (G4S_FLAG_ROW_RECOMPUTED); the call allocates that row's
+ *     buffer (vocab floats) once per handle.  Every row must be a top-k row
+ *     with 0 < TopK <= g4s_max_top_k() (G4S_ERR_INVALID_ARGUMENT otherwise)
+ *     and vocab <= 524288 (G4S_ERR_UNSUPPORTED otherwise).
+ * Synchronous.  Replaces: Forward's LM head + readback + DoSample
  * (src/Gemma4.Model.pas:1285-1300,1379-1387,2739-2827). */
 int g4s_lmhead_sample_q4_0(g4s_sampler* sampler, const void* d_tiles, int32_t cols,
                            const float* d_hidden, int32_t batch, float* d_logits,

@@ -281,3 +281,113 @@ def test_vpk_to_sample_end_to_end(orc, tmp_path):
         assert ids[r] == tok, (r, ids[r], tok)
     st.Close()
     s.close()
+
+
+def _no_logits_check(orc, s, d_tile, w, hidden, t, k, p, u, label, capacity=256):
+    """The fused call without logits against the oracle's CpuMatVecQ4 +
+    DoSample: ids, LSum, greedy id, survivor indices and probabilities."""
+    B, cols = hidden.shape
+    vocab = s.vocab
+    dh = hip.Buffer.from_array(np.ascontiguousarray(hidden, F32))
+    outs = native.DeviceOutputs(B, capacity)
+    rc, ids = s.lmhead_sample_q4_0(d_tile, cols, dh, B, None, _params(t, k, p), u,
+                                   outputs=outs.struct)
+    assert rc == 0, s.last_error()
+    o = outs.read()
+    logits = orc.matvec_q4_batch(w, hidden, vocab, cols, threads=16)
+    for r in range(B):
+        tok, det, idx, pr = orc.do_sample(logits[r], t[r], k[r], p[r], u[r], softcap=30.0,
+                                          want_probs=True)
+        ctx = f"{label} row {r} (T={t[r]}, K={k[r]}, P={p[r]}, u={u[r]!r})"
+        assert ids[r] == tok, f"{ctx}: id {ids[r]} != oracle {tok}"
+        assert o["lsum"][r].view(np.uint32) == np.float32(det["lsum"]).view(np.uint32), ctx
+        assert o["argmax"][r] == idx[det["argmax_pos"]], ctx  # a survivor position there
+        n = o["count"][r]
+        assert n == len(idx), ctx
+        assert np.array_equal(o["indices"][r][:n], idx), ctx
+        assert np.array_equal(o["probs"][r][:n].view(np.uint32), pr.view(np.uint32)), ctx
+    return o
+
+
+def test_fused_no_logits_full_size(orc):
+    """The LM head + sampler workload (32 hidden vectors, 262144 x 2560
+    weights, T=0.7, K=64 with every 8th row K=1, P=0.95) without logits:
+    candidate groups give their maxima or are recomputed (about one group in
+    two rows holds two keys of the top K), bit-exact with the oracle."""
+    B, rows, cols = 32, V, D
+    w = wl.host_q4_weights(80, rows, cols, threads=16)
+    ntile = native.q4_0_device_bytes(rows, cols, native.Q4_LAYOUT_TILED64)
+    d_rows = hip.Buffer.from_array(w)
+    d_tile = hip.Buffer(ntile)
+    native.q4_0_repack(d_rows, rows, cols, d_tile)
+    hip.synchronize()
+    d_rows.free()
+    hidden = wl.host_hidden(81, B, cols)
+    s = native.Sampler(V, max_batch=B, softcap=30.0)
+    k = np.full(B, 64, np.int32)
+    k[::8] = 1
+    t = np.full(B, 0.7, F32)
+    p = np.full(B, 0.95, F32)
+    u = wl.host_row_u(82, 0, B)
+    o = _no_logits_check(orc, s, d_tile, w, hidden, t, k, p, u, "full size", capacity=64)
+    assert not np.any(o["flags"] & native.FLAG_ROW_RECOMPUTED), o["flags"]
+    s.close()
+
+
+def test_fused_no_logits_ties(orc):
+    """Without logits: zero hidden vectors (every logit 0; the row is
+    recomputed whole and sampled again), one-hot vectors (hundreds of tied
+    logits), groups whose first two rows have the same weights (every group
+    maximum tied inside its group: recompute jobs that decide ties by index),
+    and plain rows; K from 1 to 1000."""
+    vocab, cols, B = 9000, 64, 8
+    w = wl.host_q4_weights(131, vocab, cols).reshape(vocab, cols // 32 * 18)
+    w[1::64] = w[0::64][: w[1::64].shape[0]]
+    w = w.reshape(-1)
+    ntile = native.q4_0_device_bytes(vocab, cols, native.Q4_LAYOUT_TILED64)
+    d_rows = hip.Buffer.from_array(w)
+    d_tile = hip.Buffer(ntile)
+    native.q4_0_repack(d_rows, vocab, cols, d_tile)
+    hip.synchronize()
+    hidden = wl.host_hidden(132, B, cols)
+    hidden[0] = 0.0
+    hidden[1] = 0.0
+    hidden[2] = 0.0
+    hidden[2, 5] = 1.0
+    hidden[3] = 0.0
+    hidden[3, 0] = 0.5
+    k = np.array([64, 1, 20, 256, 64, 1000, 5, 64], np.int32)
+    t = np.array([0.7, 0.7, 1.0, 0.7, 0.7, 1.0, 0.0, 1.3], F32)
+    p = np.array([0.95, 0.95, 0.9, 0.95, 0.95, 1.0, 0.95, 0.99], F32)
+    u = wl.host_row_u(133, 0, B)
+    s = native.Sampler(vocab, max_batch=B, softcap=30.0)
+    o = _no_logits_check(orc, s, d_tile, w, hidden, t, k, p, u, "ties", capacity=1000)
+    assert o["flags"][0] & native.FLAG_ROW_RECOMPUTED, hex(o["flags"][0])
+    # the same call with the logits written gives the same outputs
+    dh = hip.Buffer.from_array(hidden)
+    dl = hip.Buffer(4 * B * vocab)
+    outs = native.DeviceOutputs(B, 1000)
+    _, ids2 = s.lmhead_sample_q4_0(d_tile, cols, dh, B, dl, _params(t, k, p), u,
+                                   outputs=outs.struct)
+    o2 = outs.read()
+    for key in ("count", "argmax"):
+        assert np.array_equal(o[key], o2[key]), key
+    assert np.array_equal(o["lsum"].view(np.uint32), o2["lsum"].view(np.uint32))
+    s.close()
+
+
+def test_fused_no_logits_rejects_full_rows(orc):
+    vocab, cols = 1000, 64
+    w = wl.host_q4_weights(141, vocab, cols)
+    ntile = native.q4_0_device_bytes(vocab, cols, native.Q4_LAYOUT_TILED64)
+    d_rows = hip.Buffer.from_array(w)
+    d_tile = hip.Buffer(ntile)
+    native.q4_0_repack(d_rows, vocab, cols, d_tile)
+    hip.synchronize()
+    s = native.Sampler(vocab, max_batch=2, softcap=30.0)
+    dh = hip.Buffer.from_array(wl.host_hidden(142, 2, cols))
+    for kk in (0, vocab, 2000):
+        params = _params([0.7, 0.7], [64, kk], [0.95, 0.95])
+        rc, _ = s.lmhead_sample_q4_0(d_tile, cols, dh, 2, None, params, [0.5, 0.5], check=False)
+        assert rc == native.G4S_ERR_INVALID_ARGUMENT, (kk, rc, s.last_error())
+    s.close()
