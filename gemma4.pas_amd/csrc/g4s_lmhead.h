@@ -53,64 +53,6 @@ __host__ __device__ __forceinline__ uint32_t gsum_row(uint64_t s) { return ((uin
 /* an upper bound of the key of every row but gsum_row's */
 __host__ __device__ __forceinline__ uint32_t gsum_bound2(uint64_t s) { return ((uint32_t)s << 6) | 63u; }
 
-/* The logit of row `lane` of TILED64 group g for the hidden vector x (cols
- * = 32 * nblk values, 16-byte aligned; LDS or global memory), in the order
- * of lmhead_tiled_kernel: one fma per term, block after block, column order
- * within a block.  One wave, lane = the group's row.  The weights are loaded
- * D blocks ahead of their use (a single chain of dependent fmas per lane
- * leaves little else to hide the loads' latency), the hidden values one
- * block ahead. */
-template <int D>
-__device__ __forceinline__ float lm_group_logit(const uint8_t* tiles, int32_t g, int32_t nblk,
-                                                const float* x)
-{
-    const uint32_t lane = threadIdx.x & 63u;
-    constexpr int kTileF = kQ4TileBytes / 4;
-    constexpr int kTileQ = kQ4TileBytes / 16;
-    const uint8_t* gt = tiles + (int64_t)g * nblk * kQ4TileBytes;
-    const float* tsc = reinterpret_cast<const float*>(gt);
-    const uint4* tq = reinterpret_cast<const uint4*>(gt + kQ4TileRows * 4);
-    float sc[D];
-    uint4 w[D];
-#pragma unroll
-    for (int i = 0; i < D; ++i) {
-        const uint32_t k = (uint32_t)(i < nblk ? i : nblk - 1);
-        sc[i] = tsc[k * kTileF + lane];
-        w[i] = tq[k * kTileQ + lane];
-    }
-    float4 xv[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) xv[c] = reinterpret_cast<const float4*>(x)[c];
-    float S = 0.0f;
-    for (int32_t k0 = 0; k0 < nblk; k0 += D) {
-#pragma unroll
-        for (int i = 0; i < D; ++i) {
-            const int32_t k = k0 + i;
-            if (k < nblk) {
-                float q[32];
-                q4_dequant32(w[i], sc[i], q);
-                const uint32_t kn = (uint32_t)(k + D < nblk ? k + D : nblk - 1);
-                sc[i] = tsc[kn * kTileF + lane];
-                w[i] = tq[kn * kTileQ + lane];
-                float4 xc[8];
-#pragma unroll
-                for (int c = 0; c < 8; ++c) xc[c] = xv[c];
-                const int32_t kx = k + 1 < nblk ? k + 1 : k;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) xv[c] = reinterpret_cast<const float4*>(x + 32 * kx)[c];
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    S = __builtin_fmaf(xc[c].x, q[4 * c], S);
-                    S = __builtin_fmaf(xc[c].y, q[4 * c + 1], S);
-                    S = __builtin_fmaf(xc[c].z, q[4 * c + 2], S);
-                    S = __builtin_fmaf(xc[c].w, q[4 * c + 3], S);
-                }
-            }
-        }
-    }
-    return S;
-}
-
 /* ROWS -> TILED64 for `rows` rows starting at a 64-row boundary of the
  * destination (dst points at the first row's tile). */
 hipError_t q4_tile_launch(const uint8_t* src_rows, int32_t rows, int32_t nblk, uint8_t* dst,

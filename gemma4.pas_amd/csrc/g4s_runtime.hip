@@ -800,14 +800,11 @@ G4S_API int g4s_generate(g4s_sampler* s, int32_t batch, const g4s_params* params
 namespace {
 
 /* The fused call without logits accepts top-k rows only (0 < TopK <=
- * kMaxTopK, TopK < vocab), at most 8192 64-row groups, and a hidden vector
- * that fits the recompute launch's LDS. */
-int check_no_logits(g4s_sampler* s, int32_t cols, int32_t batch, const g4s_params* params)
+ * kMaxTopK, TopK < vocab) and at most 8192 64-row groups. */
+int check_no_logits(g4s_sampler* s, int32_t batch, const g4s_params* params)
 {
     if ((s->vocab + 63) / 64 > 8192)
         return fail(s, G4S_ERR_UNSUPPORTED, "vocab %d above 524288 without d_logits", s->vocab);
-    if ((int64_t)cols * 4 > 65536)
-        return fail(s, G4S_ERR_UNSUPPORTED, "cols %d above 16384 without d_logits", cols);
     for (int32_t r = 0; r < batch; ++r)
         if (!is_topk_row(params[r], s->vocab) || params[r].top_k > g4s::kMaxTopK)
             return fail(s, G4S_ERR_INVALID_ARGUMENT,
@@ -880,7 +877,7 @@ G4S_API int g4s_lmhead_sample_q4_0(g4s_sampler* s, const void* d_tiles, int32_t 
     rc = check_params(s, batch, params, u, ids);
     if (rc) return rc;
     if (!d_logits) {
-        rc = check_no_logits(s, cols, batch, params);
+        rc = check_no_logits(s, batch, params);
         if (rc) return rc;
     }
     hipError_t e = g4s::lmhead_tiled_launch((const uint8_t*)d_tiles, s->vocab, cols, d_hidden,

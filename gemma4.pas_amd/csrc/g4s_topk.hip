@@ -1154,30 +1154,190 @@ __global__ __launch_bounds__(kGcBlock) void group_cand_kernel(TopkArgs a, const 
 }
 
 /* The recompute jobs of group_cand_kernel (fused LM head without logits):
- * one wave per job, the row's hidden vector staged in LDS, the group's 64
- * logits in the LM head's term order (bit-exact with the logits it did not
- * write) as candidates in the job's 64 slots; a row past the vocabulary
- * gets key 0, which the merge drops with every key below tau0. */
-constexpr int kGcWeightsAhead = 16; /* weight blocks in flight per recompute wave */
+ * one workgroup per job computes the group's 64 logits for the row's hidden
+ * vector in the LM head's term order (one fma per term, block after block,
+ * column order; bit-exact with the logits it did not write) and leaves them
+ * as candidates in the job's 64 slots; a row past the vocabulary gets key 0,
+ * which the merge drops with every key below tau0.  Each logit is one chain
+ * of dependent fmas and a single wave issues about one instruction per
+ * 2 ns, so one wave (lane = the group's row) runs the chains while three
+ * others, one per SIMD, dequantize the next blocks into LDS: per term the
+ * chain wave issues one fma and half an LDS read (the next block's reads
+ * issued before the current block's fmas), instead of the dequantization's
+ * three instructions per weight. */
+constexpr int kGlBlocks = 3;                       /* weight blocks per stage */
+constexpr int kGlStride = 36;                      /* floats per row of a staged block */
+constexpr int kGlBlockF = 64 * kGlStride + 32;     /* a staged block: weights, then x */
+constexpr int kGlAhead = 8;                        /* stages of tile loads in flight */
+constexpr int kGlProd = 192;                       /* producer threads (three waves) */
+constexpr int kGlThreads = 64 + kGlProd;
+constexpr int kGlItems = kGlBlocks * 128 / kGlProd; /* (block, row, half) items per producer */
+static_assert(kGlItems * kGlProd == kGlBlocks * 128, "whole items per producer thread");
+static_assert(8 * kGlBlocks <= kGlProd, "x staging threads");
 
-__global__ __launch_bounds__(64) void group_logits_kernel(TopkArgs a)
+template <int NST>
+__global__ __launch_bounds__(kGlThreads) void group_logits_kernel(TopkArgs a)
 {
-    extern __shared__ __align__(16) float s_x[];
+    __shared__ __align__(16) float s_w[2][kGlBlocks][kGlBlockF];
+    __shared__ float4 s_xsink[64];
     const int row = blockIdx.y, j = blockIdx.x;
     const int32_t* jobs = a.gc_jobs + (int64_t)row * kGcJobStride;
     const int njob = jobs[0];
     if (j >= njob) return;
     const int g = jobs[2 + j];
     const int base = jobs[1] + 64 * j;
-    const int cols = a.lm_cols;
-    const float4* h = reinterpret_cast<const float4*>(a.lm_hidden + (int64_t)row * cols);
-    for (int i = threadIdx.x; i < cols / 4; i += 64) reinterpret_cast<float4*>(s_x)[i] = h[i];
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const int32_t nblk = a.lm_cols / 32;
+    const int32_t nst = NST > 0 ? NST : (nblk + kGlBlocks - 1) / kGlBlocks;
+    const uint8_t* gt = a.lm_tiles + (int64_t)g * nblk * kQ4TileBytes;
+    const float* hx = a.lm_hidden + (int64_t)row * a.lm_cols;
+    /* producer thread p, item q: item i = p + q * kGlProd of the stage is
+     * block i >> 7, row (i >> 1) & 63, bytes 8 (i & 1) .. +7 of its nibbles
+     * (columns 16 (i & 1) .. +15); p < 8 * kGlBlocks also stages the x
+     * values of block p >> 3, columns 4 (p & 7) .. +3 (the others load them
+     * too, unused, so that the loads stay unconditional) */
+    const int p = tid - 64;
+    const int px = p < 8 * kGlBlocks ? p : 0;
+    float rsc[kGlAhead][kGlItems];
+    uint32_t rq0[kGlAhead][kGlItems], rq1[kGlAhead][kGlItems];
+    float rx[kGlAhead][4];
+    /* the ring slot is a template argument, so that the ring stays in
+     * registers */
+    const auto load_stage = [&]<int SLOT>(std::integral_constant<int, SLOT>, int32_t st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < kGlItems; ++q) {
+            const int it = p + q * kGlProd;
+            int32_t k = st * kGlBlocks + (it >> 7);
+            k = k < nblk ? k : nblk - 1;
+            const uint8_t* tile = gt + (int64_t)k * kQ4TileBytes;
+            rsc[SLOT][q] = reinterpret_cast<const float*>(tile)[(it >> 1) & 63];
+            const uint2 w = *reinterpret_cast<const uint2*>(tile + kQ4TileRows * 4 +
+                                                           ((it >> 1) & 63) * 16 + (it & 1) * 8);
+            rq0[SLOT][q] = w.x;
+            rq1[SLOT][q] = w.y;
+        }
+        int32_t kx = st * kGlBlocks + (px >> 3);
+        kx = kx < nblk ? kx : nblk - 1;
+        const float4 xv = reinterpret_cast<const float4*>(hx + 32 * kx)[px & 7];
+        rx[SLOT][0] = xv.x;
+        rx[SLOT][1] = xv.y;
+        rx[SLOT][2] = xv.z;
+        rx[SLOT][3] = xv.w;
+    };
+    const auto produce = [&]<int SLOT>(std::integral_constant<int, SLOT>, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < kGlItems; ++q) {
+            const int it = p + q * kGlProd;
+            const float sc = rsc[SLOT][q];
+            const float m8 = -8.0f * sc;
+            const uint32_t ws[2] = {rq0[SLOT][q], rq1[SLOT][q]};
+            float w[16];
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const uint32_t lo = ws[d] & 0x0F0F0F0Fu, hi = (ws[d] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    w[8 * d + 2 * i] = __builtin_fmaf((float)((lo >> (8 * i)) & 0xFFu), sc, m8);
+                    w[8 * d + 2 * i + 1] = __builtin_fmaf((float)((hi >> (8 * i)) & 0xFFu), sc, m8);
+                }
+            }
+            float4* dst = reinterpret_cast<float4*>(
+                &s_w[buf][it >> 7][((it >> 1) & 63) * kGlStride + (it & 1) * 16]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                dst[c] = make_float4(w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]);
+        }
+        /* every producer stores its x values: those past the stage's blocks
+         * into slots nobody reads (no branch around the ring register) */
+        float4* xd = p < 8 * kGlBlocks
+                         ? reinterpret_cast<float4*>(&s_w[buf][p >> 3][64 * kGlStride]) + (p & 7)
+                         : &s_xsink[p & 63];
+        *xd = make_float4(rx[SLOT][0], rx[SLOT][1], rx[SLOT][2], rx[SLOT][3]);
+    };
+    float S = 0.0f;
+    /* the chain over one stage; block b + 1's operands are read from LDS
+     * before block b's fmas */
+    const auto consume = [&](int32_t st, int buf) __attribute__((always_inline)) {
+        float4 w0[8], w1[8], x0[8], x1[8];
+        const auto ld = [&](int b, float4 (&wv)[8], float4 (&xv)[8]) __attribute__((always_inline)) {
+            const float4* wr = reinterpret_cast<const float4*>(&s_w[buf][b][lane * kGlStride]);
+            const float4* xr = reinterpret_cast<const float4*>(&s_w[buf][b][64 * kGlStride]);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                wv[c] = wr[c];
+                xv[c] = xr[c];
+            }
+        };
+        const auto chain = [&](const float4 (&wv)[8], const float4 (&xv)[8]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                S = __builtin_fmaf(xv[c].x, wv[c].x, S);
+                S = __builtin_fmaf(xv[c].y, wv[c].y, S);
+                S = __builtin_fmaf(xv[c].z, wv[c].z, S);
+                S = __builtin_fmaf(xv[c].w, wv[c].w, S);
+            }
+        };
+        ld(0, w0, x0);
+#pragma unroll
+        for (int b = 0; b < kGlBlocks; ++b) {
+            if (st * kGlBlocks + b < nblk) { /* uniform */
+                if (b % 2 == 0) {
+                    if (b + 1 < kGlBlocks) ld(b + 1, w1, x1);
+                    chain(w0, x0);
+                } else {
+                    if (b + 1 < kGlBlocks) ld(b + 1, w0, x0);
+                    chain(w1, x1);
+                }
+            }
+        }
+    };
+    const auto clamp_st = [&](int32_t st) __attribute__((always_inline)) { return st < nst ? st : nst - 1; };
+    /* prologue: stages 0 .. kGlAhead-1 in flight, stage 0 staged */
+    if (wid > 0) {
+        [&]<int... I>(std::integer_sequence<int, I...>) {
+            (load_stage(std::integral_constant<int, I>{}, clamp_st(I)), ...);
+        }(std::make_integer_sequence<int, kGlAhead>{});
+        produce(std::integral_constant<int, 0>{}, 0);
+        load_stage(std::integral_constant<int, 0>{}, clamp_st(kGlAhead));
+    }
     __syncthreads();
-    const float S = lm_group_logit<kGcWeightsAhead>(a.lm_tiles, g, cols / 32, s_x);
-    const int64_t idx = (int64_t)g * 64 + threadIdx.x;
-    const uint32_t key = idx < a.vocab ? cand_key(S) : 0u;
-    a.cand[(int64_t)row * kCandRow + base + threadIdx.x] = cand_pack(key, (uint32_t)idx);
+    /* stage st = s0 + I: the chain wave takes buffer st & 1 (= I & 1, s0
+     * being a multiple of kGlAhead); the producers stage st + 1 from ring
+     * slot (st + 1) mod kGlAhead into the other buffer and refill that
+     * slot with stage st + 1 + kGlAhead */
+    const auto step = [&]<int I>(std::integral_constant<int, I>, int32_t s0) __attribute__((always_inline)) {
+        const int32_t st = s0 + I;
+        if (st >= nst) return; /* uniform */
+        if (wid == 0) {
+            consume(st, I & 1);
+        } else if (st + 1 < nst) {
+            constexpr int kSlot = (I + 1) % kGlAhead;
+            produce(std::integral_constant<int, kSlot>{}, (I + 1) & 1);
+            load_stage(std::integral_constant<int, kSlot>{}, clamp_st(st + 1 + kGlAhead));
+        }
+        __syncthreads();
+    };
+    if constexpr (NST > 0) {
+        /* every stage in straight-line code: the compiler then knows which
+         * loads are still in flight at each use and waits for those only
+         * (across a loop's back edge it waits for nearly all of them) */
+        [&]<int... J>(std::integer_sequence<int, J...>) {
+            (step(std::integral_constant<int, J % kGlAhead>{}, J - J % kGlAhead), ...);
+        }(std::make_integer_sequence<int, NST>{});
+    } else {
+        for (int32_t s0 = 0; s0 < nst; s0 += kGlAhead) {
+            [&]<int... I>(std::integer_sequence<int, I...>) {
+                (step(std::integral_constant<int, I>{}, s0), ...);
+            }(std::make_integer_sequence<int, kGlAhead>{});
+        }
+    }
+    if (wid == 0) {
+        const int64_t idx = (int64_t)g * 64 + lane;
+        const uint32_t key = idx < a.vocab ? cand_key(S) : 0u;
+        a.cand[(int64_t)row * kCandRow + base + lane] = cand_pack(key, (uint32_t)idx);
+    }
 }
+static_assert(kGlAhead % 2 == 0, "buffers alternate with the unrolled stage index");
 
 /* ---------------------------------------------------------------- launch */
 
@@ -1263,8 +1423,18 @@ hipError_t topk_groups_launch(const TopkConfig& c, const TopkArgs& a, const uint
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (!a.logits) {
-        hipLaunchKernelGGL(group_logits_kernel, dim3((unsigned)kGcMaxJobs, (unsigned)a.batch),
-                           dim3(64), (size_t)a.lm_cols * sizeof(float), s, b);
+        /* straight-line instantiations for hidden sizes 1536, 2048, 2560, 3072
+         * and 4096; a loop otherwise */
+        const dim3 grid((unsigned)kGcMaxJobs, (unsigned)a.batch);
+        constexpr int kS = 32 * kGlBlocks; /* columns per stage */
+        switch ((a.lm_cols + kS - 1) / kS) {
+        case (1536 + kS - 1) / kS: hipLaunchKernelGGL(group_logits_kernel<(1536 + kS - 1) / kS>, grid, dim3(kGlThreads), 0, s, b); break;
+        case (2048 + kS - 1) / kS: hipLaunchKernelGGL(group_logits_kernel<(2048 + kS - 1) / kS>, grid, dim3(kGlThreads), 0, s, b); break;
+        case (2560 + kS - 1) / kS: hipLaunchKernelGGL(group_logits_kernel<(2560 + kS - 1) / kS>, grid, dim3(kGlThreads), 0, s, b); break;
+        case (3072 + kS - 1) / kS: hipLaunchKernelGGL(group_logits_kernel<(3072 + kS - 1) / kS>, grid, dim3(kGlThreads), 0, s, b); break;
+        case (4096 + kS - 1) / kS: hipLaunchKernelGGL(group_logits_kernel<(4096 + kS - 1) / kS>, grid, dim3(kGlThreads), 0, s, b); break;
+        default: hipLaunchKernelGGL(group_logits_kernel<0>, grid, dim3(kGlThreads), 0, s, b); break;
+        }
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
