@@ -1,6 +1,6 @@
 /*
  * g4s_decode.hip -- the top-k path for decode-sized batches on gfx950
- * (rows with 0 < TopK <= 64, up to 8 rows per launch).
+ * (rows with 0 < TopK <= 256, up to 8 rows per launch).
  *
  * Replaces DoSelectTopKIndices + the top-k branch of DoSample
  * (src/Gemma4.Model.pas:2615-2689, 2765-2826) where one token per sequence
@@ -32,11 +32,15 @@
  *      copies of tau survive, or the lowest-index rule, or (when the heap's
  *      layout decides) a replay of the reference's heap over the row.  A
  *      wave whose fourth entry reaches tau' may hold more such elements:
- *      the heap is replayed (exact for every row; slow, and reached only by
- *      rows with heavy ties);
- *    - survivors in index order, then one wave runs the reference's tail:
- *      softcap, 1/T, max, exp, sequential binary32 LSum, division, argmax,
- *      sequential running sum against fl32(u*TopP).
+ *      the merge re-reads up to 64 such waves (one wave each) and adds their
+ *      other elements >= tau'; the K-th largest key can only rise, so the
+ *      candidates are then complete (more such waves, or more candidates
+ *      than LDS holds: the heap is replayed -- exact for every row, slow,
+ *      reached only by rows with heavy ties);
+ *    - survivors in index order, then one wave runs the reference's tail
+ *      (up to four survivors per lane): softcap, 1/T, max, exp, sequential
+ *      binary32 LSum, division, argmax, sequential running sum against
+ *      fl32(u*TopP).
  * TopK = 1 needs no completeness: a wave's list starts with its lowest-index
  * copy of its maximum, so the row's first maximum is the first list head
  * with the largest key.
@@ -56,9 +60,12 @@ constexpr int kDL = kDecListLen;   /* entries per wave list */
 constexpr int kDMcap = 1024;       /* merge candidates held in LDS; heap-replay tile */
 constexpr int kDTile = kDB * 4;    /* heap-replay tile: four elements per thread */
 constexpr int kDFast = 128;        /* fast-path candidates: one per thread of two waves */
+constexpr int kDInc = 64;          /* waves whose elements the merge can re-read */
 static_assert(kDMcap >= kDTile, "replay tiles fit the candidate area");
 
+template <int KMAX>
 struct DecShared {
+    static_assert(KMAX % 32 == 0, "the tail reads eight float4 of values at a time");
     uint32_t hist[256];
     int misc[8]; /* [0..2] radix step, [3] candidate counter, [4..6] selects, [7] scratch */
     int scan[kDW];
@@ -72,11 +79,14 @@ struct DecShared {
     uint32_t gq[kDFast];      /* fast path: keys above | keys equal << 16, per candidate */
     uint32_t byidx[kDFast];   /* fast path: candidates in index order */
     float vv[kDFast];         /* fast path: each candidate's v */
-    float sv[kDecMaxK];       /* the survivors' v in index order */
-    uint64_t surv[kDecMaxK];  /* heap storage during a replay */
-    uint64_t sorted[kDecMaxK];
-    alignas(16) float val[64];
-    alignas(16) float prob[64];
+    float sv[KMAX];           /* the survivors' v in index order */
+    uint64_t surv[KMAX];      /* heap storage during a replay */
+    uint64_t sorted[KMAX];
+    alignas(16) float val[KMAX];
+    alignas(16) float prob[KMAX];
+    int ninc;                 /* waves to re-read */
+    uint32_t incw[kDInc];     /* their numbers */
+    uint64_t inc4[kDInc];     /* their lists' last entries */
 };
 
 __device__ __forceinline__ uint32_t ent_key(uint64_t e) { return (uint32_t)(e >> 32); }
@@ -114,8 +124,8 @@ __device__ __forceinline__ void load4(const char* row, int64_t e0, int64_t limit
  * inserted in index order by one lane with the reference's comparisons; the
  * next tile is loaded while one is screened.  On return hv[0..K) / hi[0..K)
  * hold the heap (hi = -1 where the row had fewer than K logits above -1e30). */
-template <int DT>
-__device__ void replay_heap(const char* row, int V, int K, DecShared& sh, float* hv, int32_t* hi)
+template <int DT, typename SH>
+__device__ void replay_heap(const char* row, int V, int K, SH& sh, float* hv, int32_t* hi)
 {
     float* qv = reinterpret_cast<float*>(sh.mc);
     int32_t* qi = reinterpret_cast<int32_t*>(sh.mc) + kDTile;
@@ -185,14 +195,62 @@ __device__ __forceinline__ uint32_t rank_below(const uint32_t* ix, int n, uint32
     return r;
 }
 
+/* The K-th largest of the M candidate keys (K <= M; every key in [lo, hi]),
+ * with the counts of keys above and equal to it.  Up to 512 keys: one wave
+ * holds them in registers and searches the bits below the prefix that lo
+ * and hi share, one ballot count per bit (the count of keys >= the trial
+ * value decides each bit).  More keys: the block's radix select. */
+template <typename SH>
+__device__ uint32_t dec_kth(int M, int K, uint32_t lo, uint32_t hi, SH& sh, int* gt, int* eq)
+{
+    if (M > 512) return select_kth<kDB>(M, K, [&](int i) { return sh.mk[i]; }, sh, gt, eq);
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64) {
+        uint32_t k[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int i = q * 64 + lane;
+            k[q] = i < M ? sh.mk[i] : 0u; /* 0: no key (every candidate key is >= 1) */
+        }
+        const uint32_t d = lo ^ hi;
+        const int top = d ? 31 - __builtin_clz(d) : -1;
+        uint32_t tau = top < 0 ? hi : (top >= 31 ? 0u : (hi & ~((2u << top) - 1u)));
+        for (int b = top; b >= 0; --b) {
+            const uint32_t t = tau | (1u << b);
+            int c = 0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) c += __popcll(__ballot(k[q] >= t));
+            if (c >= K) tau = t;
+        }
+        int g = 0, e = 0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            g += __popcll(__ballot(k[q] > tau));
+            e += __popcll(__ballot(k[q] == tau));
+        }
+        if (lane == 0) {
+            sh.misc[4] = (int)tau;
+            sh.misc[5] = g;
+            sh.misc[6] = e;
+        }
+    }
+    __syncthreads();
+    const uint32_t r = (uint32_t)sh.misc[4];
+    *gt = sh.misc[5];
+    *eq = sh.misc[6];
+    __syncthreads();
+    return r;
+}
+
 }  // namespace
 
-template <int DT>
+template <int DT, int KMAX>
 __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
 {
     constexpr int VW = Elem<DT>::VW;
     constexpr int CH = kDB * VW;
-    __shared__ DecShared sh;
+    constexpr int Q = KMAX / 64; /* survivors per lane of the tail */
+    __shared__ DecShared<KMAX> sh;
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int row = blockIdx.y;
@@ -367,15 +425,19 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
         nz += (int)sh.red[3 * kDW + w];
     }
 
-    /* L0 <= the K-th largest head (K = 1: the largest) */
+    /* L0 <= the K-th largest head (K = 1: the largest): the 8 bits of the
+     * heads below their common prefix */
     uint32_t L0 = 1u;
+    int shift = 0, above = 0;
+    uint32_t pre = 0u, dig = 0u;
+    const bool radix = nz >= K && !(K == 1 || hmax == hmin);
     if (nz >= K) {
-        if (K == 1 || hmax == hmin) {
+        if (!radix) {
             L0 = K == 1 ? hmax : hmin;
         } else {
             const int top = 31 - __builtin_clz(hmax ^ hmin);
-            const int shift = top >= 7 ? top - 7 : 0;
-            const uint32_t pre = top >= 31 ? 0u : (hmax & ~((2u << top) - 1u));
+            shift = top >= 7 ? top - 7 : 0;
+            pre = top >= 31 ? 0u : (hmax & ~((2u << top) - 1u));
 #pragma unroll
             for (int w = 0; w < kDW; ++w) {
                 const uint32_t hk = ent_key(e[w * kDL]);
@@ -384,14 +446,39 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
             __syncthreads();
             radix_digit_step(K, sh.hist, sh.misc);
             __syncthreads();
-            L0 = pre | ((uint32_t)sh.misc[0] << shift);
+            dig = (uint32_t)sh.misc[0];
+            above = sh.misc[1];
+            L0 = pre | (dig << shift);
         }
     }
     L0 = L0 < 1u ? 1u : L0;
 
     /* candidates: list entries >= L0 (each wave list's candidates are a
-     * prefix of it; only candidates are written) */
-    {
+     * prefix of it; only candidates are written).  When they overflow LDS
+     * and the bound kept low bits below the digit, a second digit of the
+     * heads inside the first one raises it, and they are compacted again. */
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) {
+            if (!(sh.misc[3] > kDMcap && radix && shift > 0)) break; /* uniform */
+            const int shift2 = shift >= 8 ? shift - 8 : 0;
+            const uint32_t hi_mask = ~((1u << shift) - 1u); /* the prefix and the first digit */
+            const uint32_t lo_mask = (1u << (shift - shift2)) - 1u;
+            __syncthreads();
+            sh.hist[tid] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int w = 0; w < kDW; ++w) {
+                const uint32_t hk = ent_key(e[w * kDL]);
+                if (hk != 0u && (hk & hi_mask) == (pre | (dig << shift)))
+                    atomicAdd(&sh.hist[(hk >> shift2) & lo_mask], 1u);
+            }
+            __syncthreads();
+            radix_digit_step(K - above, sh.hist, sh.misc);
+            __syncthreads();
+            L0 = pre | (dig << shift) | ((uint32_t)sh.misc[0] << shift2);
+            if (tid == 0) sh.misc[3] = 0;
+            __syncthreads();
+        }
         int cnt = 0;
 #pragma unroll
         for (int i = 0; i < kE; ++i) cnt += ent_key(e[i]) >= L0 ? 1 : 0;
@@ -411,13 +498,14 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
                 ++pos;
             }
         }
+        __syncthreads();
     }
     if (tid == 0) {
         sh.misc[4] = 0; /* tau of the fast path */
         sh.misc[5] = 0; /* copies of tau to split */
     }
     __syncthreads();
-    const int M = sh.misc[3];
+    int M = sh.misc[3];
     const float cap_v = a.softcap;
     const float T = rp.temperature;
     const bool scale = (T > 0.0f) && (T != 1.0f);
@@ -531,15 +619,81 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
             ordered = true;
         } else if (M > kDMcap) {
             mode = 2; /* heavy ties beyond the candidate area */
-        } else if (M < K) {
-            /* fewer than K list entries: complete when no wave list is full */
-            if (w4 != 0u) mode = 2;
-            else nsurv = M; /* every logit above -1e30 survives */
         } else {
-            int G, E;
-            tau = select_kth<kDB>(M, K, [&](int i) { return sh.mk[i]; }, sh, &G, &E);
-            if (w4 >= tau) {
-                mode = 2; /* a wave may hold elements >= tau beyond its list */
+            int G = 0, E = 0;
+            if (M >= K) tau = dec_kth(M, K, L0, hmax, sh, &G, &E);
+            /* a wave whose list ends at or above tau (fewer than K candidates:
+             * above -1e30) may hold more such elements: the merge re-reads
+             * those waves and adds the rest of their elements >= tau, after
+             * which every element >= the new tau (>= tau) is a candidate */
+            const uint32_t thr = M >= K ? tau : 1u;
+            if (w4 >= thr) { /* block-uniform */
+                if (tid == 0) sh.ninc = 0;
+                __syncthreads();
+#pragma unroll
+                for (int w = 0; w < kDW; ++w) {
+                    const uint64_t e4 = e[w * kDL + kDL - 1];
+                    if (ent_key(e4) >= thr) {
+                        const int jn = atomicAdd(&sh.ninc, 1);
+                        if (jn < kDInc) {
+                            sh.incw[jn] = (uint32_t)(tid * kDW + w);
+                            sh.inc4[jn] = e4;
+                        }
+                    }
+                }
+                __syncthreads();
+                const int ninc = sh.ninc;
+                if (ninc > kDInc) {
+                    mode = 2;
+                } else {
+                    for (int i = wid; i < ninc; i += kDW) { /* one wave per listed wave */
+                        const int gw = (int)sh.incw[i];
+                        /* the list's last entry in the sorting order of phase 1
+                         * (key, then ~index: larger = preferred) */
+                        const uint64_t e4 = (sh.inc4[i] & 0xFFFFFFFF00000000ull) |
+                                            (uint32_t)~(uint32_t)sh.inc4[i];
+                        const int64_t b0 = (int64_t)(gw / kDW) * CH + (int64_t)((gw % kDW) * 64 + lane) * VW;
+                        float v[VW];
+                        load_vec<DT>(rowp, b0, V, v);
+                        uint64_t o[VW];
+                        int cnt = 0;
+#pragma unroll
+                        for (int q = 0; q < VW; ++q) {
+                            const uint32_t k = (b0 + q < V) ? cand_key(v[q]) : 0u;
+                            o[q] = k ? (((uint64_t)k << 32) | (uint32_t)~(uint32_t)(b0 + q)) : 0ull;
+                            /* entries below the list's last are not in the list */
+                            o[q] = (k >= thr && o[q] < e4) ? o[q] : 0ull;
+                            cnt += o[q] ? 1 : 0;
+                        }
+                        const int incl = wave_inclusive_scan(cnt);
+                        int base = 0;
+                        if (lane == 63) base = atomicAdd(&sh.misc[3], incl);
+                        base = __builtin_amdgcn_readlane(base, 63);
+                        int pos = base + incl - cnt;
+#pragma unroll
+                        for (int q = 0; q < VW; ++q) {
+                            if (o[q]) {
+                                if (pos < kDMcap) {
+                                    sh.mc[pos] = o[q] ^ 0xFFFFFFFFull; /* index back */
+                                    sh.mk[pos] = ent_key(o[q]);
+                                    sh.mi[pos] = ~(uint32_t)o[q];
+                                }
+                                ++pos;
+                            }
+                        }
+                    }
+                    __syncthreads();
+                    M = sh.misc[3];
+                    if (M > kDMcap)
+                        mode = 2;
+                    else if (M >= K)
+                        tau = dec_kth(M, K, L0, hmax, sh, &G, &E);
+                }
+            }
+            if (mode == 2) {
+                /* the heap replay below */
+            } else if (M < K) {
+                nsurv = M; /* every logit above -1e30 survives */
             } else {
                 const int need = K - G;
                 nsurv = K;
@@ -575,7 +729,7 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
         if (mode == 2) {
             flags |= G4S_FLAG_HEAP_REPLAY;
             float* hv = reinterpret_cast<float*>(sh.surv);
-            int32_t* hi = reinterpret_cast<int32_t*>(sh.surv) + kDecMaxK;
+            int32_t* hi = reinterpret_cast<int32_t*>(sh.surv) + KMAX;
             replay_heap<DT>(rowp, V, K, sh, hv, hi);
             /* keep the entries holding an index (Model.pas:2668-2676), then
              * rank them by index (:2678-2688) */
@@ -591,16 +745,51 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
             ordered = true;
         }
         if (!ordered) {
-            /* survivors in index order: each ranks itself among the survivors */
+            /* survivors in index order: compacted (in any order), then each
+             * ranks itself by index among them */
             auto surv_ok = [&](int i) {
                 const uint32_t k = sh.mk[i];
                 return mode == 0 ? (k >= tau)
                                  : (k > tau || (k == tau && (int32_t)sh.mi[i] <= idx_thr));
             };
-            for (int i = tid; i < M; i += kDB) sh.ix[i] = surv_ok(i) ? sh.mi[i] : 0xFFFFFFFFu;
+            if (tid == 0) sh.misc[7] = 0;
             __syncthreads();
-            for (int i = tid; i < M; i += kDB)
-                if (surv_ok(i)) sh.sorted[rank_below(sh.ix, M, sh.mi[i])] = sh.mc[i];
+            for (int i0 = 0; i0 < M; i0 += kDB) { /* uniform */
+                const int i = i0 + tid;
+                const bool ok = i < M && surv_ok(i);
+                const uint64_t m = __ballot(ok);
+                int base = 0;
+                if (lane == 0 && m) base = atomicAdd(&sh.misc[7], __popcll(m));
+                base = __builtin_amdgcn_readfirstlane(base);
+                if (ok) {
+                    const int at = base + __popcll(m & ((1ull << lane) - 1ull));
+                    sh.ix[at] = sh.mi[i];
+                    sh.surv[at] = sh.mc[i];
+                }
+            }
+            __syncthreads();
+            const int ns = sh.misc[7]; /* == nsurv <= K */
+            if (tid < 4) sh.ix[ns + tid] = 0xFFFFFFFFu; /* rank padding */
+            __syncthreads();
+            if (tid < ns) {
+                const uint32_t mine = sh.ix[tid];
+                uint32_t r0 = 0u, r1 = 0u;
+                int j = 0;
+                for (; j + 8 <= ns + 3; j += 8) {
+                    const uint4 w0 = *reinterpret_cast<const uint4*>(sh.ix + j);
+                    const uint4 w1 = *reinterpret_cast<const uint4*>(sh.ix + j + 4);
+                    r0 += (w0.x < mine ? 1u : 0u) + (w0.y < mine ? 1u : 0u) +
+                          (w0.z < mine ? 1u : 0u) + (w0.w < mine ? 1u : 0u);
+                    r1 += (w1.x < mine ? 1u : 0u) + (w1.y < mine ? 1u : 0u) +
+                          (w1.z < mine ? 1u : 0u) + (w1.w < mine ? 1u : 0u);
+                }
+                for (; j < ns; j += 4) {
+                    const uint4 w0 = *reinterpret_cast<const uint4*>(sh.ix + j);
+                    r0 += (w0.x < mine ? 1u : 0u) + (w0.y < mine ? 1u : 0u) +
+                          (w0.z < mine ? 1u : 0u) + (w0.w < mine ? 1u : 0u);
+                }
+                sh.sorted[r0 + r1] = sh.surv[tid];
+            }
         }
         __syncthreads();
         if (wid != 0) return;
@@ -616,64 +805,101 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
         publish_done(a.done, row, a.seq);
         return;
     }
-    const bool act = lane < nsurv;
-    const uint64_t my = act ? sh.sorted[lane] : 0ull;
-    /* one survivor: e = Exp(v - v) = 1 whatever v is */
-    float vv = 0.0f;
-    if (act && nsurv > 1) vv = have_v ? sh.sv[lane] : scaled(ent_key(my));
-    const float vmax = key2f(wave_max_u32(act ? f2key(vv) : 0u));      /* :2789-2792 */
-    const float ev = !act ? 0.0f : (nsurv == 1 ? 1.0f : exp_diff_cr32(vv, vmax)); /* :2797 */
-    sh.val[lane] = ev; /* +0 beyond the survivors */
+    /* survivor j = q * 64 + lane of lane `lane` */
+    bool act[Q];
+    uint64_t my[Q];
+    float vv[Q], ev[Q], p[Q];
+    uint32_t vk = 0u;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int j = q * 64 + lane;
+        act[q] = j < nsurv;
+        my[q] = act[q] ? sh.sorted[j] : 0ull;
+        /* one survivor: e = Exp(v - v) = 1 whatever v is */
+        vv[q] = 0.0f;
+        if (act[q] && nsurv > 1) vv[q] = have_v ? sh.sv[j] : scaled(ent_key(my[q]));
+        vk = act[q] ? g4s_max_u(vk, f2key(vv[q])) : vk;
+    }
+    const float vmax = key2f(wave_max_u32(vk));                         /* :2789-2792 */
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        ev[q] = !act[q] ? 0.0f : (nsurv == 1 ? 1.0f : exp_diff_cr32(vv[q], vmax)); /* :2797 */
+        sh.val[q * 64 + lane] = ev[q]; /* +0 beyond the survivors */
+    }
     __builtin_amdgcn_wave_barrier();
     /* LSum := LSum + LVals[LI], left to right in binary32 (:2798), every lane
      * on the same broadcast LDS reads; +0 padding leaves the sum unchanged */
+    const int n4 = (nsurv + 3) >> 2; /* uniform */
     float lsum = 0.0f;
     {
+        /* eight float4 reads in flight, then their 32 additions in order */
         const float4* src = reinterpret_cast<const float4*>(sh.val);
+        for (int b4 = 0; b4 < n4; b4 += 8) {
+            float4 x[8];
 #pragma unroll
-        for (int l4 = 0; l4 < 16; ++l4) {
-            const float4 x = src[l4];
-            lsum = lsum + x.x;
-            lsum = lsum + x.y;
-            lsum = lsum + x.z;
-            lsum = lsum + x.w;
+            for (int t = 0; t < 8; ++t) x[t] = src[b4 + t]; /* KMAX / 4 is a multiple of 8 */
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                lsum = lsum + x[t].x;
+                lsum = lsum + x[t].y;
+                lsum = lsum + x[t].z;
+                lsum = lsum + x[t].w;
+            }
         }
     }
-    const float p = act ? div_cr32(ev, lsum) : 0.0f;                    /* :2800-2801 */
-    sh.prob[lane] = p;
+    uint32_t pk = 0u;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        p[q] = act[q] ? div_cr32(ev[q], lsum) : 0.0f;                   /* :2800-2801 */
+        sh.prob[q * 64 + lane] = p[q];
+        pk = act[q] ? g4s_max_u(pk, __float_as_uint(p[q])) : pk;
+    }
     /* greedy choice: the first position of the largest p (p >= 0, so its bits
      * order like the values) */
-    const uint32_t pmax = wave_max_u32(act ? __float_as_uint(p) : 0u);   /* :2804-2807 */
-    const int jarg = (int)__builtin_ctzll(__ballot(act && __float_as_uint(p) == pmax));
+    const uint32_t pmax = wave_max_u32(pk);                              /* :2804-2807 */
+    int jarg = 0;
+#pragma unroll
+    for (int q = Q - 1; q >= 0; --q) {
+        const uint64_t m = __ballot(act[q] && __float_as_uint(p[q]) == pmax);
+        if (m) jarg = q * 64 + (int)__builtin_ctzll(m);
+    }
     __builtin_amdgcn_wave_barrier();
     int chosen = jarg;
     if (T > 0.0f) {                                                     /* :2811-2824 */
         flags |= G4S_FLAG_DREW;
         const float thr = mul_u_p_cr32(u, rp.top_p);
         /* LCum := LCum + LVals[LI] left to right; every running sum goes back
-         * to LDS, then one ballot finds the first that reaches thr (a +0
-         * padding term never reaches it first) */
+         * to LDS, then ballots find the first that reaches thr */
         float cum = 0.0f;
         const float4* src = reinterpret_cast<const float4*>(sh.prob);
         float4* dst = reinterpret_cast<float4*>(sh.val);
+        for (int b4 = 0; b4 < n4; b4 += 8) {
+            float4 x[8];
 #pragma unroll
-        for (int l4 = 0; l4 < 16; ++l4) {
-            const float4 x = src[l4];
-            float4 c;
-            cum = cum + x.x;
-            c.x = cum;
-            cum = cum + x.y;
-            c.y = cum;
-            cum = cum + x.z;
-            c.z = cum;
-            cum = cum + x.w;
-            c.w = cum;
-            dst[l4] = c; /* the same value from every lane */
+            for (int t = 0; t < 8; ++t) x[t] = src[b4 + t];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                float4 c;
+                cum = cum + x[t].x;
+                c.x = cum;
+                cum = cum + x[t].y;
+                c.y = cum;
+                cum = cum + x[t].z;
+                c.z = cum;
+                cum = cum + x[t].w;
+                c.w = cum;
+                dst[b4 + t] = c; /* the same value from every lane */
+            }
         }
         __builtin_amdgcn_wave_barrier();
-        const uint64_t reach = __ballot(sh.val[lane] >= thr);
-        if (reach) {
-            chosen = (int)__builtin_ctzll(reach);
+        int first = -1;
+#pragma unroll
+        for (int q = Q - 1; q >= 0; --q) {
+            const uint64_t reach = __ballot(act[q] && sh.val[q * 64 + lane] >= thr);
+            if (reach) first = q * 64 + (int)__builtin_ctzll(reach);
+        }
+        if (first >= 0) {
+            chosen = first;
             flags |= G4S_FLAG_REACHED;
         }
     }
@@ -686,10 +912,14 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
     }
     if (a.out.indices || a.out.probs) {
         const int capn = a.out.capacity < nsurv ? a.out.capacity : nsurv;
-        if (lane < capn) {
-            if (a.out.indices)
-                a.out.indices[(int64_t)row * a.out.capacity + lane] = (int32_t)ent_idx(my);
-            if (a.out.probs) a.out.probs[(int64_t)row * a.out.capacity + lane] = p;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int j = q * 64 + lane;
+            if (j < capn) {
+                if (a.out.indices)
+                    a.out.indices[(int64_t)row * a.out.capacity + j] = (int32_t)ent_idx(my[q]);
+                if (a.out.probs) a.out.probs[(int64_t)row * a.out.capacity + j] = p[q];
+            }
         }
     }
     publish_done(a.done, row, a.seq);
@@ -697,7 +927,7 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
 
 bool decode_eligible(const TopkArgs& a, int dtype)
 {
-    if (!a.dec_tickets || a.batch < 1 || a.batch > kDecMaxRows) return false;
+    if (!a.dec_tickets || a.batch < 1 || a.batch > a.dec_rows) return false;
     if (a.kbound < 1 || a.kbound > kDecMaxK) return false;
     const int64_t ch = (int64_t)kDB * (dtype == G4S_DTYPE_F32 ? 4 : 8);
     return (a.vocab + ch - 1) / ch <= kDecMaxChunks;
@@ -707,10 +937,19 @@ hipError_t decode_launch(const TopkArgs& a, int dtype, hipStream_t s)
 {
     const int64_t ch = (int64_t)kDB * (dtype == G4S_DTYPE_F32 ? 4 : 8);
     const dim3 grid((unsigned)((a.vocab + ch - 1) / ch), (unsigned)a.batch);
-    if (dtype == G4S_DTYPE_F32)
-        hipLaunchKernelGGL(topk_decode_kernel<0>, grid, dim3(kDB), 0, s, a);
-    else
-        hipLaunchKernelGGL(topk_decode_kernel<1>, grid, dim3(kDB), 0, s, a);
+    /* LDS (and so the resident workgroups of the row pass) sized by the K bound */
+    const bool small = a.kbound <= kDecSmallK;
+    if (dtype == G4S_DTYPE_F32) {
+        if (small)
+            hipLaunchKernelGGL((topk_decode_kernel<0, kDecSmallK>), grid, dim3(kDB), 0, s, a);
+        else
+            hipLaunchKernelGGL((topk_decode_kernel<0, kDecMaxK>), grid, dim3(kDB), 0, s, a);
+    } else {
+        if (small)
+            hipLaunchKernelGGL((topk_decode_kernel<1, kDecSmallK>), grid, dim3(kDB), 0, s, a);
+        else
+            hipLaunchKernelGGL((topk_decode_kernel<1, kDecMaxK>), grid, dim3(kDB), 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -1340,15 +1340,16 @@ __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
         bc[cb] = beta;
     }
     if (lane == 0) {
-        FullRow w = r;
-        w.lsum = lsum;
-        w.inv = inv;
-        w.thr = thr;
-        w.argmax = argmax;
-        w.c_last = clast;
-        w.nodraw = nodraw ? 1 : (direct ? 2 : 0);
-        w.l_rounds = rounds;
-        a.ws.rows[row] = w;
+        /* the fields this chain decides (the record itself is not held in
+         * registers through the walk) */
+        FullRow* w = &a.ws.rows[row];
+        w->lsum = lsum;
+        w->inv = inv;
+        w->thr = thr;
+        w->argmax = argmax;
+        w->c_last = clast;
+        w->nodraw = nodraw ? 1 : (direct ? 2 : 0);
+        w->l_rounds = rounds;
         a.ws.fbrow[row].nsc = nstaged < kBfStage ? nstaged : kBfStage;
     }
 }

@@ -41,7 +41,8 @@ constexpr size_t kMergeOff = kCandOff + (size_t)kRows * kCandRow * sizeof(uint64
 constexpr size_t kRecsOff = kMergeOff + (size_t)kRows * kCandRow * sizeof(uint64_t);
 constexpr size_t kWbOff = kRecsOff + (size_t)kRows * kMaxSplits * sizeof(ChunkRec);
 constexpr size_t kDecTicketsOff = kWbOff + (size_t)kRows * kWaveBounds * sizeof(uint32_t);
-constexpr int kDecWords = kDecMaxRows * kDecTicketWords;
+constexpr int kDecRows = kRows < kDecMaxBatch ? kRows : kDecMaxBatch;
+constexpr int kDecWords = kDecRows * kDecTicketWords;
 constexpr size_t kBytes = kDecTicketsOff + (size_t)kDecWords * sizeof(uint32_t);
 static_assert(kRows * sizeof(uint32_t) <= kCandOff, "tickets before the candidates");
 static_assert(kDecTicketsOff % 256 == 0, "aligned sections");
@@ -178,6 +179,7 @@ G4S_API int g4s_sample_topk_noalloc(const void* d_logits, int32_t dtype, int32_t
     a.wbounds = reinterpret_cast<uint32_t*>(base + kWbOff);
     a.tickets = reinterpret_cast<uint32_t*>(base + kTicketsOff);
     a.dec_tickets = reinterpret_cast<uint32_t*>(base + kDecTicketsOff);
+    a.dec_rows = kDecRows;
     a.ids = d_ids;
     a.done = nullptr;
     a.seq = 0;

@@ -70,7 +70,8 @@ struct g4s_sampler {
     g4s::ChunkRec* recs = nullptr;
     uint32_t* wbounds = nullptr;
     uint32_t* tickets = nullptr;
-    uint32_t* dec_tickets = nullptr; /* [min(max_batch, kDecMaxRows)][kDecTicketWords] */
+    uint32_t* dec_tickets = nullptr; /* [dec_rows][kDecTicketWords] */
+    int32_t dec_rows = 0;            /* min(max_batch, kDecMaxBatch) */
     uint64_t* gsum = nullptr;     /* [max_batch][ceil(vocab/64)] LM-head group summaries */
     int32_t* gc_jobs = nullptr;   /* [max_batch][kGcJobStride] group recompute jobs */
     float* row_logits = nullptr;  /* one row of logits for a recomputed row (allocated by
@@ -220,6 +221,7 @@ int enqueue(g4s_sampler* s, const void* d_logits, int32_t dtype, int64_t row_str
         a.wbounds = s->wbounds;
         a.tickets = s->tickets;
         a.dec_tickets = s->dec_tickets;
+        a.dec_rows = s->dec_rows;
         if (lm) {
             a.lm_tiles = lm->tiles;
             a.lm_hidden = lm->hidden;
@@ -339,7 +341,8 @@ G4S_API int g4s_create(g4s_sampler** out, int32_t vocab, int32_t max_batch, floa
     dm((void**)&s->recs, mb * g4s::kMaxSplits * sizeof(g4s::ChunkRec));
     dm((void**)&s->wbounds, mb * g4s::kWaveBounds * sizeof(uint32_t));
     dm((void**)&s->tickets, mb * sizeof(uint32_t));
-    const size_t dec_rows = mb < (size_t)g4s::kDecMaxRows ? mb : (size_t)g4s::kDecMaxRows;
+    const size_t dec_rows = mb < (size_t)g4s::kDecMaxBatch ? mb : (size_t)g4s::kDecMaxBatch;
+    s->dec_rows = (int32_t)dec_rows;
     dm((void**)&s->dec_tickets, dec_rows * g4s::kDecTicketWords * sizeof(uint32_t));
     dm((void**)&s->gsum, mb * (size_t)((vocab + 63) / 64) * sizeof(uint64_t));
     dm((void**)&s->gc_jobs, mb * g4s::kGcJobStride * sizeof(int32_t));

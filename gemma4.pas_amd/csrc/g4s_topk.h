@@ -10,12 +10,16 @@ namespace g4s {
 
 constexpr int kWaveBounds = 512; /* per-wave bounds kept per row (splits * waves) */
 
-/* The decode-sized launch (g4s_decode.hip): batches of up to kDecMaxRows rows
- * whose TopK bound is at most kDecMaxK, on vocabularies of at most
- * kDecMaxChunks 16-byte-per-thread workgroup chunks (262144 binary32 logits,
- * 524288 bf16). */
-constexpr int kDecMaxRows = 8;
-constexpr int kDecMaxK = 64;
+/* The decode-sized launch (g4s_decode.hip): batches of up to kDecMaxBatch
+ * rows (as many as the handle's election counters hold) whose TopK bound is
+ * at most kDecMaxK, on vocabularies of at most kDecMaxChunks
+ * 16-byte-per-thread workgroup chunks (262144 binary32 logits, 524288 bf16).
+ * K bounds up to kDecSmallK take an instantiation with less LDS.  (Larger
+ * batches take the chunked launch: screening a row into 1024 wave lists
+ * costs more instructions per logit than the chunk workgroups' bounds.) */
+constexpr int kDecMaxBatch = 8;
+constexpr int kDecMaxK = 256;
+constexpr int kDecSmallK = 64;
 constexpr int kDecBlock = 256;                 /* threads per workgroup */
 constexpr int kDecMaxChunks = 256;             /* workgroups per row */
 constexpr int kDecListLen = 4;                 /* entries per wave list */
@@ -80,8 +84,9 @@ struct TopkArgs {
     uint32_t* done;    /* [batch] host-pinned completion words, or NULL */
     uint32_t seq;      /* value written to done[row] once the row's outputs are visible */
     g4s_outputs out;
-    uint32_t* dec_tickets; /* [batch][kDecTicketWords] election counters of the decode
+    uint32_t* dec_tickets; /* [dec_rows][kDecTicketWords] election counters of the decode
                               launch, zero between launches; NULL: no decode launch */
+    int32_t dec_rows;      /* rows dec_tickets holds (the decode launch's batch bound) */
     /* the fused LM head without logits (logits == NULL): its TILED64
      * weights, hidden vectors [batch][lm_cols] and the recompute jobs
      * [batch][kGcJobStride] */

@@ -1,13 +1,14 @@
 """GPU parity of the decode-sized top-k launch (batches of up to 8 rows with
-TopK <= 64, csrc/g4s_decode.hip) against the CPU oracle through the C ABI:
+TopK <= 256, csrc/g4s_decode.hip) against the CPU oracle through the C ABI:
 token ids, survivor index sets, probabilities (bit-exact; the stated
 tolerance is 1e-6 relative), LSum and the greedy id.  The launch's merge is
-exact only when every wave list is complete below the K-th key, so rows are
-built to reach each of its branches: no ties, lowest-index ties, heap-layout
-ties, a wave holding more than four of the top K, rows with fewer valid
-logits than K, and K = 1 with planted copies of the maximum.  A batch of nine
-rows takes the chunked launch (g4s_topk.hip); both launches must agree on
-every output.
+exact only when every wave list is complete below the K-th key, or made
+complete by re-reading the waves whose lists reach it, so rows are built to
+reach each of its branches: no ties, lowest-index ties, heap-layout ties,
+waves holding more than four of the top K (re-read), more such waves than
+the merge re-reads (heap replay), rows with fewer valid logits than K, and
+K = 1 with planted copies of the maximum.  A batch of more than 8 rows takes
+the chunked launch (g4s_topk.hip); both launches must agree on every output.
 """
 import numpy as np
 import pytest
@@ -109,32 +110,34 @@ def test_decode_full_size_regimes(orc):
     check_rows(orc, rows, t, k, p, u, ids, o, label="decode regimes")
     assert o["flags"][5] & native.FLAG_TIE_LOWEST
     assert o["flags"][7] & native.FLAG_TIE_LOWEST
-    for r in (0, 1, 2, 4):  # wave lists incomplete below the K-th key
+    for r in (0, 1, 2):  # every wave list incomplete below the K-th key
         assert o["flags"][r] & native.FLAG_HEAP_REPLAY, (r, hex(o["flags"][r]))
-    for r in (3, 6):
+    # row 4: one wave holds six of the top K -- re-read, no replay
+    for r in (3, 4, 6):
         assert not (o["flags"][r] & (native.FLAG_HEAP_REPLAY | native.FLAG_TIE_LOWEST)), r
     s.close()
 
 
 def test_decode_and_chunked_launches_agree(orc):
     """The same eight rows once as a batch of eight (the decode-sized launch)
-    and once inside a batch of nine (the chunked launch): every output equal
-    (flags may name a different resolution of the same ties)."""
+    and once at the head of a batch of 65 (the chunked launch): every output
+    equal (flags may name a different resolution of the same ties)."""
     rng = np.random.default_rng(92)
     rows = _full_size_rows(rng)
     t = np.array([0.7, 1.0, 0.5, 0.7, 1.0, 0.0, 0.9, 0.8], F32)
     k = np.array([64, 64, 20, 64, 64, 1, 64, 20], np.int32)
     p = np.array([0.95, 0.9, 0.8, 0.95, 0.99, 0.95, 0.9, 0.97], F32)
     u = np.array([0.5, 0.25, 0.125, 0.75, 0.875, 0.0, 0.3, 0.6])
-    s = native.Sampler(V, max_batch=9, softcap=CAP)
+    s = native.Sampler(V, max_batch=65, softcap=CAP)
     _, ids8, o8 = _sample(s, rows, t, k, p, u)
-    rows9 = np.concatenate([rows, rows[3:4]])
-    _, ids9, o9 = _sample(s, rows9, np.append(t, t[3]), np.append(k, k[3]), np.append(p, p[3]),
-                          np.append(u, u[3]))
+    n = 65
+    rep = np.arange(n) % 8
+    _, ids9, o9 = _sample(s, rows[rep], t[rep], k[rep], p[rep], u[rep])
     assert np.array_equal(ids8, ids9[:8])
     for key in ("count", "argmax"):
         assert np.array_equal(o8[key], o9[key][:8]), key
     assert np.array_equal(o8["lsum"].view(np.uint32), o9["lsum"][:8].view(np.uint32))
+    assert np.array_equal(ids9[8:], ids9[rep[8:]])
     for r in range(8):
         n = int(o8["count"][r])
         assert np.array_equal(o8["indices"][r][:n], o9["indices"][r][:n]), r
@@ -176,4 +179,65 @@ def test_decode_stream_rows(orc):
         want, _, _, _ = orc.do_sample(rows[r], 0.7, kk, 0.95, float(u[r]), softcap=CAP,
                                       want_probs=False)
         assert got[r] == want, (r, got[r], want)
+    s.close()
+
+
+def _wide_wave_rows(rng, n):
+    """N(0, 1) rows with groups of large values planted inside single waves
+    of 256 logits (the lists hold four per wave): row r plants r % 4 + 1
+    groups of 5-12 values above 6, so the K-th largest key of K >= 20 lies
+    among them or below."""
+    rows = rng.normal(0, 1, (n, V)).astype(F32)
+    for r in range(n):
+        for _ in range(r % 4 + 1):
+            w = int(rng.integers(0, V // 256))
+            m = int(rng.integers(5, 13))
+            pos = w * 256 + rng.choice(256, m, replace=False)
+            rows[r, pos] = rng.uniform(6, 9, m).astype(F32)
+    return rows
+
+
+@pytest.mark.parametrize("B", [4, 8])
+def test_decode_large_k_and_rereads(orc, B):
+    """K up to 256: peaky rows, and rows whose large values crowd single
+    waves so that the merge re-reads them; every output against the
+    oracle."""
+    rng = np.random.default_rng(93 + B)
+    half = B // 2
+    rows = np.concatenate([wl.host_peaky_rows(20261206, 0, B - half, V),
+                           _wide_wave_rows(rng, half)])
+    t, k, p = wl.host_mixed_params(20261206, 0, B)
+    k = np.array([(1, 20, 64, 256, 200, 130)[r % 6] for r in range(B)], np.int32)
+    u = wl.host_row_u(20261206, 0, B)
+    s = native.Sampler(V, max_batch=B, softcap=CAP)
+    d = hip.Buffer.from_array(rows)
+    outs = native.DeviceOutputs(B, 256)
+    rc, ids = s.sample(d, B, _params(t, k, p), u, outputs=outs.struct)
+    assert rc == 0, s.last_error()
+    o = outs.read()
+    check_rows(orc, rows, t, k, p, u, ids, o, label=f"B={B} large K")
+    assert not np.any(o["flags"] & native.FLAG_HEAP_REPLAY), o["flags"]
+    s.close()
+
+
+def test_mixed_benchmark_batch(orc):
+    """The mixed-settings benchmark batch (64 peaky rows, K in {1, 20, 64,
+    256}, launched with k_bound 256: the chunked launch) through the
+    stream-ordered entry point: ids against the oracle's."""
+    B = 64
+    rows = wl.host_peaky_rows(20261207, 0, B, V)
+    t, k, p = wl.host_mixed_params(20261207, 0, B)
+    u = wl.host_row_u(20261207, 0, B)
+    s = native.Sampler(V, max_batch=B, softcap=CAP)
+    d = hip.Buffer.from_array(rows)
+    parr = native.params_array(_params(t, k, p))
+    dp = hip.Buffer(16 * B)
+    hip.check(hip.lib().hipMemcpy(dp.ptr, parr, 16 * B, hip.H2D))
+    du = hip.Buffer.from_array(np.asarray(u, np.float64))
+    di = hip.Buffer(4 * B)
+    s.sample_async(d, B, dp, du, 256, 0, di)
+    hip.synchronize()
+    ids = di.download(np.int32)
+    want = orc.sample_batch(rows, 0, V, V, (t, k, p), u, softcap=CAP, threads=16)
+    assert np.array_equal(ids, want), (np.nonzero(ids != want), ids, want)
     s.close()

@@ -118,11 +118,12 @@ def test_mixed_batch(big, orc):
     print(f"mixed batch: boundary draws {nb}")
 
 
-@pytest.mark.parametrize("B", [16, 17, 40])
+@pytest.mark.parametrize("B", [16, 40, 65, 80])
 def test_batch_launch_modes(big, orc, B):
-    """K <= 64 batches on both sides of the merge-launch split: 16 rows of 32
-    chunk workgroups fit the device at once (one launch, last-workgroup
-    merges); 17 and 40 rows do not (a chunk launch, then a merge launch)."""
+    """K <= 64 batches of the chunked launch on both sides of its merge-launch
+    split: 16 rows of 32 chunk workgroups fit the device at once (one launch,
+    last-workgroup merges); 40, 65 and 80 rows do not (a chunk launch, then a
+    merge launch)."""
     rows = wl.host_peaky_rows(SEED + 7, 0, B, V)
     ks = [1, 7, 33, 64]
     k = np.array([ks[r % 4] for r in range(B)], np.int32)
@@ -131,8 +132,11 @@ def test_batch_launch_modes(big, orc, B):
     u = wl.host_row_u(SEED + 7, 0, B)
     d = hip.Buffer.from_array(rows)
     outs = native.DeviceOutputs(B, 64)
-    _, ids = big.sample(d, B, _params(t, k, p), u, outputs=outs.struct)
+    s = big if B <= 64 else native.Sampler(V, max_batch=B, softcap=CAP)  # big holds 64 rows
+    _, ids = s.sample(d, B, _params(t, k, p), u, outputs=outs.struct)
     check_rows(orc, rows, t, k, p, u, ids, outs.read(), label=f"B={B}")
+    if s is not big:
+        s.close()
 
 
 def test_async_matches_sync(big, orc):
@@ -218,8 +222,10 @@ def test_heap_tie_counterexample(orc):
 
 def test_full_size_tie_regimes(big, orc):
     """Full-size rows whose K-th value is massively tied: all-equal rows
-    (exact per-chunk select, lowest-index rule), 0/1 rows with late 2s (heap
-    replay), and bf16-valued rows."""
+    (chunked launch: exact per-chunk select, lowest-index rule; decode-sized
+    launch: every wave list incomplete, heap replay), 0/1 rows with late 2s
+    (heap replay), and bf16-valued rows -- as a batch of 4 (the decode-sized
+    launch) and at the head of a batch of 65 (the chunked launch)."""
     rng = np.random.default_rng(77)
     rows = np.zeros((4, V), F32)
     rows[1] = rng.integers(0, 2, V)
@@ -236,8 +242,21 @@ def test_full_size_tie_regimes(big, orc):
     _, ids = big.sample(d, 4, _params(t, k, p), u, outputs=outs.struct)
     o = outs.read()
     check_rows(orc, rows, t, k, p, u, ids, o, label="ties")
+    assert o["flags"][0] & native.FLAG_HEAP_REPLAY
+    assert o["flags"][3] & native.FLAG_HEAP_REPLAY
+    n = 65
+    rep = np.arange(n) % 4
+    s = native.Sampler(V, max_batch=n, softcap=CAP)
+    d65 = hip.Buffer.from_array(rows[rep])
+    outs = native.DeviceOutputs(n, 256)
+    _, ids65 = s.sample(d65, n, _params(t[rep], k[rep], p[rep]), u[rep], outputs=outs.struct)
+    o = outs.read()
+    assert np.array_equal(ids65, ids[rep]), (ids65, ids)
+    sub = {key: (val[:4] if hasattr(val, "__len__") else val) for key, val in o.items()}
+    check_rows(orc, rows, t, k, p, u, ids65[:4], sub, label="ties (chunked)")
     assert o["flags"][0] & native.FLAG_TIE_LOWEST
     assert o["flags"][3] & native.FLAG_HEAP_REPLAY
+    s.close()
 
 
 def test_bf16_logits_topk(orc):
