@@ -457,6 +457,10 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
      * prefix of it; only candidates are written).  When they overflow LDS
      * and the bound kept low bits below the digit, a second digit of the
      * heads inside the first one raises it, and they are compacted again. */
+    if (tid == 0) {
+        sh.misc[4] = 0; /* tau of the fast path */
+        sh.misc[5] = 0; /* copies of tau to split */
+    }
     for (int pass = 0; pass < 2; ++pass) {
         if (pass == 1) {
             if (!(sh.misc[3] > kDMcap && radix && shift > 0)) break; /* uniform */
@@ -500,11 +504,6 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
         }
         __syncthreads();
     }
-    if (tid == 0) {
-        sh.misc[4] = 0; /* tau of the fast path */
-        sh.misc[5] = 0; /* copies of tau to split */
-    }
-    __syncthreads();
     int M = sh.misc[3];
     const float cap_v = a.softcap;
     const float T = rp.temperature;
