@@ -139,6 +139,40 @@ def test_batch_launch_modes(big, orc, B):
         s.close()
 
 
+@pytest.mark.parametrize("dtype,vocab,B", [(native.DTYPE_F32, 100000, 72),
+                                           (native.DTYPE_BF16, V, 40)])
+def test_chunked_two_launch_large_k(orc, dtype, vocab, B):
+    """Batches whose K bound lies in 65..256 and whose chunk workgroups do not
+    fit the device at once take a chunk launch and then a merge launch of the
+    1024 x 32 shape: fp32 rows of a vocabulary that ends in a partial chunk,
+    and bf16 rows.  Rows 0 and 1 are massively tied (all equal; 0/1 with a
+    few 2s), so their chunks hold more candidates than slots and take the
+    exact per-chunk select; the others are ordinary rows with K in
+    {1, 20, 64, 256}."""
+    rng = np.random.default_rng(vocab + B)
+    if dtype == native.DTYPE_F32:
+        rows = wl.host_peaky_rows(SEED + 11, 0, B, vocab)
+    else:
+        rows = (wl.host_flat_bf16_rows(SEED + 11, 0, B, vocab).astype(np.uint32) << 16).view(F32)
+    rows[0] = 0.25
+    rows[1] = rng.integers(0, 2, vocab)
+    rows[1][rng.choice(vocab, 7, replace=False)] = 2.0
+    ks = [256, 200, 1, 20, 64, 256]
+    k = np.array([ks[r] if r < 2 else ks[2 + r % 4] for r in range(B)], np.int32)
+    t = np.array([(0.7, 1.0, 1.3)[r % 3] for r in range(B)], F32)
+    p = np.array([(0.9, 0.95, 1.0)[r % 3] for r in range(B)], F32)
+    u = wl.host_row_u(SEED + 11, 0, B)
+    host = rows if dtype == native.DTYPE_F32 else (rows.view(np.uint32) >> 16).astype(np.uint16)
+    d = hip.Buffer.from_array(np.ascontiguousarray(host))
+    s = native.Sampler(vocab, max_batch=B, softcap=CAP)
+    outs = native.DeviceOutputs(B, 256)
+    _, ids = s.sample(d, B, _params(t, k, p), u, dtype=dtype, outputs=outs.struct)
+    o = outs.read()
+    check_rows(orc, rows, t, k, p, u, ids, o, label=f"two launches dtype={dtype}")
+    assert o["flags"][0] & native.FLAG_TIE_LOWEST
+    s.close()
+
+
 def test_async_matches_sync(big, orc):
     B = 16
     rows = wl.host_peaky_rows(SEED + 2, 0, B, V)
