@@ -171,6 +171,68 @@ __device__ __forceinline__ bool wave_fast_select(const uint64_t* mc, int M, int 
 }
 
 
+/* The K-th largest key tau of the M <= BLOCK candidates in LDS (K < M),
+ * over the whole workgroup: 8-bit MSD radix passes over the bits below the
+ * keys' common prefix only (every candidate key is >= 1), one candidate
+ * per thread.  When exactly K candidates are >= tau they are the survivors:
+ * written to surv (any order) and true is returned; otherwise false. */
+template <int BLOCK, typename SH>
+__device__ __forceinline__ bool block_fast_select(SH& sh, int M, int K, uint64_t* surv)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    constexpr int NW = BLOCK / 64;
+    const uint64_t c = tid < M ? sh.mc[tid] : 0ull;
+    const uint32_t k = cand_key_of(c);
+    const uint32_t hw = wave_max_u32(k), lw = wave_min_u32(tid < M ? k : 0xFFFFFFFFu);
+    if (lane == 0) {
+        sh.red[wid] = hw;
+        sh.red[NW + wid] = lw;
+    }
+    __syncthreads();
+    uint32_t hi = 0u, lo = 0xFFFFFFFFu;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        hi = g4s_max_u(hi, sh.red[w]);
+        lo = g4s_min_u(lo, sh.red[NW + w]);
+    }
+    uint32_t tau;
+    int G = 0, E;
+    if (hi == lo) {
+        tau = hi;
+        E = M;
+    } else {
+        int top = 31 - __builtin_clz(hi ^ lo);
+        uint32_t prefix = top >= 31 ? 0u : (hi & ~((2u << top) - 1u));
+        uint32_t mask = top >= 31 ? 0u : ~((2u << top) - 1u);
+        int kk = K;
+        E = 0;
+        for (;;) {
+            const int shift = top >= 7 ? top - 7 : 0;
+            for (int b = tid; b < 256; b += BLOCK) sh.hist[b] = 0u;
+            __syncthreads();
+            if (tid < M && (k & mask) == prefix) atomicAdd(&sh.hist[(k >> shift) & 255u], 1u);
+            __syncthreads();
+            radix_digit_step(kk, sh.hist, sh.misc + 4);
+            __syncthreads();
+            G += sh.misc[5];
+            E = sh.misc[6];
+            kk -= sh.misc[5];
+            prefix |= (uint32_t)sh.misc[4] << shift;
+            mask |= ((top - shift == 31) ? 0xFFFFFFFFu : ((2u << (top - shift)) - 1u)) << shift;
+            if (shift == 0) break;
+            top = shift - 1;
+            __syncthreads(); /* the digit step's words are read before the next pass */
+        }
+        tau = prefix;
+    }
+    if (E != K - G) return false; /* uniform */
+    int tot;
+    const bool keep = tid < M && k >= tau;
+    const int pos = block_exclusive_scan<BLOCK>(keep ? 1 : 0, sh.scan, tot);
+    if (keep) surv[pos] = c;
+    return true;
+}
+
 }  // namespace
 
 template <int BLOCK, int ITEMS, int DT, int KCAP>
@@ -636,15 +698,18 @@ __global__ __launch_bounds__(BLOCK) void topk_kernel(TopkArgs a)
         if (M <= K) {
             for (int i = tid; i < M; i += BLOCK) sh.surv[i] = sh.mc[i];
             nsurv = M;
-        } else if (M <= 512 && M <= MCAP) {
+        } else if (M <= 128 && M <= MCAP) {
             if (wid == 0) {
-                const bool fast = M <= 128   ? wave_fast_select<2>(sh.mc, M, K, sh.surv)
-                                  : M <= 256 ? wave_fast_select<4>(sh.mc, M, K, sh.surv)
-                                             : wave_fast_select<8>(sh.mc, M, K, sh.surv);
+                const bool fast = wave_fast_select<2>(sh.mc, M, K, sh.surv);
                 if (lane == 0) sh.misc[5] = fast ? 0 : 1;
             }
             __syncthreads();
             general = sh.misc[5] != 0;
+            if (!general) nsurv = K;
+        } else if (M <= 512 && M <= MCAP && M <= BLOCK) {
+            /* the whole workgroup's radix select (one wave's ballot search
+             * over 4-8 keys per lane takes longer) */
+            general = !block_fast_select<BLOCK>(sh, M, K, sh.surv);
             if (!general) nsurv = K;
         } else {
             general = true;
