@@ -76,8 +76,6 @@ struct DecShared {
     alignas(16) uint32_t mk[kDMcap];      /* the candidates' keys */
     alignas(16) uint32_t mi[kDMcap];      /* the candidates' indices */
     alignas(16) uint32_t ix[kDMcap];      /* survivor indices for the index ranking (else ~0) */
-    uint32_t gq[kDFast];      /* fast path: keys above | keys equal << 16, per candidate */
-    uint32_t byidx[kDFast];   /* fast path: candidates in index order */
     float vv[kDFast];         /* fast path: each candidate's v */
     float sv[KMAX];           /* the survivors' v in index order */
     uint64_t surv[KMAX];      /* heap storage during a replay */
@@ -483,25 +481,38 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
             if (tid == 0) sh.misc[3] = 0;
             __syncthreads();
         }
+        /* in index order: thread t holds workgroup t's lists, wave by wave,
+         * and a wave's elements precede the next wave's; inside one list an
+         * entry's place is its index rank among the list's candidates */
         int cnt = 0;
 #pragma unroll
         for (int i = 0; i < kE; ++i) cnt += ent_key(e[i]) >= L0 ? 1 : 0;
-        const int incl = wave_inclusive_scan(cnt);
-        int base = 0;
-        if (lane == 63) base = atomicAdd(&sh.misc[3], incl);
-        base = __builtin_amdgcn_readlane(base, 63);
-        int pos = base + incl - cnt;
+        int total;
+        int pos = block_exclusive_scan<kDB>(cnt, sh.scan, total);
 #pragma unroll
-        for (int i = 0; i < kE; ++i) {
-            if (ent_key(e[i]) >= L0) {
-                if (pos < kDMcap) {
-                    sh.mc[pos] = e[i];
-                    sh.mk[pos] = ent_key(e[i]);
-                    sh.mi[pos] = ent_idx(e[i]);
+        for (int w = 0; w < kDW; ++w) {
+            int cw = 0;
+#pragma unroll
+            for (int l = 0; l < kDL; ++l) {
+                const uint64_t x = e[w * kDL + l];
+                if (ent_key(x) >= L0) {
+                    int r = 0;
+#pragma unroll
+                    for (int l2 = 0; l2 < kDL; ++l2) {
+                        const uint64_t y = e[w * kDL + l2];
+                        r += (l2 != l && ent_key(y) >= L0 && ent_idx(y) < ent_idx(x)) ? 1 : 0;
+                    }
+                    if (pos + r < kDMcap) {
+                        sh.mc[pos + r] = x;
+                        sh.mk[pos + r] = ent_key(x);
+                        sh.mi[pos + r] = ent_idx(x);
+                    }
+                    ++cw;
                 }
-                ++pos;
             }
+            pos += cw;
         }
+        if (tid == 0) sh.misc[3] = total;
         __syncthreads();
     }
     int M = sh.misc[3];
@@ -521,65 +532,50 @@ __global__ __launch_bounds__(kDB) void topk_decode_kernel(TopkArgs a)
     int nsurv = 0;
     bool have_v = false;
     if (K >= 2 && M >= K && M <= kDFast) {
-        /* fast path, two halves at once: waves 0-1 rank each candidate (keys
-         * above and equal to it, indices below it), waves 2-3 compute every
-         * candidate's v.  With no copies of the K-th key tau to split and no
-         * wave list reaching tau, the K candidates >= tau are the survivors
-         * and their v are ready. */
-        if (wid < 2) {
-            const int c = tid;
-            if (c < M) {
-                const uint32_t kc = sh.mk[c], ic = sh.mi[c];
-                uint32_t g = 0u, q = 0u, r = 0u;
-                int j = 0;
-                for (; j + 4 <= M; j += 4) {
-                    const uint4 kw = *reinterpret_cast<const uint4*>(sh.mk + j);
-                    const uint4 iw = *reinterpret_cast<const uint4*>(sh.mi + j);
-                    g += (kw.x > kc ? 1u : 0u) + (kw.y > kc ? 1u : 0u) + (kw.z > kc ? 1u : 0u) +
-                         (kw.w > kc ? 1u : 0u);
-                    q += (kw.x == kc ? 1u : 0u) + (kw.y == kc ? 1u : 0u) +
-                         (kw.z == kc ? 1u : 0u) + (kw.w == kc ? 1u : 0u);
-                    r += (iw.x < ic ? 1u : 0u) + (iw.y < ic ? 1u : 0u) + (iw.z < ic ? 1u : 0u) +
-                         (iw.w < ic ? 1u : 0u);
-                }
-                for (; j < M; ++j) {
-                    const uint32_t kj = sh.mk[j];
-                    g += kj > kc ? 1u : 0u;
-                    q += kj == kc ? 1u : 0u;
-                    r += sh.mi[j] < ic ? 1u : 0u;
-                }
-                sh.gq[c] = g | (q << 16);
-                sh.byidx[r] = (uint32_t)c;
-                const uint32_t Ku = (uint32_t)K;
-                if (g < Ku && Ku <= g + q) sh.misc[4] = (int)kc; /* all writers agree */
-                if (g < Ku && g + q > Ku) sh.misc[5] = 1;
+        /* fast path: wave 0 finds the K-th largest key tau of the candidates
+         * (a ballot search, two keys per lane) while waves 2-3 compute every
+         * candidate's v.  With no copies of tau to split and no wave list
+         * reaching tau, the K candidates >= tau are the survivors, already in
+         * index order, and their v are ready. */
+        if (wid == 0) {
+            const uint32_t k0 = lane < M ? sh.mk[lane] : 0u;
+            const uint32_t k1 = lane + 64 < M ? sh.mk[lane + 64] : 0u;
+            /* every candidate key lies in [L0, hmax] */
+            const uint32_t d = L0 ^ hmax;
+            const int top = d ? 31 - __builtin_clz(d) : -1;
+            uint32_t tau = top < 0 ? hmax : (top >= 31 ? 0u : (hmax & ~((2u << top) - 1u)));
+            for (int b = top; b >= 0; --b) {
+                const uint32_t t = tau | (1u << b);
+                if (__popcll(__ballot(k0 >= t)) + __popcll(__ballot(k1 >= t)) >= K) tau = t;
             }
-        } else {
+            const int G = __popcll(__ballot(k0 > tau)) + __popcll(__ballot(k1 > tau));
+            const int E = __popcll(__ballot(k0 == tau)) + __popcll(__ballot(k1 == tau));
+            if (lane == 0) {
+                sh.misc[4] = (int)tau;
+                sh.misc[5] = (E == K - G && w4 < tau) ? 0 : 1;
+            }
+        } else if (wid >= 2) {
             const int c = tid - 2 * 64;
             if (c < M) sh.vv[c] = scaled(sh.mk[c]);
         }
         __syncthreads();
-        const uint32_t tau = (uint32_t)sh.misc[4];
-        if (sh.misc[5] == 0 && w4 < tau) {
+        if (sh.misc[5] == 0) {
             if (wid != 0) return;
-            /* the survivors (G < K) in index order: candidate positions in
-             * index order, two per lane, compacted by ballot */
+            const uint32_t tau = (uint32_t)sh.misc[4];
             const int q0 = lane, q1 = lane + 64;
-            const uint32_t c0 = q0 < M ? sh.byidx[q0] : 0u;
-            const uint32_t c1 = q1 < M ? sh.byidx[q1] : 0u;
-            const bool s0 = q0 < M && (sh.gq[c0] & 0xFFFFu) < (uint32_t)K;
-            const bool s1 = q1 < M && (sh.gq[c1] & 0xFFFFu) < (uint32_t)K;
+            const bool s0 = q0 < M && sh.mk[q0] >= tau;
+            const bool s1 = q1 < M && sh.mk[q1] >= tau;
             const uint64_t m0 = __ballot(s0), m1 = __ballot(s1);
             const uint64_t lt = (1ull << lane) - 1ull;
             if (s0) {
                 const int at = __popcll(m0 & lt);
-                sh.sorted[at] = cand_pack(sh.mk[c0], sh.mi[c0]);
-                sh.sv[at] = sh.vv[c0];
+                sh.sorted[at] = cand_pack(sh.mk[q0], sh.mi[q0]);
+                sh.sv[at] = sh.vv[q0];
             }
             if (s1) {
                 const int at = __popcll(m0) + __popcll(m1 & lt);
-                sh.sorted[at] = cand_pack(sh.mk[c1], sh.mi[c1]);
-                sh.sv[at] = sh.vv[c1];
+                sh.sorted[at] = cand_pack(sh.mk[q1], sh.mi[q1]);
+                sh.sv[at] = sh.vv[q1];
             }
             __builtin_amdgcn_wave_barrier();
             nsurv = K;
