@@ -545,8 +545,11 @@ def main():
         f"{pct(g_gpu, 50):.2f} us GPU events, p99 {pct(g_gpu, 99):.2f} us, host sees it after "
         f"{pct(g_host, 50):.2f} us (p50), {pct(g_call, 50):.2f} us inside the call, "
         f"mismatches {bad_graph}")
-    b2b_us, b2b_ids = graph_back_to_back(H, stream, row0, n_graph)
-    bad_b2b = int(np.sum(b2b_ids != ids[:n_graph]))
+    # at least five graphs of 100 rows, whatever --steps is; every id against
+    # the oracle
+    n_b2b = max(n_graph, 500)
+    b2b_us, b2b_ids = graph_back_to_back(H, stream, row0, n_b2b)
+    bad_b2b = check_decode_ids(row0, b2b_ids, threads, 0)[0]
     bad_graph += bad_b2b
     log(f"decode stream (hipGraphs of 100 rows back to back): per-row p50 {pct(b2b_us, 50):.2f} "
         f"us, p99 {pct(b2b_us, 99):.2f} us over {len(b2b_us)} graphs, mismatches {bad_b2b}")
@@ -691,7 +694,7 @@ def main():
                            "hip_env": {"DEBUG_HIP_GRAPH_PACKET_CAPTURE":
                                        os.environ.get("DEBUG_HIP_GRAPH_PACKET_CAPTURE")},
                            "stream": "hipStreamNonBlocking, default priority"},
-        "graph_back_to_back": {"rows": n_graph, "rows_per_graph": 100,
+        "graph_back_to_back": {"rows": n_b2b, "rows_per_graph": 100,
                                "per_row_p50_us": pct(b2b_us, 50),
                                "per_row_p99_us": pct(b2b_us, 99)},
         "id_mismatches": bad + bad_async + bad_graph,
