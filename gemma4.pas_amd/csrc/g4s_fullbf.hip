@@ -994,9 +994,21 @@ __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_
     const uint4* src = reinterpret_cast<const uint4*>(gst);
     uint4* dst = reinterpret_cast<uint4*>(L.st);
     const int nvec = ns * (int)(sizeof(BfStage) / 16);
-    /* global and LDS never alias: the unrolled loads issue ahead of the stores */
-#pragma unroll 11
-    for (int i = tid; i < nvec; i += kFullBlock) dst[i] = src[i];
+    /* every staged chunk's 16-byte pieces loaded in batches of eight, each
+     * batch's loads issued before its stores (a plain copy loop waits for
+     * each load before its store) */
+    constexpr int kCopy = (kBfStage * (int)(sizeof(BfStage) / 16) + kFullBlock - 1) / kFullBlock;
+    static_assert(kCopy <= 24, "three batches of eight");
+    for (int r0 = 0; r0 < kCopy && tid + r0 * kFullBlock < nvec; r0 += 8) {
+        uint4 c0, c1, c2, c3, c4, c5, c6, c7;
+        const int i0 = tid + r0 * kFullBlock;
+#define G4S_LD(k) if (i0 + (k) * kFullBlock < nvec) c##k = src[i0 + (k) * kFullBlock];
+#define G4S_ST(k) if (i0 + (k) * kFullBlock < nvec) dst[i0 + (k) * kFullBlock] = c##k;
+        G4S_LD(0) G4S_LD(1) G4S_LD(2) G4S_LD(3) G4S_LD(4) G4S_LD(5) G4S_LD(6) G4S_LD(7)
+        G4S_ST(0) G4S_ST(1) G4S_ST(2) G4S_ST(3) G4S_ST(4) G4S_ST(5) G4S_ST(6) G4S_ST(7)
+#undef G4S_LD
+#undef G4S_ST
+    }
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
         const int c = tid + q * kFullBlock;
@@ -1241,7 +1253,7 @@ __device__ int64_t bf_walk(const char* rowp, int c0, int nch, State& st, float t
  * (Tensors.pas:668), the argmax, and the draw's predictions (the last chunk
  * it needs, the predicted binade of its running sum entering every chunk,
  * the chunks to stage). */
-__global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
+__global__ __launch_bounds__(kFullBlock) __attribute__((amdgpu_waves_per_eu(1, 2))) void fb_lsum_chain_kernel(FullArgs a)
 {
     extern __shared__ __align__(16) char dsm[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1356,7 +1368,7 @@ __global__ __launch_bounds__(kFullBlock) void fb_lsum_chain_kernel(FullArgs a)
 
 /* One workgroup per row: the first index whose left-to-right binary32
  * running sum of p reaches thr (Model.pas:2727-2735), else the argmax. */
-__global__ __launch_bounds__(kFullBlock) void fb_cdf_chain_kernel(FullArgs a)
+__global__ __launch_bounds__(kFullBlock) __attribute__((amdgpu_waves_per_eu(1, 2))) void fb_cdf_chain_kernel(FullArgs a)
 {
     extern __shared__ __align__(16) char dsm[];
     const int tid = threadIdx.x, lane = tid & 63;
