@@ -246,15 +246,17 @@ __global__ __launch_bounds__(kFullBlock) void fb_max_kernel(FullArgs a)
     if (row_class(a, ri.p.top_k) != kRowFull) return;
     const int n = a.nch - cw < a.cpw ? a.nch - cw : a.cpw;
     const char* rowp = row_ptr<1>(a, row);
+    /* every load issued unconditionally (a run shorter than cpw reads its
+     * first chunk again in the unused slots), so that each chunk's terms are
+     * waited for on their own */
     uint4 w[kBfMaxCpw][2];
 #pragma unroll
     for (int q = 0; q < kBfMaxCpw; ++q) {
-        if (q < n) {
-            const uint4* src = reinterpret_cast<const uint4*>(
-                rowp + ((int64_t)(cw + q) * kFullChunk + (int64_t)lane * kFullPer) * 2);
-            w[q][0] = src[0];
-            w[q][1] = src[1];
-        }
+        const int cq = q < n ? cw + q : cw;
+        const uint4* src = reinterpret_cast<const uint4*>(
+            rowp + ((int64_t)cq * kFullChunk + (int64_t)lane * kFullPer) * 2);
+        w[q][0] = src[0];
+        w[q][1] = src[1];
     }
     /* the run's largest and smallest x (the key of the float maximum is the
      * largest key: the order-preserving map identifies -0 and +0) */
@@ -891,17 +893,25 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
         w[0] = src[0];
         w[1] = src[1];
     };
+    /* The loads are issued unconditionally (past the run's last chunk a slot
+     * reads that chunk again), and the next slot's terms are waited for
+     * before this slot is loaded again: the waits then never include the
+     * load just issued, which stays in flight while the next chunk is
+     * processed. */
+    const auto ready = [](const uint4 (&v)[2]) {
+        asm volatile("" ::"v"(v[0].x), "v"(v[0].y), "v"(v[0].z), "v"(v[0].w), "v"(v[1].x),
+                     "v"(v[1].y), "v"(v[1].z), "v"(v[1].w));
+    };
     uint4 w[kRing][2];
 #pragma unroll
-    for (int r = 0; r < kRing; ++r)
-        if (r < n) load(w[r], cw + r);
+    for (int r = 0; r < kRing; ++r) load(w[r], cw + (r < n ? r : n - 1));
     for (int q = 0; q < n; q += kRing) {
 #pragma unroll
         for (int r = 0; r < kRing; ++r) {
-            if (q + r < n) {
-                maps_chunk<P, ALL>(R, w[r], q + r);
-                if (q + r + kRing < n) load(w[r], cw + q + r + kRing);
-            }
+            if (q + r < n) maps_chunk<P, ALL>(R, w[r], q + r);
+            ready(w[(r + 1) % kRing]);
+            const int nx = q + r + kRing;
+            load(w[r], cw + (nx < n ? nx : n - 1));
         }
     }
 }
