@@ -146,16 +146,16 @@ G4S_HD float round_dd_f32(double hi, double lo)
  * binary64 ulps of y (normal binary32 range) or eps_rel*y (subnormal range)? */
 G4S_HD bool rounding_safe(double y, int tol_ulps, double eps_rel)
 {
+    /* both tests evaluated and one selected (no branch: callers evaluate
+     * several of these side by side) */
     double a = fabs_d(y);
-    if (a >= 0x1p-126) {
-        int32_t low = (int32_t)(d2u(a) & 0x1FFFFFFFu);
-        int32_t dist = low - 0x10000000;
-        if (dist < 0) dist = -dist;
-        return dist > tol_ulps;
-    }
-    double z = a * 0x1p149; /* exact: units of the binary32 subnormal grid */
+    int32_t low = (int32_t)(d2u(a) & 0x1FFFFFFFu);
+    int32_t dist = low - 0x10000000;
+    dist = dist < 0 ? -dist : dist;
+    double z = a * 0x1p149; /* exact below 2^-126: units of the binary32 subnormal grid */
     double frac = z - __builtin_floor(z);
-    return fabs_d(frac - 0.5) > z * eps_rel + 0x1p-60;
+    const bool sub = fabs_d(frac - 0.5) > z * eps_rel + 0x1p-60;
+    return a >= 0x1p-126 ? dist > tol_ulps : sub;
 }
 
 /* -------------------------------------------------------------- constants */
@@ -210,10 +210,9 @@ G4S_HD dd inv_fact(int n)
 
 /* ------------------------------------------------------------------- exp */
 
-/* e^x in binary64 for x in [-750, 710]; relative error < 2^-51.5 when the
- * result is a normal binary64 (x > -708).  r = x - k ln2, |r| <= 0.347,
- * degree-13 Taylor polynomial (truncation < 2^-57). */
-G4S_HD double exp_fast_d(double x)
+/* e^x = 2^k * exp_fast_poly(x): r = x - k ln2, |r| <= 0.347, degree-13
+ * Taylor polynomial (truncation < 2^-57). */
+G4S_HD double exp_fast_poly(double x, int* kout)
 {
     double k = __builtin_rint(x * G4S_LOG2E);
     double r = fma_d(-k, G4S_LN2_HI32, x); /* exact */
@@ -231,8 +230,15 @@ G4S_HD double exp_fast_d(double x)
     q = fma_d(q, r, 0x1.5555555555555p-3);       /* 1/3!  */
     q = fma_d(q, r, 0.5);
     q = fma_d(q, r, 1.0);
-    double y = fma_d(q, r, 1.0);
-    int ki = (int)k;
+    *kout = (int)k;
+    return fma_d(q, r, 1.0);
+}
+/* e^x in binary64 for x in [-750, 710]; relative error < 2^-51.5 when the
+ * result is a normal binary64 (x > -708). */
+G4S_HD double exp_fast_d(double x)
+{
+    int ki;
+    const double y = exp_fast_poly(x, &ki);
     if (ki < -1000) return y * pow2i(-1000) * pow2i(ki + 1000);
     if (ki > 1000) return y * pow2i(1000) * pow2i(ki - 1000);
     return y * pow2i(ki);
@@ -289,6 +295,27 @@ G4S_HD float exp_diff_cr32(float a, float b)
 {
     dd d = two_sum((double)a, -(double)b);
     return exp_cr32(d.hi, d.lo);
+}
+
+/* exp_cr32 without its double-double route and without branches, so that
+ * several evaluations interleave: *r = exp_cr32(xh, xl) whenever it returns
+ * true (the same binary64 evaluation and the same rounding test, the special
+ * cases selected); false (rarely) when that route is needed. */
+G4S_HD bool exp_cr32_try(double xh, double xl, float* r)
+{
+    const bool nan = isnan_d(xh), over = xh > 89.0, under = xh < -104.0;
+    const bool special = nan || over || under;
+    int ki;
+    /* |x| <= 104: k within +-151, so the scale needs no split */
+    double y = exp_fast_poly(special ? 0.0 : xh, &ki) * pow2i(ki);
+    y = fma_d(y, xl, y);
+    *r = nan ? (float)xh : (over ? __builtin_inff() : (under ? 0.0f : (float)y));
+    return special || rounding_safe(y, 8, 0x1p-50);
+}
+G4S_HD bool exp_diff_cr32_try(float a, float b, float* r)
+{
+    dd d = two_sum((double)a, -(double)b);
+    return exp_cr32_try(d.hi, d.lo, r);
 }
 
 /* ------------------------------------------------------------------ tanh */

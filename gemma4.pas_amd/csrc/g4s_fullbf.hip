@@ -369,11 +369,32 @@ static_assert(kRowEnt * kRowWG * kFullBlock == kBfTab, "whole workgroups of tabl
 
 /* e of one bf16 code: RN32(exp(y - m)), y from the handle's table scaled by
  * 1/T when the row scales (the same value e_direct computes). */
+__device__ __forceinline__ float bf_e_y(float y0, int scale, float inv_t, float m)
+{
+    return exp_diff_cr32(scale ? y0 * inv_t : y0, m); /* Tensors.pas:660 */
+}
 __device__ __forceinline__ float bf_e(const float* ytab, uint32_t code, int scale, float inv_t,
                                      float m)
 {
-    const float y0 = ytab[code];
-    return exp_diff_cr32(scale ? y0 * inv_t : y0, m); /* Tensors.pas:660 */
+    return bf_e_y(ytab[code], scale, inv_t, m);
+}
+
+/* bf_e_y of N values side by side: the branch-free binary64 route for all
+ * of them (their evaluations interleave), then the exact route for the few
+ * it leaves. */
+template <int N>
+__device__ __forceinline__ void bf_e_many(const float (&y0)[N], int scale, float inv_t, float m,
+                                          float (&ev)[N])
+{
+    uint32_t miss = 0u;
+#pragma unroll
+    for (int q = 0; q < N; ++q)
+        if (!exp_diff_cr32_try(scale ? y0[q] * inv_t : y0[q], m, &ev[q])) miss |= 1u << q;
+    if (miss != 0u) {
+#pragma unroll
+        for (int q = 0; q < N; ++q)
+            if ((miss >> q) & 1u) ev[q] = bf_e_y(y0[q], scale, inv_t, m);
+    }
 }
 
 /* Workgroups 1 .. kRowWG of a row: table entries ((g-1)*kRowEnt + q)*256 +
@@ -403,15 +424,17 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
     if (g > 0 && g <= kRowWG) {
         uint64_t tb = 0ull;
         uint32_t k1 = 0xFFFFFFFFu;
-        float ev[kRowEnt];
+        /* every entry's y gathered before the exps, which run side by side */
+        float ev[kRowEnt], y0[kRowEnt];
         uint32_t code[kRowEnt];
 #pragma unroll
         for (int q = 0; q < kRowEnt; ++q) {
             const int i = ((g - 1) * kRowEnt + q) * kFullBlock + tid;
             code[q] = ((uint32_t)(i >> 12) << 15) |
                       ((uint32_t)(win + ((i >> 7) & (kBfWin - 1))) << 7) | (uint32_t)(i & 127);
-            ev[q] = bf_e(ytab, code[q], scale, inv_t, m);
+            y0[q] = ytab[code[q]];
         }
+        bf_e_many(y0, scale, inv_t, m, ev);
 #pragma unroll
         for (int q = 0; q < kRowEnt; ++q) {
             const int i = ((g - 1) * kRowEnt + q) * kFullBlock + tid;
@@ -452,21 +475,27 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
         const double v = (double)c.sapx * exp_fast_d(z);
         return (v >= 0.0 && v < 1e300) ? v : 0.0;
     };
+    constexpr int kCpt = (kBfMaxChunks + kFullBlock - 1) / kFullBlock;
     const int cpt = (nch + kFullBlock - 1) / kFullBlock;
+    /* each estimate evaluated once and kept for the three passes */
+    double es[kCpt];
     double tsum = 0.0;
-    for (int q = 0; q < cpt; ++q) {
+#pragma unroll
+    for (int q = 0; q < kCpt; ++q) {
         const int cb = tid * cpt + q;
-        if (cb < nch) tsum += est(rc[cb]);
+        es[q] = (q < cpt && cb < nch) ? est(rc[cb]) : 0.0;
+        tsum += es[q];
     }
     double total;
     const double pre0 = block_excl_scan_d(tsum, sh, total);
     int cnt = 0;
     {
         double p = pre0;
-        for (int q = 0; q < cpt; ++q) {
+#pragma unroll
+        for (int q = 0; q < kCpt; ++q) {
             const int cb = tid * cpt + q;
-            if (cb < nch) {
-                const double e = est(rc[cb]);
+            if (q < cpt && cb < nch) {
+                const double e = es[q];
                 if (cb > 0 && binade_of(p * (1.0 - kMargin)) != binade_of((p + e) * (1.0 + kMargin)))
                     ++cnt;
                 p += e;
@@ -479,10 +508,11 @@ __global__ __launch_bounds__(kFullBlock) void fb_row_kernel(FullArgs a)
     BfStage* sg = a.ws.stage + (int64_t)row * kBfStage;
     {
         double p = pre0;
-        for (int q = 0; q < cpt; ++q) {
+#pragma unroll
+        for (int q = 0; q < kCpt; ++q) {
             const int cb = tid * cpt + q;
-            if (cb < nch) {
-                const double e = est(rc[cb]);
+            if (q < cpt && cb < nch) {
+                const double e = es[q];
                 int32_t beta = -1;
                 if (cb > 0) {
                     const int lo = binade_of(p * (1.0 - kMargin));
@@ -546,11 +576,22 @@ __device__ void bf_head(const FullArgs& a, int row, float* hbuf)
     const uint4* src = reinterpret_cast<const uint4*>(row_ptr<1>(a, row) + (int64_t)lane * kFullPer * 2);
     const uint4 w0 = src[0], w1 = src[1];
     const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-    float t[kFullPer];
+    float t[kFullPer], y0[kFullPer];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        t[2 * i] = bf_e(a.ws.ytab, ww[i] & 0xFFFFu, r.scale, r.inv_t, r.m);
-        t[2 * i + 1] = bf_e(a.ws.ytab, ww[i] >> 16, r.scale, r.inv_t, r.m);
+        y0[2 * i] = a.ws.ytab[ww[i] & 0xFFFFu];
+        y0[2 * i + 1] = a.ws.ytab[ww[i] >> 16];
+    }
+    /* two halves of eight: sixteen side by side would not fit this kernel's
+     * registers */
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float yh[kFullPer / 2], th[kFullPer / 2];
+#pragma unroll
+        for (int j = 0; j < kFullPer / 2; ++j) yh[j] = y0[h * (kFullPer / 2) + j];
+        bf_e_many(yh, r.scale, r.inv_t, r.m, th);
+#pragma unroll
+        for (int j = 0; j < kFullPer / 2; ++j) t[h * (kFullPer / 2) + j] = th[j];
     }
     float4* hd = reinterpret_cast<float4*>(a.ws.head + (int64_t)row * kFullChunk + lane * kFullPer);
     float4* hb = reinterpret_cast<float4*>(hbuf + lane * kFullPer);

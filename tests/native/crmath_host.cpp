@@ -11,6 +11,17 @@ using namespace g4s::cr;
 extern "C" {
 float t_exp_cr32(double xh, double xl) { return exp_cr32(xh, xl); }
 float t_exp_diff_cr32(float a, float b) { return exp_diff_cr32(a, b); }
+int t_exp_diff_cr32_try(float a, float b, float* r) { return exp_diff_cr32_try(a, b, r) ? 1 : 0; }
+int t_exp_cr32_try(double xh, double xl, float* r) { return exp_cr32_try(xh, xl, r) ? 1 : 0; }
+/* n pairs: ok[i] = 1 when the try path settled pair i, out_try[i] its value,
+ * out_ref[i] = exp_diff_cr32(a[i], b[i]) */
+void t_exp_diff_try_bulk(const float* a, const float* b, float* out_try, float* out_ref, int* ok, long n)
+{
+    for (long i = 0; i < n; ++i) {
+        ok[i] = exp_diff_cr32_try(a[i], b[i], &out_try[i]) ? 1 : 0;
+        out_ref[i] = exp_diff_cr32(a[i], b[i]);
+    }
+}
 double t_exp_fast_d(double x) { return exp_fast_d(x); }
 void t_exp_dd(double xh, double xl, double* out) { dd r = exp_dd(xh, xl); out[0] = r.hi; out[1] = r.lo; }
 double t_tanh_fast_d(double w) { return tanh_fast_d(w); }

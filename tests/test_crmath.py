@@ -122,6 +122,43 @@ def test_exp_edges(cr):
         assert cr.t_exp_cr32(x, 0.0) == rn32(mp.exp(mp.mpf(x)))
 
 
+def test_exp_try_path_agrees(cr):
+    """exp_cr32_try (the branch-free binary64 route the row tables use) gives
+    exp_cr32's value whenever it settles an input, and refuses the inputs
+    whose result lies too close to a binary32 midpoint (those take the
+    double-double route): random differences over the whole range, results
+    down to the subnormals, the special cases and constructed hard cases."""
+    rng = np.random.default_rng(11)
+    n = 200000
+    a = np.concatenate([rng.normal(0, 10, n // 2), rng.uniform(-120, 95, n // 2)]).astype(F32)
+    b = np.concatenate([rng.normal(0, 10, n // 2), np.zeros(n // 2)]).astype(F32)
+    out_t = np.zeros(n, F32)
+    out_r = np.zeros(n, F32)
+    ok = np.zeros(n, np.int32)
+    cr.t_exp_diff_try_bulk.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_long]
+    cr.t_exp_diff_try_bulk(a.ctypes.data, b.ctypes.data, out_t.ctypes.data, out_r.ctypes.data,
+                           ok.ctypes.data, n)
+    settled = ok.astype(bool)
+    assert settled.mean() > 0.999
+    assert np.array_equal(out_t[settled].view(np.uint32), out_r[settled].view(np.uint32))
+    assert (out_r[settled] == 0).any() and (out_r[settled] < np.finfo(F32).tiny).any()
+    cr.t_exp_cr32_try.argtypes = [ctypes.c_double, ctypes.c_double, ctypes.POINTER(ctypes.c_float)]
+    r = ctypes.c_float()
+    for x, want in ((float("nan"), None), (100.0, np.inf), (-200.0, 0.0), (0.0, 1.0)):
+        assert cr.t_exp_cr32_try(x, 0.0, ctypes.byref(r)) == 1
+        assert (np.isnan(r.value) if want is None else r.value == want)
+    refused = 0
+    for _ in range(300):
+        f = F32(rng.uniform(0.01, 1.0))
+        g = np.nextafter(f, F32(np.inf))
+        x = float(mp.log((mp.mpf(float(f)) + mp.mpf(float(g))) / 2))
+        if cr.t_exp_cr32_try(x, 0.0, ctypes.byref(r)):
+            assert r.value == cr.t_exp_cr32(x, 0.0)
+        else:
+            refused += 1
+    assert refused > 30
+
+
 def test_softcap_random_and_hard(cr):
     rng = np.random.default_rng(5)
     inv = F32(1.0) / F32(30.0)
