@@ -679,8 +679,8 @@ __host__ __device__ __forceinline__ int bf_maps_cpw(int cpw) { return 3 * cpw; }
  * map {-1, -1}, or an invalid binade for a staged chunk. */
 constexpr int32_t kDeferred = -1;
 
-/* The per-chunk work of fb_maps_kernel (chunk cw + q of the wave, its two
- * 16-byte loads in w); the row's values arrive in MapsRow. */
+/* The per-chunk work of fb_maps_kernel (chunk cw + q * cstep of the wave,
+ * its two 16-byte loads in w); the row's values arrive in MapsRow. */
 struct MapsRow {
     const float* tab;
     BfStage* stg;
@@ -693,7 +693,7 @@ struct MapsRow {
     Ctx ctx;
     uint32_t base, base2;
     int32_t betas;
-    int cw, tbase;
+    int cw, cstep, tbase; /* chunk q of the wave: cw + q * cstep */
     float tmax, kninf, kpinf, ktiny;
     bool maps;
 };
@@ -712,10 +712,10 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
     const Ctx& ctx = R.ctx;
     const uint32_t base = R.base, base2 = R.base2;
     const int32_t betas = R.betas;
-    const int cw = R.cw, tbase = R.tbase;
+    const int tbase = R.tbase;
     const float tmax = R.tmax, kninf = R.kninf, kpinf = R.kpinf, ktiny = R.ktiny;
     const bool maps = R.maps;
-    const int cb = cw + q;
+    const int cb = R.cw + q * R.cstep;
     if (!ALL && cb == 0) return; /* chunk 0: outputs only */
     const int64_t e0 = (int64_t)cb * kFullChunk + (int64_t)lane * kFullPer;
     float t[kFullPer];
@@ -884,21 +884,31 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
         else if (r.nodraw == 0)
             bf_draw0(a, row, r, hbuf);
     }
-    const int cw = (blockIdx.x * kBfWaves + wid) * cpw;
+    /* In the LSum pass a workgroup before the row's last one deals its chunks
+     * to its waves in turn (chunk q of wave w: base + w + q * kBfWaves): the
+     * chunks of a binade that takes the per-term tie vote, and the staged
+     * chunks, which cluster where the sum is small, spread over all eight
+     * waves.  The last workgroup keeps runs of consecutive chunks, so that
+     * its last wave holds few and has time for chunk 0.  (The draw's pass,
+     * which stops near the middle of most rows, ran slower dealt.) */
+    const int gch = kBfWaves * cpw;
+    const bool deal = !P && (int)blockIdx.x < clast / gch; /* every chunk of it is <= clast */
+    const int cw = deal ? (int)blockIdx.x * gch + wid : (blockIdx.x * kBfWaves + wid) * cpw;
+    const int cstep = deal ? kBfWaves : 1;
     if (cw > clast) return;
-    const int n = clast + 1 - cw < cpw ? clast + 1 - cw : cpw;
+    const int n = deal ? cpw : (clast + 1 - cw < cpw ? clast + 1 - cw : cpw);
     const char* rowp = row_ptr<1>(a, row);
     const int64_t rbase = (int64_t)row * a.ws.cstride;
     const uint32_t base = (uint32_t)r.win_lo << 7;
     const uint32_t base2 = base | (base << 16);
     const int tbase = P ? kTieBaseP : kTieBaseE;
-    const int32_t betas = lane < n ? (P ? a.ws.beta_c : a.ws.beta_l)[rbase + cw + lane] : 0;
+    const int32_t betas = lane < n ? (P ? a.ws.beta_c : a.ws.beta_l)[rbase + cw + lane * cstep] : 0;
     PMap* gmap = (P ? a.ws.cmap : a.ws.lmap) + rbase;
-    /* chunks whose run can hold an e == 1 (bit q: chunk cw + q) */
+    /* chunks whose run can hold an e == 1 (bit q: chunk cw + q * cstep) */
     uint64_t argm = 0ull;
     if (!P) {
         const uint32_t key1 = a.ws.fbrow[row].key1;
-        argm = __ballot(lane < n && a.ws.chunks[rbase + cw + lane].maxkey >= key1);
+        argm = __ballot(lane < n && a.ws.chunks[rbase + cw + lane * cstep].maxkey >= key1);
     }
     const bool maps = !P || !r.nodraw;
     const float tmax = P ? r.inv : 1.0f; /* no term exceeds it: e <= 1, p <= fl32(1/LSum) */
@@ -922,6 +932,7 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
     R.base2 = base2;
     R.betas = betas;
     R.cw = cw;
+    R.cstep = cstep;
     R.tbase = tbase;
     R.tmax = tmax;
     R.kninf = kninf;
@@ -945,14 +956,14 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
     };
     uint4 w[kRing][2];
 #pragma unroll
-    for (int r = 0; r < kRing; ++r) load(w[r], cw + (r < n ? r : n - 1));
+    for (int r = 0; r < kRing; ++r) load(w[r], cw + (r < n ? r : n - 1) * cstep);
     for (int q = 0; q < n; q += kRing) {
 #pragma unroll
         for (int r = 0; r < kRing; ++r) {
             if (q + r < n) maps_chunk<P, ALL>(R, w[r], q + r);
             ready(w[(r + 1) % kRing]);
             const int nx = q + r + kRing;
-            load(w[r], cw + (nx < n ? nx : n - 1));
+            load(w[r], cw + (nx < n ? nx : n - 1) * cstep);
         }
     }
 }
