@@ -825,8 +825,8 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
  * argmax in the chunks whose run can hold an e == 1.  With
  * ALL (P and every probability requested): the probabilities, including
  * those of codes outside the table; otherwise a chunk holding such a code
- * is left to the chain.  Every wave streams a run of bf_maps_cpw() chunks,
- * kRing of them in flight. */
+ * is left to the chain.  Every wave streams the chunks dealt to it (about
+ * bf_maps_cpw() of them), kRing of them in flight. */
 template <bool P, bool ALL>
 __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))) void fb_maps_kernel(FullArgs a)
 {
@@ -875,28 +875,25 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
     } else {
         tm = a.ws.tmask[(int64_t)row * 2];
     }
-    /* the last wave of the row's last workgroup (one the last chunks leave
-     * idle, or the one with fewest) also evaluates chunk 0: for LSum, and
-     * for the draw against thr */
-    if (blockIdx.x == clast / (kBfWaves * cpw) && wid == kBfWaves - 1) {
+    /* The last wave of the row's last workgroup evaluates chunk 0 (for LSum,
+     * or the draw against thr) and takes no other chunk.  Chunks 0 .. clast
+     * are dealt in turn to the row's other waves (W of them, over workgroups
+     * 0 .. glast): wave g takes g, g + W, g + 2W, ...  The chunks of a binade
+     * that takes the per-term tie vote, and the staged chunks, which cluster
+     * where the sum is small, so spread over every wave of the row. */
+    const int glast = clast / (kBfWaves * cpw);
+    if ((int)blockIdx.x == glast && wid == kBfWaves - 1) {
         if (!P)
             bf_head(a, row, hbuf);
         else if (r.nodraw == 0)
             bf_draw0(a, row, r, hbuf);
+        return;
     }
-    /* In the LSum pass a workgroup before the row's last one deals its chunks
-     * to its waves in turn (chunk q of wave w: base + w + q * kBfWaves): the
-     * chunks of a binade that takes the per-term tie vote, and the staged
-     * chunks, which cluster where the sum is small, spread over all eight
-     * waves.  The last workgroup keeps runs of consecutive chunks, so that
-     * its last wave holds few and has time for chunk 0.  (The draw's pass,
-     * which stops near the middle of most rows, ran slower dealt.) */
-    const int gch = kBfWaves * cpw;
-    const bool deal = !P && (int)blockIdx.x < clast / gch; /* every chunk of it is <= clast */
-    const int cw = deal ? (int)blockIdx.x * gch + wid : (blockIdx.x * kBfWaves + wid) * cpw;
-    const int cstep = deal ? kBfWaves : 1;
+    const int W = (glast + 1) * kBfWaves - 1;
+    const int cw = (int)blockIdx.x * kBfWaves + wid;
+    const int cstep = W;
     if (cw > clast) return;
-    const int n = deal ? cpw : (clast + 1 - cw < cpw ? clast + 1 - cw : cpw);
+    const int n = (clast - cw) / W + 1; /* <= cpw * 8 / 7 + 1 */
     const char* rowp = row_ptr<1>(a, row);
     const int64_t rbase = (int64_t)row * a.ws.cstride;
     const uint32_t base = (uint32_t)r.win_lo << 7;
