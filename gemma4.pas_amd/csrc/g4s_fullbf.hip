@@ -170,13 +170,37 @@ __device__ __forceinline__ PMap thread_map_fma(const float (&t)[kFullPer], int32
     return f;
 }
 
-/* The lane map of a chunk's terms in binade e: without a possible tie the
- * constant map (the fma form where every term is below 2^(e-128), i.e.
- * tmax * 2^(150-e) < 2^22), else the exact per-term lane map. */
+/* thread_map_fma with the tie vote: r = fl(q + 1.5 * 2^23) holds rint(q)
+ * (every term below 2^22 units), and fma(t, S, 1.5 * 2^23 - r) is
+ * q - rint(q) exactly; a term is a half-unit tie when that is +-1/2.  A tie
+ * anywhere in the wave takes ss::lane_map_fma, the lane maps in the same
+ * form (closed form for a lane with one tie). */
+__device__ __forceinline__ PMap thread_map_fma_tie(const float (&t)[kFullPer], int32_t e)
+{
+    const float S = __builtin_ldexpf(1.0f, 150 - e);
+    uint32_t acc = 0u;
+    float dmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kFullPer; ++j) {
+        const float r = __builtin_fmaf(t[j], S, kMagic);
+        acc += __float_as_uint(r);
+        dmax = __builtin_fmaxf(dmax, __builtin_fabsf(__builtin_fmaf(t[j], S, kMagic - r)));
+    }
+    if (__ballot(dmax == 0.5f) != 0) return ss::lane_map_fma(t, kFullPer, e);
+    PMap f;
+    f.d0 = f.d1 = (int32_t)(acc - (uint32_t)kFullPer * kMagicBits);
+    return f;
+}
+
+/* The lane map of a chunk's terms in binade e: the constant map when no
+ * term can be a half-unit tie (the fma form where every term is below
+ * 2^(e-128), i.e. tmax * 2^(150-e) < 2^22), else with the tie vote, and the
+ * exact per-term lane map where a tie is found. */
 __device__ __forceinline__ PMap bf_map(const float (&t)[kFullPer], int32_t e, bool tie, float tmax)
 {
-    if (tie) return thread_map(t, kFullPer, e);
-    if (__builtin_ldexpf(tmax, 150 - e) < 4194303.0f) return thread_map_fma(t, e);
+    const bool small = __builtin_ldexpf(tmax, 150 - e) < 4194303.0f;
+    if (tie) return small ? thread_map_fma_tie(t, e) : thread_map(t, kFullPer, e);
+    if (small) return thread_map_fma(t, e);
     return thread_map_nt(t, e);
 }
 

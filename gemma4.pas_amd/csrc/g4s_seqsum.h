@@ -169,6 +169,11 @@ G4S_SS_HD PMap map_sat(PMap f)
  * 2^25, where a term alone leaves the binade, and d0 at 2^26). */
 G4S_SS_HD PMap lane_map(const float* t, int n, int32_t e)
 {
+    /* A tie adds fi + x, x = (P ^ fi) & 1, which leaves the sum even: the
+     * parity P carried from term to term is 0 after a tie and P ^ (c & 1)
+     * after any other term adding c units, so it does not wait on the
+     * units a tie adds (the chain between terms is one xor and one
+     * select). */
     int32_t D = 0, P = 0, delta = 0;
     bool seen = false;
     for (int j = 0; j < n; ++j) {
@@ -178,18 +183,54 @@ G4S_SS_HD PMap lane_map(const float* t, int n, int32_t e)
         const float fr = q - fl;
         const int32_t fi = (int32_t)fl;
         const bool tie = fr == 0.5f;
+        const int32_t c = fi + ((!tie && fr > 0.5f) ? 1 : 0);
         const int32_t x = (P ^ fi) & 1;
-        const int32_t a = fi + (tie ? x : (fr > 0.5f ? 1 : 0));
         delta = (tie && !seen) ? 1 - 2 * x : delta;
         seen = seen || tie;
-        D += a;
+        D += c + (tie ? x : 0);
         D = D > (1 << 26) ? (1 << 26) : D;
-        P = (P ^ a) & 1;
+        P = tie ? 0 : (P ^ (c & 1));
     }
     PMap r;
     r.d0 = D;
     r.d1 = D + delta;
     return r;
+}
+
+/* lane_map for terms q = t * 2^(150-e) all in [0, 2^22), in one fma pass:
+ * r = fl(q + 1.5 * 2^23) holds rint(q) and fma(t, 2^(150-e), 1.5 * 2^23 - r)
+ * is q - rint(q) exactly, +-1/2 at a half-unit tie.  Without a tie the map is
+ * the constant sum of rint(q); with one, that sum less the tie's rint plus
+ * floor(q) + x, x = (units before it + floor(q)) & 1 for the even start and
+ * 1 - x for the odd one (the tie makes the sum even).  Two or more ties in
+ * the lane take lane_map. */
+G4S_SS_HD PMap lane_map_fma(const float* t, int n, int32_t e)
+{
+    const float S = __builtin_ldexpf(1.0f, 150 - e);
+    const float M = 12582912.0f; /* 1.5 * 2^23 */
+    int32_t tot = 0, before = 0, rj = 0, fj = 0, nt = 0;
+    for (int j = 0; j < n; ++j) {
+        const float r = __builtin_fmaf(t[j], S, M);
+        const float d = __builtin_fmaf(t[j], S, M - r);
+        const int32_t ri = (int32_t)(r - M);
+        if (__builtin_fabsf(d) == 0.5f) {
+            before = tot;
+            rj = ri;
+            fj = d > 0.0f ? ri : ri - 1;
+            ++nt;
+        }
+        tot += ri;
+    }
+    PMap f;
+    if (nt > 1) return lane_map(t, n, e);
+    if (nt == 0) {
+        f.d0 = f.d1 = tot;
+        return f;
+    }
+    const int32_t x = (before + fj) & 1;
+    f.d0 = tot - rj + fj + x;
+    f.d1 = f.d0 + 1 - 2 * x;
+    return f;
 }
 
 /* One reference step, S <- RN32(S + a), on a state (exact by definition). */

@@ -222,6 +222,39 @@ int64_t ss_check_lane_map(uint64_t seed, int64_t n)
     return bad;
 }
 
+/* lane_map_fma against lane_map: runs of 1-16 terms below 2^22 units (none,
+ * one or several forced half-unit ties, zeros, terms of few fraction bits);
+ * both maps must be equal. */
+int64_t ss_check_lane_map_fma(uint64_t seed, int64_t n)
+{
+    Rng r{seed};
+    int64_t bad = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t e = 30 + (int32_t)(r.next() % 170);
+        const int len = 1 + (int)(r.next() % 16);
+        float t[16];
+        const int mode = (int)(r.next() % 4);
+        for (int j = 0; j < len; ++j) {
+            double q;
+            const uint64_t z = r.next();
+            const uint64_t tie_rate = mode == 3 ? 3 : 31; /* mode 3: several ties a lane */
+            if ((z & 7) == 0) {
+                q = 0.0;
+            } else if (((z >> 3) & tie_rate) == 1) {
+                q = (double)(r.next() % 4194303) + 0.5;             /* a tie */
+            } else {
+                const int bits = 1 + (int)(r.next() % 12);           /* fraction bits */
+                const double scale = mode == 0 ? 4096.0 : (mode == 1 ? 64.0 : 4194000.0);
+                q = std::floor(r.unif() * scale * (double)(1 << bits)) / (double)(1 << bits);
+            }
+            t[j] = (float)std::ldexp(q, e - 150);
+        }
+        const PMap f = lane_map_fma(t, len, e), g = lane_map(t, len, e);
+        if (f.d0 != g.d0 || f.d1 != g.d1) ++bad;
+    }
+    return bad;
+}
+
 /* Associativity of map composition over random term maps. */
 int64_t ss_check_assoc(uint64_t seed, int64_t n)
 {

@@ -24,6 +24,8 @@ def ss():
     L.ss_check_term_ct_f.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     L.ss_check_lane_map.restype = ctypes.c_int64
     L.ss_check_lane_map.argtypes = [ctypes.c_uint64, ctypes.c_int64]
+    L.ss_check_lane_map_fma.restype = ctypes.c_int64
+    L.ss_check_lane_map_fma.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     L.ss_check_assoc.restype = ctypes.c_int64
     L.ss_check_assoc.argtypes = [ctypes.c_uint64, ctypes.c_int64]
     L.ss_check_sequence.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
@@ -48,6 +50,13 @@ def test_lane_map_matches_literal_loop(ss):
     against the literal binary32 loop from even and odd entering sums, and
     against the composition of per-term maps."""
     assert ss.ss_check_lane_map(11, 400_000) == 0
+
+
+def test_lane_map_fma_equals_lane_map(ss):
+    """The one-pass form the bf16 map passes use for waves holding a tie
+    (terms below 2^22 units; one tie in a lane closed-form, more take
+    lane_map) gives lane_map's map exactly, from both parities."""
+    assert ss.ss_check_lane_map_fma(12, 400_000) == 0
 
 
 def test_composition_associative(ss):
