@@ -125,7 +125,9 @@ struct BfStage {
     int32_t b;
     int32_t chunk;
     int32_t pad[2];
-    int32_t xs[128]; /* inclusive lane scans of the constant lo [0..63] and hi [64..127] maps */
+    /* inclusive lane scans of the lo maps from an even [0..63] and an odd
+     * [64..127] entering significand, and of the hi maps [128..255] */
+    int32_t xs[256];
     float t[kFullChunk];
 };
 static_assert(sizeof(BfStage) % 16 == 0, "BfStage copies in 16-byte units");

@@ -809,8 +809,9 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
     if (beta <= -2) {
         /* a staged chunk, for the chain: its terms (pad[0]: a code outside the
          * table) and its lane maps in the predicted binade b and in b + 1
-         * (ties per the row's mask), with their inclusive lane scans when both
-         * are constant (pad[1] = 1) */
+         * (ties per the row's mask), with their inclusive lane scans from an
+         * even and from an odd entering significand (pad[1]: bit h set when
+         * the maps in b + h are constant, bit 2 when the scans are there) */
         BfStage* sg = stg + (-2 - beta);
         if (lane == 0) sg->pad[0] = outside ? 1 : 0;
         float4* dst = reinterpret_cast<float4*>(sg->t + lane * kFullPer);
@@ -819,20 +820,24 @@ __device__ __forceinline__ void maps_chunk(const MapsRow& R, const uint4 (&w)[2]
             dst[k] = make_float4(t[4 * k], t[4 * k + 1], t[4 * k + 2], t[4 * k + 3]);
         const int32_t b = __builtin_amdgcn_readfirstlane(sg->b);
         if (b >= 1) {
-            bool cst = true;
-            int32_t d[2];
+            int32_t flags = 4;
 #pragma nounroll
             for (int h = 0; h < 2; ++h) {
                 const PMap m = bf_map(t, b + h, outside || tie_possible(tm, tbase, b + h), tmax);
                 (h ? sg->hi : sg->lo)[lane] = m;
-                cst = cst && __ballot(m.d0 != m.d1) == 0;
-                d[h] = m.d0 > ss::kTop ? ss::kTop : m.d0;
+                int32_t x0, x1;
+                if (__ballot(m.d0 != m.d1) == 0) {
+                    x0 = x1 = wave_inclusive_scan(m.d0 > ss::kTop ? ss::kTop : m.d0);
+                    flags |= 1 << h;
+                } else {
+                    const PMap incl = wave_scan_maps(m);
+                    x0 = incl.d0;
+                    x1 = incl.d1;
+                }
+                sg->xs[128 * h + lane] = x0;
+                sg->xs[128 * h + 64 + lane] = x1;
             }
-            if (cst) {
-                sg->xs[lane] = wave_inclusive_scan(d[0]);
-                sg->xs[64 + lane] = wave_inclusive_scan(d[1]);
-            }
-            if (lane == 0) sg->pad[1] = cst ? 1 : 0;
+            if (lane == 0) sg->pad[1] = flags;
         }
     } else if (beta >= 1) {
         const PMap cm =
@@ -1081,7 +1086,7 @@ __device__ __forceinline__ void bf_chain_prologue(const PMap* gmap, const int32_
      * batch's loads issued before its stores (a plain copy loop waits for
      * each load before its store) */
     constexpr int kCopy = (kBfStage * (int)(sizeof(BfStage) / 16) + kFullBlock - 1) / kFullBlock;
-    static_assert(kCopy <= 24, "three batches of eight");
+    static_assert(kCopy <= 32, "four batches of eight");
     for (int r0 = 0; r0 < kCopy && tid + r0 * kFullBlock < nvec; r0 += 8) {
         uint4 c0, c1, c2, c3, c4, c5, c6, c7;
         const int i0 = tid + r0 * kFullBlock;
@@ -1160,15 +1165,15 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
     const int sl = beta <= -2 ? -2 - beta : -1;
     const BfStage* sg = sl >= 0 ? L.st + sl : nullptr;
     /* every LDS read of a staged chunk issued together: its binade, its
-     * terms, and the lane scans of its b and b + 1 maps (the exclusive scan is
-     * the inclusive one less the lane's own capped increment) */
-    int32_t b = -1, cst = 0, xl = 0, xh = 0, own = 0;
+     * terms, and the lane scans of its b maps from the parity st enters with
+     * and of its b + 1 maps from either parity */
+    int32_t b = -1, cst = 0, xl = 0, xh0 = 0, xh1 = 0;
     if (sg) {
         b = sg->b;
         cst = sg->pad[1];
-        xl = sg->xs[lane];
-        xh = sg->xs[64 + lane];
-        own = sg->lo[lane].d0;
+        xl = sg->xs[64 * (st.m & 1) + lane];
+        xh0 = sg->xs[128 + lane];
+        xh1 = sg->xs[192 + lane];
         const float4* src = reinterpret_cast<const float4*>(sg->t + lane * kFullPer);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -1180,7 +1185,7 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
         }
     }
     if (sg && b >= 1) {
-        if (st.e == b && cst != 0) {
+        if (st.e == b && (cst & 4) != 0) {
             ++*rounds;
             const int32_t mo = st.m + xl;
             const uint64_t bal = __ballot(mo >= ss::kTop || ss::value_of(State{b, mo}) >= thr);
@@ -1189,7 +1194,8 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
                 return st;
             }
             const int ls = (int)__builtin_ctzll(bal);
-            const int32_t xl0 = xl - (own > ss::kTop ? ss::kTop : own);
+            /* lanes before ls stayed in b: their scan is exact */
+            const int32_t xl0 = ls == 0 ? 0 : __builtin_amdgcn_readlane(xl, ls - 1);
             const int32_t mi = st.m + xl0;
             float sum = ss::value_of(State{b, mi < ss::kTop ? mi : 0});
             int below = 0;
@@ -1207,12 +1213,22 @@ __device__ State bf_chain_chunk(const char* rowp, int c, State st, float thr, co
             }
             pos = ls + 1;
             if (st.e == b + 1) {
-                const int32_t m2 = st.m + (xh - __builtin_amdgcn_readlane(xh, ls));
-                const uint64_t bad =
-                    __ballot(lane >= pos && (m2 >= ss::kTop || ss::value_of(State{b + 1, m2}) >= thr));
-                if (bad == 0) {
-                    st.m = __builtin_amdgcn_readlane(m2, 63);
-                    return st;
+                /* lanes after ls from st: a difference of the b + 1 scans from
+                 * a start whose parity after lane ls is st's (any start when
+                 * the maps are constant) */
+                const int32_t r0 = __builtin_amdgcn_readlane(xh0, ls);
+                const int32_t r1 = __builtin_amdgcn_readlane(xh1, ls);
+                const int32_t pp = st.m & 1;
+                const bool use0 = (cst & 2) != 0 || (r0 < ss::kTop && (r0 & 1) == pp);
+                const bool use1 = !use0 && r1 < ss::kTop && ((1 + r1) & 1) == pp;
+                if (use0 || use1) {
+                    const int32_t m2 = st.m + (use0 ? xh0 - r0 : xh1 - r1);
+                    const uint64_t bad = __ballot(
+                        lane >= pos && (m2 >= ss::kTop || ss::value_of(State{b + 1, m2}) >= thr));
+                    if (bad == 0) {
+                        st.m = __builtin_amdgcn_readlane(m2, 63);
+                        return st;
+                    }
                 }
             }
         } else if (st.e == b) {
