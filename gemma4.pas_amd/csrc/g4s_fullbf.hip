@@ -870,7 +870,14 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
     if (row_class(a, ri.p.top_k) != kRowFull) return;
     const FullRow r = a.ws.rows[row];
     const int clast = P ? r.c_last : nch - 1;
-    if ((int)blockIdx.x * kBfWaves * cpw > clast) return;
+    /* the wave that evaluates chunk 0 is in workgroup glast: the last one
+     * with a chunk of the LSum pass, the last of the grid in the draw's pass
+     * (whose last chunk varies by row); another workgroup that no chunk is
+     * dealt to has nothing to do */
+    const int glast = P ? (int)gridDim.x - 1 : clast / (kBfWaves * cpw);
+    if (P ? (clast < 0 || ((int)blockIdx.x != glast && (int)blockIdx.x * kBfWaves > clast))
+          : (int)blockIdx.x * kBfWaves * cpw > clast)
+        return;
     {
         const float4* src = reinterpret_cast<const float4*>(a.ws.etab8 + (int64_t)row * kBfTab);
         float4 v[kBfTab / 4 / kBfBlock];
@@ -904,13 +911,14 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
     } else {
         tm = a.ws.tmask[(int64_t)row * 2];
     }
-    /* The last wave of the row's last workgroup evaluates chunk 0 (for LSum,
-     * or the draw against thr) and takes no other chunk.  Chunks 0 .. clast
-     * are dealt in turn to the row's other waves (W of them, over workgroups
-     * 0 .. glast): wave g takes g, g + W, g + 2W, ...  The chunks of a binade
-     * that takes the per-term tie vote, and the staged chunks, which cluster
-     * where the sum is small, so spread over every wave of the row. */
-    const int glast = clast / (kBfWaves * cpw);
+    /* The last wave of workgroup glast evaluates chunk 0 (for LSum, or the
+     * draw against thr) and takes no other chunk.  Chunks 0 .. clast are dealt
+     * in turn to the row's other waves (W of them, over workgroups 0 ..
+     * glast): wave g takes g, g + W, g + 2W, ...  The chunks of a binade that
+     * takes the per-term tie vote, and the staged chunks, which cluster where
+     * the sum is small, so spread over every wave of the row, and in the
+     * draw's pass a row that stops early spreads as wide as one that does
+     * not. */
     if ((int)blockIdx.x == glast && wid == kBfWaves - 1) {
         if (!P)
             bf_head(a, row, hbuf);
