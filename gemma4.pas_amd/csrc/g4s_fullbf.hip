@@ -869,7 +869,10 @@ __global__ __launch_bounds__(kBfBlock) __attribute__((amdgpu_waves_per_eu(6, 6))
     const RowIn ri = row_in(a, row);
     if (row_class(a, ri.p.top_k) != kRowFull) return;
     const FullRow r = a.ws.rows[row];
-    const int clast = P ? r.c_last : nch - 1;
+    /* the draw's pass has nothing to do for a row that draws nothing (T <= 0,
+     * or a threshold <= 0: its chain writes the outputs) unless every
+     * probability is written */
+    const int clast = P ? ((!ALL && r.nodraw != 0) ? -1 : r.c_last) : nch - 1;
     /* the wave that evaluates chunk 0 is in workgroup glast: the last one
      * with a chunk of the LSum pass, the last of the grid in the draw's pass
      * (whose last chunk varies by row); another workgroup that no chunk is
