@@ -16,7 +16,8 @@ constexpr int kWaveBounds = 512; /* per-wave bounds kept per row (splits * waves
  * 16-byte-per-thread workgroup chunks (262144 binary32 logits, 524288 bf16).
  * K bounds up to kDecSmallK take an instantiation with less LDS.  (Larger
  * batches take the chunked launch: screening a row into 1024 wave lists
- * costs more instructions per logit than the chunk workgroups' bounds.) */
+ * costs more instructions per logit than the chunk workgroups' bounds: with
+ * this launch a B=64 batch of mixed K took 76.1 us against 37.2 us.) */
 constexpr int kDecMaxBatch = 8;
 constexpr int kDecMaxK = 256;
 constexpr int kDecSmallK = 64;
